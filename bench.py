@@ -1,0 +1,164 @@
+"""Headline benchmark: 8-step DiT denoise at 1024x1024, FP16 storage / FP32
+accumulate, 36 blocks, on one MI355X, plus the MFMA utilisation of the
+GEMM + SDPA kernels and a CPU baseline (the oracle) on the host cores.
+
+One "step" = one Euler step of the denoise loop through the C++ facade:
+time features, input head, 36 blocks (S = 4096 image + 64 text tokens,
+40 valid), output head, Euler update and the finite check. Weights are
+synthetic N(0, 0.02) generated on the device; latent [128,64,64] and text
+[64,3072] are synthetic N(0,1). Inputs are resident in HBM before timing.
+
+Prints one JSON line (rank 0).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "ernie-image-ncnn-vulkan_amd"))
+
+METRIC = "DiT denoise steps/s at 1024×1024 fp16 (36 blk); SDPA+GEMM % MFMA peak"
+PEAK = {"fp16": 2.5e15, "bf16": 2.5e15, "fp32": 157.3e12}
+HBM_PEAK = 8.0e12
+DIM, FFN, LATENT_CH, TEXT_DIM = 4096, 12288, 128, 3072
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=8)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--blocks", type=int, default=36)
+    ap.add_argument("--precision", choices=("fp16", "bf16", "fp32"), default="fp16")
+    ap.add_argument("--grid", type=int, default=64, help="latent grid side (64 -> 1024x1024)")
+    ap.add_argument("--text", type=int, default=64)
+    ap.add_argument("--valid-text", type=int, default=40)
+    ap.add_argument("--cpu-baseline", choices=("on", "off"), default="on")
+    ap.add_argument("--cpu-tokens", type=int, default=4160, help="tokens of the single-block CPU sample")
+    return ap.parse_args()
+
+
+def cpu_baseline(tokens):
+    """One FP32 block of the oracle (C++ restatement of the reference CPU path)
+    at full width on the host cores; extrapolated to a 36-block denoise step."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import numpy as np
+    import oracle as O
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    names = ("norm1", "wq", "wk", "wv", "norm_q", "norm_k", "wo", "norm2", "w_up", "w_gate", "w_down")
+    shapes = ((DIM,), (DIM, DIM), (DIM, DIM), (DIM, DIM), (128,), (128,), (DIM, DIM), (DIM,), (FFN, DIM),
+              (FFN, DIM), (DIM, FFN))
+    w = {n: O.normal(s, 0, offset=i << 40, mean=1.0 if n.startswith("norm") else 0.0, std=0.02)
+         for i, (n, s) in enumerate(zip(names, shapes))}
+    grid = 64 if tokens >= 4160 else 32
+    text = tokens - grid * grid
+    cos, sin, mask = O.dit_constants(O.rope_frequencies(), grid, grid, min(40, text), text)
+    x = O.normal((tokens, DIM), 1)
+    mods = O.normal((6, DIM), 101, std=0.5)
+    t0 = time.perf_counter()
+    O.block_forward(w, x, mods, cos, sin, mask, precise=False, threads=threads)
+    block_s = time.perf_counter() - t0
+    return {"value": 1.0 / (36.0 * block_s), "unit": "steps/s", "cores": threads, "kind": "port",
+            "sample": f"1 FP32 DiT block (dim 4096, FFN 12288, S={tokens}) of the C++ oracle, "
+                      f"{block_s:.2f} s, extrapolated x36 blocks per step (heads and Euler excluded)",
+            "block_seconds": block_s}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the DiT block path runs on a single device "
+              "(multi-GPU sharding is a design note, not part of this build)", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+    import ernie_amd as E
+
+    dt = {"fp16": E.FP16, "bf16": E.BF16, "fp32": E.FP32}[args.precision]
+    H = W = args.grid
+    hw = H * W
+    S = hw + args.text
+    fac = E.Facade(0)
+    ctx = fac.hip
+    for b in range(args.blocks):
+        ctx.block_init_random(b, DIM, FFN, dt, seed=1000 + b, std=0.02)
+    ctx.heads_init_random(DIM, LATENT_CH, TEXT_DIM, dt, seed=7, std=0.02)
+    latent = torch.empty((LATENT_CH, H, W), dtype=torch.float32, device="cuda")
+    ctx.fill_normal(latent, E.FP32, latent.numel(), seed=3)
+    text = torch.empty((args.text, TEXT_DIM), dtype=torch.float32, device="cuda")
+    ctx.fill_normal(text, E.FP32, text.numel(), seed=4)
+    text[args.valid_text:] = 0.0  # pad_text
+    cos, sin, mask, valid = E.dit_constants(E.rope_frequencies(), W, H, args.valid_text, args.text)
+    cos_d, sin_d, mask_d = (torch.from_numpy(a).cuda() for a in (cos, sin, mask))
+    blocks = list(range(args.blocks))
+    start_latent = latent.clone()
+    torch.cuda.synchronize()
+
+    def run(steps, start_step):
+        latent.copy_(start_latent)
+        torch.cuda.synchronize()
+        return fac.denoise(blocks, latent, H, W, text, args.text, cos_d, sin_d, mask_d, valid,
+                           steps, start_step=start_step, dtype=dt)
+
+    if args.warmup > 0:
+        run(max(args.warmup, 1), 0)
+    print(f"bench: warmup done ({args.warmup} steps)", file=sys.stderr, flush=True)
+    ctx.profile_reset()
+    ctx.profile(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    step_s, _ = run(args.steps, 0)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ctx.profile(False)
+    prof = ctx.profile_query()
+    finite = bool(torch.isfinite(latent).all().item())
+    print(f"bench: timed {args.steps} steps in {elapsed:.3f} s", file=sys.stderr, flush=True)
+
+    mfma_cls = ("gemm_qkv", "sdpa", "gemm_out", "gemm_up_gate", "gemm_down")
+    tot_flop = sum(prof[c]["flop"] for c in mfma_cls)
+    tot_ms = sum(prof[c]["ms"] for c in mfma_cls)
+    peak = PEAK[args.precision]
+    dom = max(mfma_cls, key=lambda c: prof[c]["ms"])
+    d = prof[dom]
+    avg_s = d["ms"] / max(d["launches"], 1) * 1e-3
+    flop_per_launch = d["flop"] / max(d["launches"], 1)
+    achieved = flop_per_launch / avg_s if avg_s > 0 else 0.0
+    kernels = {c: {"launches": prof[c]["launches"], "avg_us": prof[c]["ms"] * 1e3 / max(prof[c]["launches"], 1),
+                   "tflops": (prof[c]["flop"] / (prof[c]["ms"] * 1e-3) / 1e12) if prof[c]["ms"] and prof[c]["flop"]
+                   else None,
+                   "gbps": (prof[c]["bytes"] / (prof[c]["ms"] * 1e-3) / 1e9) if prof[c]["ms"] else None}
+               for c in E.PROFILE_CLASSES}
+    result = {
+        "metric": METRIC, "value": args.steps / elapsed, "unit": "steps/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": elapsed / args.steps * 1e3, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": args.precision, "data": "synthetic",
+        "config": {"workload": f"{args.steps}-step flow-matching Euler DiT denoise at {16 * W}x{16 * H} "
+                               f"(latent [128,{H},{W}], {hw} image + {args.text} text tokens, {args.valid_text} valid, "
+                               f"S={S}), {args.blocks} blocks, dim 4096, 32 heads x 128, FFN 12288 gated erf-GELU, "
+                               f"{args.precision} storage / fp32 accumulate, turbo schedule shift 4, CFG 1",
+                   "blocks": args.blocks, "tokens": S, "latent": [LATENT_CH, H, W], "text_tokens": args.text,
+                   "valid_text": args.valid_text},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved / 1e12, "peak": peak / 1e12,
+                     "unit": "TFLOP/s", "frac": achieved / peak, "traffic": None,
+                     "flop_per_launch": flop_per_launch, "avg_launch_us": avg_s * 1e6},
+        "mfma_util_sdpa_gemm": (tot_flop / (tot_ms * 1e-3)) / peak if tot_ms else None,
+        "sdpa_gemm_tflops": (tot_flop / (tot_ms * 1e-3)) / 1e12 if tot_ms else None,
+        "kernels": kernels,
+        "step_seconds": [round(float(s), 5) for s in step_s],
+        "latent_finite": finite,
+    }
+    if args.cpu_baseline == "on":
+        print("bench: cpu baseline ...", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(args.cpu_tokens)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    fac.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,961 @@
+// SPDX-License-Identifier: MIT
+// extern "C" layer of ernie_hip (declarations and reference citations in
+// include/ernie_hip.h). Owns the HIP stream, the resident block / head weights,
+// the activation workspace and the optional per-kernel event timing.
+#include "ernie_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "kernels.hpp"
+
+using namespace ehip;
+
+namespace {
+
+constexpr int kHeadDim = 128;
+
+struct DeviceBuffer {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+
+struct BlockWeights {
+    bool loaded = false;
+    int dim = 0, ffn = 0, dtype = 0;
+    DeviceBuffer norm1, norm_q, norm_k, norm2;  // FP32
+    DeviceBuffer wqkv;                          // [3*dim][dim]
+    DeviceBuffer wo;                            // [dim][dim]
+    DeviceBuffer w_ug;                          // [2*ffn][dim], 32-row up/gate interleave
+    DeviceBuffer w_down;                        // [dim][ffn]
+};
+
+struct HeadWeights {
+    bool loaded = false;
+    int dim = 0, latent_ch = 0, text_dim = 0, dtype = 0;
+    DeviceBuffer x_w, x_b, text_w, t1_w, t1_b, t2_w, t2_b, mod_w, mod_b, out_mod_w, out_mod_b, proj_w, proj_b;
+};
+
+struct Launch {
+    int cls;
+    hipEvent_t start, stop;
+    double flop, bytes;
+};
+
+}  // namespace
+
+struct ernie_hip_ctx {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    std::string error;
+    int query_rows = 128;
+    std::vector<BlockWeights> blocks;
+    HeadWeights heads;
+    // Activation workspace, grown on demand.
+    DeviceBuffer ws;
+    DeviceBuffer staging;  // FP32 upload staging
+    DeviceBuffer head_ws;  // head intermediates
+    DeviceBuffer dit_act;  // run_dit activations: x [S][dim], c, mods
+    // Event timing.
+    bool profiling = false;
+    std::vector<hipEvent_t> event_pool;
+    size_t event_next = 0;
+    std::vector<Launch> pending;
+    long launches[ERNIE_PROFILE_CLASSES] = {};
+    double ms[ERNIE_PROFILE_CLASSES] = {};
+    double flop[ERNIE_PROFILE_CLASSES] = {};
+    double bytes[ERNIE_PROFILE_CLASSES] = {};
+};
+
+namespace {
+
+int fail(ernie_hip_ctx* ctx, int code, const std::string& msg)
+{
+    if (ctx) ctx->error = msg;
+    return code;
+}
+
+int hip_status(ernie_hip_ctx* ctx, hipError_t e, const char* what)
+{
+    if (e == hipSuccess) return ERNIE_OK;
+    const int code = e == hipErrorOutOfMemory ? ERNIE_ALLOCATION_FAILED : ERNIE_ERROR;
+    return fail(ctx, code, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// Kernel launcher statuses: -1 = rejected shape, -k = hipError k.
+int kernel_status(ernie_hip_ctx* ctx, int rc, const char* what)
+{
+    if (rc == 0) return ERNIE_OK;
+    if (rc == -1) return fail(ctx, ERNIE_ERROR, std::string(what) + ": invalid arguments");
+    return hip_status(ctx, hipError_t(-rc), what);
+}
+
+bool valid_dtype(int dt) { return dt == ERNIE_DTYPE_FP32 || dt == ERNIE_DTYPE_FP16 || dt == ERNIE_DTYPE_BF16; }
+size_t esize(int dt) { return dt == ERNIE_DTYPE_FP32 ? 4 : 2; }
+
+int dev_alloc(ernie_hip_ctx* ctx, DeviceBuffer& b, size_t bytes, const char* what)
+{
+    if (b.ptr && b.bytes >= bytes) return ERNIE_OK;
+    if (b.ptr) {
+        // Work queued on the stream may still read the old buffer.
+        (void)hipStreamSynchronize(ctx->stream);
+        (void)hipFree(b.ptr);
+        b.ptr = nullptr;
+        b.bytes = 0;
+    }
+    if (!bytes) return ERNIE_OK;
+    const hipError_t e = hipMalloc(&b.ptr, bytes);
+    if (e != hipSuccess) {
+        b.ptr = nullptr;
+        return hip_status(ctx, e, what);
+    }
+    b.bytes = bytes;
+    return ERNIE_OK;
+}
+
+void dev_free(DeviceBuffer& b)
+{
+    if (b.ptr) (void)hipFree(b.ptr);
+    b = DeviceBuffer{};
+}
+
+void free_block(BlockWeights& w)
+{
+    for (DeviceBuffer* b : {&w.norm1, &w.norm_q, &w.norm_k, &w.norm2, &w.wqkv, &w.wo, &w.w_ug, &w.w_down}) dev_free(*b);
+    w = BlockWeights{};
+}
+
+void free_heads(HeadWeights& h)
+{
+    for (DeviceBuffer* b : {&h.x_w, &h.x_b, &h.text_w, &h.t1_w, &h.t1_b, &h.t2_w, &h.t2_b, &h.mod_w, &h.mod_b,
+                            &h.out_mod_w, &h.out_mod_b, &h.proj_w, &h.proj_b})
+        dev_free(*b);
+    h = HeadWeights{};
+}
+
+// ---- event timing ------------------------------------------------------------------
+hipEvent_t next_event(ernie_hip_ctx* ctx)
+{
+    if (ctx->event_next == ctx->event_pool.size()) {
+        hipEvent_t e = nullptr;
+        if (hipEventCreate(&e) != hipSuccess) return nullptr;
+        ctx->event_pool.push_back(e);
+    }
+    return ctx->event_pool[ctx->event_next++];
+}
+
+struct Timed {
+    ernie_hip_ctx* ctx;
+    int cls;
+    double flop, bytes;
+    hipEvent_t start = nullptr;
+    Timed(ernie_hip_ctx* c, int k, double f, double b) : ctx(c), cls(k), flop(f), bytes(b)
+    {
+        if (ctx->profiling) {
+            start = next_event(ctx);
+            if (start) (void)hipEventRecord(start, ctx->stream);
+        }
+    }
+    ~Timed()
+    {
+        if (!start) return;
+        hipEvent_t stop = next_event(ctx);
+        if (!stop) return;
+        (void)hipEventRecord(stop, ctx->stream);
+        ctx->pending.push_back(Launch{cls, start, stop, flop, bytes});
+    }
+};
+
+int collect(ernie_hip_ctx* ctx)
+{
+    if (ctx->pending.empty()) {
+        ctx->event_next = 0;
+        return ERNIE_OK;
+    }
+    const hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_status(ctx, e, "profile synchronize");
+    for (const Launch& l : ctx->pending) {
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, l.start, l.stop) == hipSuccess) {
+            ctx->launches[l.cls] += 1;
+            ctx->ms[l.cls] += ms;
+            ctx->flop[l.cls] += l.flop;
+            ctx->bytes[l.cls] += l.bytes;
+        }
+    }
+    ctx->pending.clear();
+    ctx->event_next = 0;
+    return ERNIE_OK;
+}
+
+enum { P_QKV = 0, P_SDPA = 1, P_OUT = 2, P_UG = 3, P_DOWN = 4, P_NORM = 5, P_ROPE = 6, P_HEADS = 7 };
+
+double gemm_bytes(double M, double N, double K, double e, double eo) { return (M * K + N * K) * e + M * N * eo; }
+
+// ---- uploads ------------------------------------------------------------------------
+int upload_f32(ernie_hip_ctx* ctx, DeviceBuffer& dst, const float* src, size_t count, const char* what)
+{
+    int rc = dev_alloc(ctx, dst, count * 4, what);
+    if (rc) return rc;
+    return hip_status(ctx, hipMemcpyAsync(dst.ptr, src, count * 4, hipMemcpyHostToDevice, ctx->stream), what);
+}
+
+// Host FP32 -> device dtype at `dst` (+ element offset) via the staging buffer.
+int upload_convert(ernie_hip_ctx* ctx, void* dst, size_t dst_offset, int dtype, const float* src, size_t count,
+                   const char* what)
+{
+    int rc = dev_alloc(ctx, ctx->staging, count * 4, "staging buffer");
+    if (rc) return rc;
+    rc = hip_status(ctx, hipMemcpyAsync(ctx->staging.ptr, src, count * 4, hipMemcpyHostToDevice, ctx->stream), what);
+    if (rc) return rc;
+    char* base = static_cast<char*>(dst) + dst_offset * esize(dtype);
+    rc = kernel_status(ctx, convert(ctx->staging.ptr, ERNIE_DTYPE_FP32, base, dtype, count, ctx->stream), what);
+    if (rc) return rc;
+    // The staging buffer is reused by the next upload: finish this one first.
+    return hip_status(ctx, hipStreamSynchronize(ctx->stream), what);
+}
+
+int alloc_block(ernie_hip_ctx* ctx, BlockWeights& w, int dim, int ffn, int dtype)
+{
+    const size_t e = esize(dtype);
+    int rc = 0;
+    rc = rc ? rc : dev_alloc(ctx, w.norm1, (size_t)dim * 4, "block weights");
+    rc = rc ? rc : dev_alloc(ctx, w.norm2, (size_t)dim * 4, "block weights");
+    rc = rc ? rc : dev_alloc(ctx, w.norm_q, kHeadDim * 4, "block weights");
+    rc = rc ? rc : dev_alloc(ctx, w.norm_k, kHeadDim * 4, "block weights");
+    rc = rc ? rc : dev_alloc(ctx, w.wqkv, 3 * (size_t)dim * dim * e, "block weights");
+    rc = rc ? rc : dev_alloc(ctx, w.wo, (size_t)dim * dim * e, "block weights");
+    rc = rc ? rc : dev_alloc(ctx, w.w_ug, 2 * (size_t)ffn * dim * e, "block weights");
+    rc = rc ? rc : dev_alloc(ctx, w.w_down, (size_t)dim * ffn * e, "block weights");
+    if (rc) {
+        free_block(w);
+        return rc;
+    }
+    w.dim = dim;
+    w.ffn = ffn;
+    w.dtype = dtype;
+    return ERNIE_OK;
+}
+
+int check_block_dims(ernie_hip_ctx* ctx, int dim, int ffn, int dtype)
+{
+    if (!valid_dtype(dtype)) return fail(ctx, ERNIE_ERROR, "invalid dtype");
+    if (dim < 128 || dim % 128 || dim > 4096) return fail(ctx, ERNIE_ERROR, "dim must be a multiple of 128 in [128,4096]");
+    if (ffn < 32 || ffn % 32) return fail(ctx, ERNIE_ERROR, "ffn must be a positive multiple of 32");
+    return ERNIE_OK;
+}
+
+BlockWeights* block_slot(ernie_hip_ctx* ctx, int index)
+{
+    if (index < 0 || index > 4096) return nullptr;
+    if ((size_t)index >= ctx->blocks.size()) ctx->blocks.resize(index + 1);
+    return &ctx->blocks[index];
+}
+
+// ---- workspace -------------------------------------------------------------------------
+struct BlockWs {
+    void* h;      // [S][dim] dtype
+    void* qkv;    // [S][3dim] dtype
+    void* attn;   // [S][dim] dtype
+    float* x1;    // [S][dim] f32
+    void* p;      // [S][ffn] dtype
+};
+
+int block_workspace(ernie_hip_ctx* ctx, int S, int dim, int ffn, int dtype, BlockWs& ws)
+{
+    const size_t e = esize(dtype);
+    auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+    const size_t h = up((size_t)S * dim * e), qkv = up(3 * (size_t)S * dim * e), x1 = up((size_t)S * dim * 4),
+                 p = up((size_t)S * ffn * e);
+    const int rc = dev_alloc(ctx, ctx->ws, h + qkv + h + x1 + p, "block workspace");
+    if (rc) return rc;
+    char* b = static_cast<char*>(ctx->ws.ptr);
+    ws.h = b;
+    ws.qkv = b + h;
+    ws.attn = b + h + qkv;
+    ws.x1 = reinterpret_cast<float*>(b + h + qkv + h);
+    ws.p = b + h + qkv + h + x1;
+    return ERNIE_OK;
+}
+
+int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, float* out, const float* mods,
+                  const float* cos_t, const float* sin_t, const float* mask, int valid_keys, int S)
+{
+    const int D = w.dim, F = w.ffn, dt = w.dtype, H = D / kHeadDim;
+    const double e = (double)esize(dt), dS = S;
+    BlockWs ws{};
+    int rc = block_workspace(ctx, S, D, F, dt, ws);
+    if (rc) return rc;
+    hipStream_t s = ctx->stream;
+    const float *shift_sa = mods, *scale_sa = mods + D, *gate_sa = mods + 2 * D;
+    const float *shift_mlp = mods + 3 * D, *scale_mlp = mods + 4 * D, *gate_mlp = mods + 5 * D;
+    // rmsn_8 + add_0/mul_1/add_2
+    {
+        Timed t(ctx, P_NORM, 0, dS * D * (4 + e));
+        rc = kernel_status(ctx, rmsnorm_modulate(x, ERNIE_DTYPE_FP32, static_cast<const float*>(w.norm1.ptr), shift_sa, scale_sa,
+                                                 S, D, 1e-6f, ws.h, dt, s), "rmsnorm_modulate");
+        if (rc) return rc;
+    }
+    // gemm_0/1/2 as one [3D][D] projection
+    {
+        GemmArgs g;
+        g.A = ws.h; g.lda = D; g.W = w.wqkv.ptr; g.ldw = D; g.M = S; g.N = 3 * D; g.K = D; g.dtype = dt;
+        g.epilogue = EPI_STORE; g.C = ws.qkv; g.ldc = 3 * D; g.c_dtype = dt;
+        Timed t(ctx, P_QKV, 2.0 * dS * 3 * D * D, gemm_bytes(dS, 3.0 * D, D, e, e));
+        rc = kernel_status(ctx, gemm(g, s), "gemm qkv");
+        if (rc) return rc;
+    }
+    // rmsn_9 / rmsn_10 + rotary, in place on the Q and K column blocks
+    {
+        Timed t(ctx, P_ROPE, 0, dS * 2 * D * e * 2 + dS * 128 * 8);
+        rc = kernel_status(ctx, qk_norm_rope(ws.qkv, dt, S, H, 3L * D, static_cast<const float*>(w.norm_q.ptr), cos_t,
+                                             sin_t, s), "qk_norm_rope q");
+        if (rc) return rc;
+        rc = kernel_status(ctx, qk_norm_rope(static_cast<char*>(ws.qkv) + (size_t)D * esize(dt), dt, S, H, 3L * D,
+                                             static_cast<const float*>(w.norm_k.ptr), cos_t, sin_t, s),
+                           "qk_norm_rope k");
+        if (rc) return rc;
+    }
+    // sdpa_22
+    {
+        SdpaArgs a;
+        const size_t eb = esize(dt);
+        a.q = ws.qkv; a.k = static_cast<char*>(ws.qkv) + (size_t)D * eb; a.v = static_cast<char*>(ws.qkv) + 2 * (size_t)D * eb;
+        a.o = ws.attn; a.dtype = dt; a.heads = H; a.kv_heads = H; a.sq = S; a.sk = S; a.d = kHeadDim;
+        a.q_hs = a.k_hs = a.v_hs = kHeadDim; a.q_rs = a.k_rs = a.v_rs = 3L * D;
+        a.o_hs = kHeadDim; a.o_rs = D;
+        a.mask = mask; a.mask_heads = 1; a.mask_rows = 1; a.valid_keys = valid_keys;
+        Timed t(ctx, P_SDPA, 4.0 * dS * dS * kHeadDim * H, 4.0 * dS * D * e);
+        rc = kernel_status(ctx, sdpa(a, s), "sdpa");
+        if (rc) return rc;
+    }
+    // gemm_3 + mul_15 + ErnieResidualAdd add_16 (FP32)
+    {
+        GemmArgs g;
+        g.A = ws.attn; g.lda = D; g.W = w.wo.ptr; g.ldw = D; g.M = S; g.N = D; g.K = D; g.dtype = dt;
+        g.epilogue = EPI_GATE_RESID; g.C = ws.x1; g.ldc = D; g.c_dtype = ERNIE_DTYPE_FP32; g.resid = x; g.ld_resid = D;
+        g.gate = gate_sa;
+        Timed t(ctx, P_OUT, 2.0 * dS * D * D, gemm_bytes(dS, D, D, e, 8));
+        rc = kernel_status(ctx, gemm(g, s), "gemm out");
+        if (rc) return rc;
+    }
+    // rmsn_11 + add_17/mul_18/add_19
+    {
+        Timed t(ctx, P_NORM, 0, dS * D * (4 + e));
+        rc = kernel_status(ctx, rmsnorm_modulate(ws.x1, ERNIE_DTYPE_FP32, static_cast<const float*>(w.norm2.ptr), shift_mlp,
+                                                 scale_mlp, S, D, 1e-6f, ws.h, dt, s), "rmsnorm_modulate 2");
+        if (rc) return rc;
+    }
+    // gemm_4 (up) + gemm_5 (gate) + ErnieGELU + mul_20 in one GEMM epilogue
+    {
+        GemmArgs g;
+        g.A = ws.h; g.lda = D; g.W = w.w_ug.ptr; g.ldw = D; g.M = S; g.N = 2 * F; g.K = D; g.dtype = dt;
+        g.epilogue = EPI_GEGLU; g.C = ws.p; g.ldc = F; g.c_dtype = dt;
+        Timed t(ctx, P_UG, 2.0 * dS * 2 * F * D, gemm_bytes(dS, 2.0 * F, D, e, 0) + dS * F * e);
+        rc = kernel_status(ctx, gemm(g, s), "gemm up/gate");
+        if (rc) return rc;
+    }
+    // gemm_6 + mul_21 + ErnieResidualAdd add_22
+    {
+        GemmArgs g;
+        g.A = ws.p; g.lda = F; g.W = w.w_down.ptr; g.ldw = F; g.M = S; g.N = D; g.K = F; g.dtype = dt;
+        g.epilogue = EPI_GATE_RESID; g.C = out; g.ldc = D; g.c_dtype = ERNIE_DTYPE_FP32; g.resid = ws.x1; g.ld_resid = D;
+        g.gate = gate_mlp;
+        Timed t(ctx, P_DOWN, 2.0 * dS * D * F, gemm_bytes(dS, D, F, e, 8));
+        rc = kernel_status(ctx, gemm(g, s), "gemm down");
+        if (rc) return rc;
+    }
+    return ERNIE_OK;
+}
+
+// ---- heads ------------------------------------------------------------------------
+int head_gemm(ernie_hip_ctx* ctx, const void* a, const void* w, const float* bias, float* c, int M, int N, int K, int dt)
+{
+    GemmArgs g;
+    g.A = a; g.lda = K; g.W = w; g.ldw = K; g.M = M; g.N = N; g.K = K; g.dtype = dt;
+    g.epilogue = EPI_STORE; g.C = c; g.ldc = N; g.c_dtype = ERNIE_DTYPE_FP32; g.bias = bias;
+    Timed t(ctx, P_HEADS, 2.0 * M * N * K, gemm_bytes(M, N, K, (double)esize(dt), 4));
+    return kernel_status(ctx, gemm(g, ctx->stream), "head gemm");
+}
+
+int input_head(ernie_hip_ctx* ctx, const float* latent, int hw, const float* text, int T, const float* feat, float* x,
+               float* c, float* mods)
+{
+    const HeadWeights& h = ctx->heads;
+    const int D = h.dim, dt = h.dtype;
+    const size_t e = esize(dt);
+    auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+    const size_t tok = up((size_t)hw * h.latent_ch * e), txt = up((size_t)T * h.text_dim * e), t1 = up((size_t)D * 4);
+    int rc = dev_alloc(ctx, ctx->head_ws, tok + txt + t1, "head workspace");
+    if (rc) return rc;
+    char* b = static_cast<char*>(ctx->head_ws.ptr);
+    void* tokens = b;
+    void* text_d = b + tok;
+    float* t1v = reinterpret_cast<float*>(b + tok + txt);
+    hipStream_t s = ctx->stream;
+    rc = kernel_status(ctx, transpose_to_tokens(latent, h.latent_ch, hw, tokens, dt, s), "latent tokens");
+    if (rc) return rc;
+    rc = head_gemm(ctx, tokens, h.x_w.ptr, static_cast<const float*>(h.x_b.ptr), x, hw, D, h.latent_ch, dt);
+    if (rc) return rc;
+    if (T > 0) {
+        rc = kernel_status(ctx, convert(text, ERNIE_DTYPE_FP32, text_d, dt, (size_t)T * h.text_dim, s), "text convert");
+        if (rc) return rc;
+        rc = head_gemm(ctx, text_d, h.text_w.ptr, nullptr, x + (size_t)hw * D, T, D, h.text_dim, dt);
+        if (rc) return rc;
+    }
+    Timed t(ctx, P_HEADS, 2.0 * D * (8.0 * D), (double)D * 8 * D * e);
+    rc = kernel_status(ctx, gemv(h.t1_w.ptr, dt, static_cast<const float*>(h.t1_b.ptr), feat, D, D, 0, t1v, s), "time mlp 1");
+    if (rc) return rc;
+    rc = kernel_status(ctx, gemv(h.t2_w.ptr, dt, static_cast<const float*>(h.t2_b.ptr), t1v, D, D, 1, c, s), "time mlp 2");
+    if (rc) return rc;
+    return kernel_status(ctx, gemv(h.mod_w.ptr, dt, static_cast<const float*>(h.mod_b.ptr), c, 6 * D, D, 1, mods, s),
+                         "adaLN");
+}
+
+int output_head(ernie_hip_ctx* ctx, const float* x, int hw, const float* c, float* pred)
+{
+    const HeadWeights& h = ctx->heads;
+    const int D = h.dim, dt = h.dtype;
+    const size_t e = esize(dt);
+    auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+    const size_t mm = up(2 * (size_t)D * 4), y = up((size_t)hw * D * e), proj = up((size_t)hw * h.latent_ch * 4);
+    int rc = dev_alloc(ctx, ctx->head_ws, mm + y + proj, "head workspace");
+    if (rc) return rc;
+    char* b = static_cast<char*>(ctx->head_ws.ptr);
+    float* mmv = reinterpret_cast<float*>(b);
+    void* yv = b + mm;
+    float* projv = reinterpret_cast<float*>(b + mm + y);
+    hipStream_t s = ctx->stream;
+    {
+        Timed t(ctx, P_HEADS, 2.0 * D * 2 * D, 2.0 * D * D * e);
+        rc = kernel_status(ctx, gemv(h.out_mod_w.ptr, dt, static_cast<const float*>(h.out_mod_b.ptr), c, 2 * D, D, 0,
+                                     mmv, s), "output adaLN");
+        if (rc) return rc;
+    }
+    rc = kernel_status(ctx, layernorm_modulate(x, mmv + D, mmv, hw, D, 1e-6f, yv, dt, s), "output layernorm");
+    if (rc) return rc;
+    rc = head_gemm(ctx, yv, h.proj_w.ptr, static_cast<const float*>(h.proj_b.ptr), projv, hw, h.latent_ch, D, dt);
+    if (rc) return rc;
+    return kernel_status(ctx, tokens_to_latent(projv, hw, h.latent_ch, pred, s), "output unpatchify");
+}
+
+int check_block_call(ernie_hip_ctx* ctx, int index, int S, const void* x, const void* out, const void* mods,
+                     const void* cos_t, const void* sin_t, int valid_keys)
+{
+    if (index < 0 || (size_t)index >= ctx->blocks.size() || !ctx->blocks[index].loaded)
+        return fail(ctx, ERNIE_ERROR, "block " + std::to_string(index) + " is not loaded");
+    if (S < 1 || S > 65536) return fail(ctx, ERNIE_ERROR, "token count out of range");
+    if (!x || !out || !mods || !cos_t || !sin_t) return fail(ctx, ERNIE_ERROR, "null block tensor");
+    if (valid_keys < 0 || valid_keys > S) return fail(ctx, ERNIE_ERROR, "valid_keys out of range");
+    return ERNIE_OK;
+}
+
+}  // namespace
+
+// =====================================================================================
+extern "C" {
+
+int ernie_hip_create(int device, ernie_hip_ctx** out)
+{
+    if (!out) return ERNIE_ERROR;
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) return ERNIE_ERROR;
+    if (hipSetDevice(device) != hipSuccess) return ERNIE_ERROR;
+    auto* ctx = new (std::nothrow) ernie_hip_ctx();
+    if (!ctx) return ERNIE_ALLOCATION_FAILED;
+    ctx->device = device;
+    if (hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess) {
+        delete ctx;
+        return ERNIE_ERROR;
+    }
+    ctx->stream = ctx->own_stream;
+    *out = ctx;
+    return ERNIE_OK;
+}
+
+void ernie_hip_destroy(ernie_hip_ctx* ctx)
+{
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    for (auto& b : ctx->blocks) free_block(b);
+    free_heads(ctx->heads);
+    dev_free(ctx->ws);
+    dev_free(ctx->staging);
+    dev_free(ctx->head_ws);
+    dev_free(ctx->dit_act);
+    for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
+    if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+}
+
+const char* ernie_hip_last_error(const ernie_hip_ctx* ctx) { return ctx ? ctx->error.c_str() : "null context"; }
+
+int ernie_hip_set_stream(ernie_hip_ctx* ctx, void* stream)
+{
+    if (!ctx) return ERNIE_ERROR;
+    ctx->stream = static_cast<hipStream_t>(stream);
+    return ERNIE_OK;
+}
+
+void* ernie_hip_own_stream(ernie_hip_ctx* ctx) { return ctx ? ctx->own_stream : nullptr; }
+
+void* ernie_hip_get_stream(ernie_hip_ctx* ctx) { return ctx ? ctx->stream : nullptr; }
+
+int ernie_hip_synchronize(ernie_hip_ctx* ctx)
+{
+    if (!ctx) return ERNIE_ERROR;
+    return hip_status(ctx, hipStreamSynchronize(ctx->stream), "synchronize");
+}
+
+int ernie_hip_malloc(ernie_hip_ctx* ctx, size_t bytes, void** out)
+{
+    if (!ctx || !out) return ERNIE_ERROR;
+    *out = nullptr;
+    return hip_status(ctx, hipMalloc(out, bytes ? bytes : 1), "malloc");
+}
+
+int ernie_hip_free(ernie_hip_ctx* ctx, void* ptr)
+{
+    if (!ctx) return ERNIE_ERROR;
+    return hip_status(ctx, hipFree(ptr), "free");
+}
+
+int ernie_hip_memcpy_h2d(ernie_hip_ctx* ctx, void* dst, const void* src, size_t bytes)
+{
+    if (!ctx) return ERNIE_ERROR;
+    int rc = hip_status(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "h2d");
+    return rc ? rc : hip_status(ctx, hipStreamSynchronize(ctx->stream), "h2d");
+}
+
+int ernie_hip_memcpy_d2h(ernie_hip_ctx* ctx, void* dst, const void* src, size_t bytes)
+{
+    if (!ctx) return ERNIE_ERROR;
+    int rc = hip_status(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "d2h");
+    return rc ? rc : hip_status(ctx, hipStreamSynchronize(ctx->stream), "d2h");
+}
+
+// ---- operators ----------------------------------------------------------------------
+int ernie_hip_rmsnorm(ernie_hip_ctx* ctx, const void* x, int x_dtype, const float* gamma, const float* shift,
+                      const float* scale, int rows, int width, float eps, void* out, int out_dtype)
+{
+    if (!ctx) return ERNIE_ERROR;
+    return kernel_status(ctx, rmsnorm_modulate(x, x_dtype, gamma, shift, scale, rows, width, eps, out, out_dtype,
+                                               ctx->stream), "rmsnorm");
+}
+
+int ernie_hip_layernorm_modulate(ernie_hip_ctx* ctx, const float* x, const float* shift, const float* scale, int rows,
+                                 int width, float eps, void* out, int out_dtype)
+{
+    if (!ctx) return ERNIE_ERROR;
+    return kernel_status(ctx, layernorm_modulate(x, shift, scale, rows, width, eps, out, out_dtype, ctx->stream),
+                         "layernorm");
+}
+
+int ernie_hip_gelu(ernie_hip_ctx* ctx, void* data, int dtype, size_t count)
+{
+    if (!ctx) return ERNIE_ERROR;
+    return kernel_status(ctx, gelu_inplace(data, dtype, count, ctx->stream), "gelu");
+}
+
+int ernie_hip_residual_add(ernie_hip_ctx* ctx, const void* a, int a_dtype, const void* b, int b_dtype, float* out,
+                           size_t count)
+{
+    if (!ctx) return ERNIE_ERROR;
+    return kernel_status(ctx, residual_add(a, a_dtype, b, b_dtype, out, count, ctx->stream), "residual_add");
+}
+
+int ernie_hip_gemm(ernie_hip_ctx* ctx, const void* a, long lda, const void* w, long ldw, const float* bias, void* c,
+                   long ldc, int m, int n, int k, int dtype, int out_dtype)
+{
+    if (!ctx) return ERNIE_ERROR;
+    GemmArgs g;
+    g.A = a; g.lda = lda; g.W = w; g.ldw = ldw; g.M = m; g.N = n; g.K = k; g.dtype = dtype;
+    g.epilogue = EPI_STORE; g.C = c; g.ldc = ldc; g.c_dtype = out_dtype; g.bias = bias;
+    return kernel_status(ctx, gemm(g, ctx->stream), "gemm");
+}
+
+int ernie_hip_sdpa(ernie_hip_ctx* ctx, const void* q, const void* k, const void* v, void* out, int dtype, int heads,
+                   int kv_heads, int sq, int sk, int d, long q_hs, long q_rs, long k_hs, long k_rs, long v_hs,
+                   long v_rs, long o_hs, long o_rs, const float* mask, int mask_heads, int mask_rows, int valid_keys,
+                   float scale)
+{
+    if (!ctx) return ERNIE_ERROR;
+    SdpaArgs a;
+    a.q = q; a.k = k; a.v = v; a.o = out; a.dtype = dtype; a.heads = heads; a.kv_heads = kv_heads;
+    a.sq = sq; a.sk = sk; a.d = d; a.q_hs = q_hs; a.q_rs = q_rs; a.k_hs = k_hs; a.k_rs = k_rs;
+    a.v_hs = v_hs; a.v_rs = v_rs; a.o_hs = o_hs; a.o_rs = o_rs; a.mask = mask; a.mask_heads = mask_heads;
+    a.mask_rows = mask_rows; a.valid_keys = valid_keys; a.scale = scale;
+    return kernel_status(ctx, sdpa(a, ctx->stream), "sdpa");
+}
+
+int ernie_hip_set_attention_query_rows(ernie_hip_ctx* ctx, int rows)
+{
+    if (!ctx) return ERNIE_ERROR;
+    if (rows != 128 && rows != 64 && rows != 32 && rows != 16)
+        return fail(ctx, ERNIE_ERROR, "Attention query rows must be 128, 64, 32 or 16");
+    ctx->query_rows = rows;
+    return ERNIE_OK;
+}
+
+uint64_t ernie_hip_attention_internal_submissions(const ernie_hip_ctx*) { return 0; }
+
+int ernie_hip_qk_norm_rope(ernie_hip_ctx* ctx, void* x, int dtype, int rows, int heads, long row_stride,
+                           const float* gamma, const float* cos_t, const float* sin_t)
+{
+    if (!ctx) return ERNIE_ERROR;
+    return kernel_status(ctx, qk_norm_rope(x, dtype, rows, heads, row_stride, gamma, cos_t, sin_t, ctx->stream),
+                         "qk_norm_rope");
+}
+
+int ernie_hip_euler_step(ernie_hip_ctx* ctx, const float* x, const float* v, float delta, size_t count, float* out)
+{
+    if (!ctx) return ERNIE_ERROR;
+    if (!std::isfinite(delta) || delta >= 0.f || delta < -1.f)
+        return fail(ctx, ERNIE_ERROR, "Incompatible Euler shapes or delta outside [-1,0)");
+    return kernel_status(ctx, euler_step(x, v, delta, count, out, ctx->stream), "euler");
+}
+
+int ernie_hip_finite(ernie_hip_ctx* ctx, const float* x, size_t count, int* finite)
+{
+    if (!ctx || !finite) return ERNIE_ERROR;
+    int* flag = nullptr;
+    int rc = hip_status(ctx, hipMalloc(&flag, sizeof(int)), "finite flag");
+    if (rc) return rc;
+    int host = 0;
+    rc = hip_status(ctx, hipMemcpyAsync(flag, &host, sizeof(int), hipMemcpyHostToDevice, ctx->stream), "finite flag");
+    if (!rc) rc = kernel_status(ctx, finite_flags(x, count, flag, ctx->stream), "finite");
+    if (!rc) rc = hip_status(ctx, hipMemcpyAsync(&host, flag, sizeof(int), hipMemcpyDeviceToHost, ctx->stream), "finite");
+    if (!rc) rc = hip_status(ctx, hipStreamSynchronize(ctx->stream), "finite");
+    (void)hipFree(flag);
+    if (!rc) *finite = host ? 0 : 1;
+    return rc;
+}
+
+int ernie_hip_fill_normal(ernie_hip_ctx* ctx, void* out, int dtype, size_t count, uint64_t seed, uint64_t offset,
+                          float mean, float std_dev)
+{
+    if (!ctx) return ERNIE_ERROR;
+    return kernel_status(ctx, fill_normal(out, dtype, count, seed, offset, mean, std_dev, ctx->stream), "fill_normal");
+}
+
+int ernie_hip_convert(ernie_hip_ctx* ctx, const void* in, int in_dtype, void* out, int out_dtype, size_t count)
+{
+    if (!ctx) return ERNIE_ERROR;
+    return kernel_status(ctx, convert(in, in_dtype, out, out_dtype, count, ctx->stream), "convert");
+}
+
+// ---- blocks -----------------------------------------------------------------------------
+int ernie_hip_block_upload(ernie_hip_ctx* ctx, int index, const ernie_block_host_weights* w, int dim, int ffn,
+                           int dtype)
+{
+    if (!ctx || !w) return ERNIE_ERROR;
+    int rc = check_block_dims(ctx, dim, ffn, dtype);
+    if (rc) return rc;
+    const float* parts[] = {w->norm1, w->wq, w->wk, w->wv, w->norm_q, w->norm_k, w->wo, w->norm2, w->w_up, w->w_gate, w->w_down};
+    for (const float* p : parts)
+        if (!p) return fail(ctx, ERNIE_ERROR, "null block weight");
+    BlockWeights* slot = block_slot(ctx, index);
+    if (!slot) return fail(ctx, ERNIE_ERROR, "block index out of range");
+    free_block(*slot);
+    BlockWeights bw;
+    rc = alloc_block(ctx, bw, dim, ffn, dtype);
+    if (rc) return rc;
+    const size_t DD = (size_t)dim * dim;
+    rc = rc ? rc : upload_f32(ctx, bw.norm1, w->norm1, dim, "norm1");
+    rc = rc ? rc : upload_f32(ctx, bw.norm2, w->norm2, dim, "norm2");
+    rc = rc ? rc : upload_f32(ctx, bw.norm_q, w->norm_q, kHeadDim, "norm_q");
+    rc = rc ? rc : upload_f32(ctx, bw.norm_k, w->norm_k, kHeadDim, "norm_k");
+    rc = rc ? rc : upload_convert(ctx, bw.wqkv.ptr, 0, dtype, w->wq, DD, "wq");
+    rc = rc ? rc : upload_convert(ctx, bw.wqkv.ptr, DD, dtype, w->wk, DD, "wk");
+    rc = rc ? rc : upload_convert(ctx, bw.wqkv.ptr, 2 * DD, dtype, w->wv, DD, "wv");
+    rc = rc ? rc : upload_convert(ctx, bw.wo.ptr, 0, dtype, w->wo, DD, "wo");
+    rc = rc ? rc : upload_convert(ctx, bw.w_down.ptr, 0, dtype, w->w_down, (size_t)dim * ffn, "w_down");
+    for (int parity = 0; parity < 2 && !rc; ++parity) {
+        const float* src = parity ? w->w_gate : w->w_up;
+        const size_t count = (size_t)ffn * dim;
+        rc = dev_alloc(ctx, ctx->staging, count * 4, "staging buffer");
+        if (!rc) rc = hip_status(ctx, hipMemcpyAsync(ctx->staging.ptr, src, count * 4, hipMemcpyHostToDevice, ctx->stream), "w_ug");
+        if (!rc) rc = kernel_status(ctx, interleave_up_gate(static_cast<const float*>(ctx->staging.ptr), bw.w_ug.ptr,
+                                                            dtype, ffn, dim, parity, ctx->stream), "w_ug");
+        if (!rc) rc = hip_status(ctx, hipStreamSynchronize(ctx->stream), "w_ug");
+    }
+    if (rc) {
+        free_block(bw);
+        return rc;
+    }
+    bw.loaded = true;
+    *slot = bw;
+    return ERNIE_OK;
+}
+
+int ernie_hip_block_init_random(ernie_hip_ctx* ctx, int index, int dim, int ffn, int dtype, uint64_t seed,
+                                float std_dev)
+{
+    if (!ctx) return ERNIE_ERROR;
+    int rc = check_block_dims(ctx, dim, ffn, dtype);
+    if (rc) return rc;
+    BlockWeights* slot = block_slot(ctx, index);
+    if (!slot) return fail(ctx, ERNIE_ERROR, "block index out of range");
+    free_block(*slot);
+    BlockWeights bw;
+    rc = alloc_block(ctx, bw, dim, ffn, dtype);
+    if (rc) return rc;
+    const uint64_t stride = 1ull << 40;  // independent sub-stream per tensor
+    hipStream_t s = ctx->stream;
+    struct Item { void* p; int dt; size_t n; float mean; };
+    const Item items[] = {
+        {bw.norm1.ptr, ERNIE_DTYPE_FP32, (size_t)dim, 1.f}, {bw.wqkv.ptr, dtype, 3 * (size_t)dim * dim, 0.f},
+        {bw.norm_q.ptr, ERNIE_DTYPE_FP32, kHeadDim, 1.f},   {bw.norm_k.ptr, ERNIE_DTYPE_FP32, kHeadDim, 1.f},
+        {bw.wo.ptr, dtype, (size_t)dim * dim, 0.f}, {bw.norm2.ptr, ERNIE_DTYPE_FP32, (size_t)dim, 1.f},
+        {bw.w_ug.ptr, dtype, 2 * (size_t)ffn * dim, 0.f}, {bw.w_down.ptr, dtype, (size_t)dim * ffn, 0.f}};
+    uint64_t k = 0;
+    for (const Item& it : items) {
+        rc = kernel_status(ctx, fill_normal(it.p, it.dt, it.n, seed, (k++) * stride, it.mean, std_dev, s), "init");
+        if (rc) break;
+    }
+    if (!rc) rc = hip_status(ctx, hipStreamSynchronize(s), "init");
+    if (rc) {
+        free_block(bw);
+        return rc;
+    }
+    bw.loaded = true;
+    *slot = bw;
+    return ERNIE_OK;
+}
+
+int ernie_hip_block_release(ernie_hip_ctx* ctx, int index)
+{
+    if (!ctx || index < 0 || (size_t)index >= ctx->blocks.size()) return ERNIE_ERROR;
+    (void)hipStreamSynchronize(ctx->stream);
+    free_block(ctx->blocks[index]);
+    return ERNIE_OK;
+}
+
+int ernie_hip_block_count(const ernie_hip_ctx* ctx)
+{
+    if (!ctx) return 0;
+    int n = 0;
+    for (const auto& b : ctx->blocks) n += b.loaded ? 1 : 0;
+    return n;
+}
+
+int ernie_hip_block_forward(ernie_hip_ctx* ctx, int index, const float* x, float* out, const float* mods,
+                            const float* cos_t, const float* sin_t, const float* mask, int valid_keys, int S)
+{
+    if (!ctx) return ERNIE_ERROR;
+    int rc = check_block_call(ctx, index, S, x, out, mods, cos_t, sin_t, valid_keys);
+    if (rc) return rc;
+    return block_forward(ctx, ctx->blocks[index], x, out, mods, cos_t, sin_t, mask, valid_keys, S);
+}
+
+int ernie_hip_block_sequence(ernie_hip_ctx* ctx, const int* blocks, int count, const float* x, float* out,
+                             const float* mods, const float* cos_t, const float* sin_t, const float* mask,
+                             int valid_keys, int S, double* seconds)
+{
+    if (!ctx || !blocks) return ERNIE_ERROR;
+    if (count < 1 || count > 36) return fail(ctx, ERNIE_ERROR, "Expected 1..36 blocks");
+    for (int i = 0; i < count; ++i) {
+        int rc = check_block_call(ctx, blocks[i], S, x, out, mods, cos_t, sin_t, valid_keys);
+        if (rc) return rc;
+        if (ctx->blocks[blocks[i]].dim != ctx->blocks[blocks[0]].dim)
+            return fail(ctx, ERNIE_ERROR, "blocks differ in width");
+    }
+    // One event before each block and one after the last; a single wait at the end.
+    std::vector<hipEvent_t> ev;
+    if (seconds) {
+        ev.resize(count + 1, nullptr);
+        for (auto& e : ev)
+            if (hipEventCreate(&e) != hipSuccess) {
+                for (auto& f : ev)
+                    if (f) (void)hipEventDestroy(f);
+                return fail(ctx, ERNIE_ERROR, "event create");
+            }
+    }
+    int rc = ERNIE_OK;
+    for (int i = 0; i < count && !rc; ++i) {
+        if (seconds) (void)hipEventRecord(ev[i], ctx->stream);
+        rc = block_forward(ctx, ctx->blocks[blocks[i]], i == 0 ? x : out, out, mods, cos_t, sin_t, mask, valid_keys, S);
+    }
+    if (seconds) {
+        if (!rc) {
+            (void)hipEventRecord(ev[count], ctx->stream);
+            rc = hip_status(ctx, hipEventSynchronize(ev[count]), "block timing");
+        }
+        for (int i = 0; i < count && !rc; ++i) {
+            float ms = 0.f;
+            (void)hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
+            seconds[i] = ms * 1e-3;
+        }
+        for (auto& e : ev) (void)hipEventDestroy(e);
+    }
+    return rc;
+}
+
+// ---- heads --------------------------------------------------------------------------------
+int ernie_hip_heads_upload(ernie_hip_ctx* ctx, const ernie_heads_host_weights* w, int dim, int latent_ch, int text_dim,
+                           int dtype)
+{
+    if (!ctx || !w) return ERNIE_ERROR;
+    if (!valid_dtype(dtype) || dim < 128 || dim % 128 || latent_ch < 1 || text_dim < 1)
+        return fail(ctx, ERNIE_ERROR, "invalid head dimensions");
+    if (latent_ch % 32 || text_dim % 32) return fail(ctx, ERNIE_ERROR, "head widths must be multiples of 32");
+    free_heads(ctx->heads);
+    HeadWeights& h = ctx->heads;
+    const size_t e = esize(dtype), D = dim;
+    int rc = 0;
+    auto mat = [&](DeviceBuffer& b, const float* src, size_t n, const char* what) {
+        if (rc) return;
+        if (!src) { rc = fail(ctx, ERNIE_ERROR, std::string("null ") + what); return; }
+        rc = dev_alloc(ctx, b, n * e, what);
+        if (!rc) rc = upload_convert(ctx, b.ptr, 0, dtype, src, n, what);
+    };
+    auto vec = [&](DeviceBuffer& b, const float* src, size_t n, const char* what) {
+        if (rc) return;
+        if (!src) { rc = fail(ctx, ERNIE_ERROR, std::string("null ") + what); return; }
+        rc = upload_f32(ctx, b, src, n, what);
+    };
+    mat(h.x_w, w->x_w, D * latent_ch, "x_w");
+    vec(h.x_b, w->x_b, D, "x_b");
+    mat(h.text_w, w->text_w, D * text_dim, "text_w");
+    mat(h.t1_w, w->t1_w, D * D, "t1_w");
+    vec(h.t1_b, w->t1_b, D, "t1_b");
+    mat(h.t2_w, w->t2_w, D * D, "t2_w");
+    vec(h.t2_b, w->t2_b, D, "t2_b");
+    mat(h.mod_w, w->mod_w, 6 * D * D, "mod_w");
+    vec(h.mod_b, w->mod_b, 6 * D, "mod_b");
+    mat(h.out_mod_w, w->out_mod_w, 2 * D * D, "out_mod_w");
+    vec(h.out_mod_b, w->out_mod_b, 2 * D, "out_mod_b");
+    mat(h.proj_w, w->proj_w, (size_t)latent_ch * D, "proj_w");
+    vec(h.proj_b, w->proj_b, latent_ch, "proj_b");
+    if (!rc) rc = hip_status(ctx, hipStreamSynchronize(ctx->stream), "heads upload");
+    if (rc) {
+        free_heads(h);
+        return rc;
+    }
+    h.dim = dim; h.latent_ch = latent_ch; h.text_dim = text_dim; h.dtype = dtype; h.loaded = true;
+    return ERNIE_OK;
+}
+
+int ernie_hip_heads_init_random(ernie_hip_ctx* ctx, int dim, int latent_ch, int text_dim, int dtype, uint64_t seed,
+                                float std_dev)
+{
+    if (!ctx) return ERNIE_ERROR;
+    if (!valid_dtype(dtype) || dim < 128 || dim % 128 || latent_ch < 32 || latent_ch % 32 || text_dim < 32 ||
+        text_dim % 32)
+        return fail(ctx, ERNIE_ERROR, "invalid head dimensions");
+    free_heads(ctx->heads);
+    HeadWeights& h = ctx->heads;
+    const size_t D = dim;
+    struct Item { DeviceBuffer* b; bool matrix; size_t n; };
+    const Item items[] = {{&h.x_w, true, D * latent_ch}, {&h.x_b, false, D}, {&h.text_w, true, D * text_dim},
+                          {&h.t1_w, true, D * D}, {&h.t1_b, false, D}, {&h.t2_w, true, D * D}, {&h.t2_b, false, D},
+                          {&h.mod_w, true, 6 * D * D}, {&h.mod_b, false, 6 * D}, {&h.out_mod_w, true, 2 * D * D},
+                          {&h.out_mod_b, false, 2 * D}, {&h.proj_w, true, (size_t)latent_ch * D},
+                          {&h.proj_b, false, (size_t)latent_ch}};
+    int rc = 0;
+    uint64_t k = 0;
+    for (const Item& it : items) {
+        const int dt = it.matrix ? dtype : ERNIE_DTYPE_FP32;
+        rc = dev_alloc(ctx, *it.b, it.n * esize(dt), "heads");
+        if (!rc) rc = kernel_status(ctx, fill_normal(it.b->ptr, dt, it.n, seed, (k++) << 40, 0.f, std_dev, ctx->stream), "heads init");
+        if (rc) break;
+    }
+    if (!rc) rc = hip_status(ctx, hipStreamSynchronize(ctx->stream), "heads init");
+    if (rc) {
+        free_heads(h);
+        return rc;
+    }
+    h.dim = dim; h.latent_ch = latent_ch; h.text_dim = text_dim; h.dtype = dtype; h.loaded = true;
+    return ERNIE_OK;
+}
+
+int ernie_hip_input_head(ernie_hip_ctx* ctx, const float* latent, int hw, const float* text, int text_tokens,
+                         const float* time_features, float* x, float* c, float* mods)
+{
+    if (!ctx) return ERNIE_ERROR;
+    if (!ctx->heads.loaded) return fail(ctx, ERNIE_ERROR, "heads are not loaded");
+    if (!latent || !time_features || !x || !c || !mods || hw < 1 || text_tokens < 0 || (text_tokens && !text))
+        return fail(ctx, ERNIE_ERROR, "invalid input head arguments");
+    return input_head(ctx, latent, hw, text, text_tokens, time_features, x, c, mods);
+}
+
+int ernie_hip_output_head(ernie_hip_ctx* ctx, const float* x, int S, int hw, const float* c, float* prediction)
+{
+    if (!ctx) return ERNIE_ERROR;
+    if (!ctx->heads.loaded) return fail(ctx, ERNIE_ERROR, "heads are not loaded");
+    if (!x || !c || !prediction || hw < 1 || hw > S) return fail(ctx, ERNIE_ERROR, "invalid output head arguments");
+    return output_head(ctx, x, hw, c, prediction);
+}
+
+int ernie_hip_dit_forward(ernie_hip_ctx* ctx, const float* latent, int hw, const float* text, int text_tokens,
+                          const float* time_features, const float* cos_t, const float* sin_t, const float* mask,
+                          int valid_keys, const int* blocks, int count, float* prediction)
+{
+    if (!ctx) return ERNIE_ERROR;
+    if (!ctx->heads.loaded) return fail(ctx, ERNIE_ERROR, "heads are not loaded");
+    const int D = ctx->heads.dim, S = hw + text_tokens;
+    if (!blocks || count < 1 || count > 36) return fail(ctx, ERNIE_ERROR, "Expected 1..36 blocks");
+    for (int i = 0; i < count; ++i) {
+        int rc = check_block_call(ctx, blocks[i], S, latent, prediction, prediction, cos_t, sin_t, valid_keys);
+        if (rc) return rc;
+        if (ctx->blocks[blocks[i]].dim != D) return fail(ctx, ERNIE_ERROR, "block and head widths differ");
+    }
+    // x [S][D], c [D], mods [6][D], all FP32, in a context-owned buffer.
+    const size_t bytes = ((size_t)S * D + 7 * (size_t)D) * 4;
+    int rc = dev_alloc(ctx, ctx->dit_act, bytes, "dit activations");
+    if (rc) return rc;
+    float* x = static_cast<float*>(ctx->dit_act.ptr);
+    float* c = x + (size_t)S * D;
+    float* mods = c + D;
+    rc = input_head(ctx, latent, hw, text, text_tokens, time_features, x, c, mods);
+    for (int i = 0; i < count && !rc; ++i)
+        rc = block_forward(ctx, ctx->blocks[blocks[i]], x, x, mods, cos_t, sin_t, mask, valid_keys, S);
+    if (!rc) rc = output_head(ctx, x, hw, c, prediction);
+    return rc;
+}
+
+// ---- profiling ------------------------------------------------------------------------------
+int ernie_hip_profile_enable(ernie_hip_ctx* ctx, int enable)
+{
+    if (!ctx) return ERNIE_ERROR;
+    if (!enable) {
+        int rc = collect(ctx);
+        ctx->profiling = false;
+        return rc;
+    }
+    ctx->profiling = true;
+    return ERNIE_OK;
+}
+
+int ernie_hip_profile_collect(ernie_hip_ctx* ctx) { return ctx ? collect(ctx) : ERNIE_ERROR; }
+
+int ernie_hip_profile_reset(ernie_hip_ctx* ctx)
+{
+    if (!ctx) return ERNIE_ERROR;
+    int rc = collect(ctx);
+    for (int i = 0; i < ERNIE_PROFILE_CLASSES; ++i) {
+        ctx->launches[i] = 0;
+        ctx->ms[i] = ctx->flop[i] = ctx->bytes[i] = 0;
+    }
+    return rc;
+}
+
+int ernie_hip_profile_query(const ernie_hip_ctx* ctx, int cls, long* launches, double* ms, double* flop, double* bytes)
+{
+    if (!ctx || cls < 0 || cls >= ERNIE_PROFILE_CLASSES) return ERNIE_ERROR;
+    if (launches) *launches = ctx->launches[cls];
+    if (ms) *ms = ctx->ms[cls];
+    if (flop) *flop = ctx->flop[cls];
+    if (bytes) *bytes = ctx->bytes[cls];
+    return ERNIE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,79 @@
+// SPDX-License-Identifier: MIT
+// Host-side launch interface of the HIP kernels. Every launcher validates the
+// shapes its kernel assumes and returns 0 or a negative status (-1 invalid
+// argument, or a hipError_t negated) without launching when they do not hold.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace ehip {
+
+// ---- GEMM: C[M,N] = A[M,K] * W[N,K]^T with a fused epilogue -----------------
+enum Epilogue : int {
+    EPI_STORE = 0,       // C = acc (+ bias[n]), C dtype = c_dtype
+    EPI_GATE_RESID = 1,  // C(f32) = resid(f32) + gate[n] * acc
+    EPI_GEGLU = 2,       // W rows interleaved in 32-row [up | gate] pairs; C[m][n/2] = up * gelu(gate)
+};
+
+struct GemmArgs {
+    const void* A = nullptr;  // [M][lda], dtype
+    long lda = 0;
+    const void* W = nullptr;  // [N][ldw], dtype
+    long ldw = 0;
+    int M = 0, N = 0, K = 0;
+    int dtype = 0;            // operand dtype (F32 / F16 / BF16)
+    int epilogue = EPI_STORE;
+    void* C = nullptr;
+    long ldc = 0;
+    int c_dtype = 0;
+    const float* bias = nullptr;   // [N] (EPI_STORE only)
+    const float* resid = nullptr;  // [M][ld_resid] f32 (EPI_GATE_RESID; may alias C)
+    long ld_resid = 0;
+    const float* gate = nullptr;   // [N]
+};
+int gemm(const GemmArgs& a, hipStream_t stream);
+
+// ---- flash SDPA ---------------------------------------------------------------
+struct SdpaArgs {
+    const void* q = nullptr; const void* k = nullptr; const void* v = nullptr; void* o = nullptr;
+    int dtype = 0;
+    int heads = 0, kv_heads = 0, sq = 0, sk = 0, d = 0;
+    long q_hs = 0, q_rs = 0, k_hs = 0, k_rs = 0, v_hs = 0, v_rs = 0, o_hs = 0, o_rs = 0;  // strides (elements)
+    const float* mask = nullptr;  // additive [mask_heads][mask_rows][sk]; mask_rows 1 or sq
+    int mask_heads = 1, mask_rows = 1;
+    int valid_keys = 0;           // keys >= valid_keys are excluded (0 = sk)
+    float scale = 0.f;
+};
+int sdpa(const SdpaArgs& a, hipStream_t stream);
+
+// ---- bandwidth-bound kernels ------------------------------------------------------
+// out = RMSNorm(x) * gamma [* (1 + scale) + shift]; FP32 statistics.
+int rmsnorm_modulate(const void* x, int x_dtype, const float* gamma, const float* shift, const float* scale,
+                     int rows, int width, float eps, void* out, int out_dtype, hipStream_t s);
+// out = LayerNorm(x) (non-affine) * (1 + scale) + shift.
+int layernorm_modulate(const float* x, const float* shift, const float* scale, int rows, int width, float eps,
+                       void* out, int out_dtype, hipStream_t s);
+// Per-head RMSNorm over 128 values followed by ERNIE rotary, in place, for
+// `nheads` heads of `rows` tokens at x + t*row_stride + h*128.
+int qk_norm_rope(void* x, int dtype, int rows, int nheads, long row_stride, const float* gamma,
+                 const float* cos_t, const float* sin_t, hipStream_t s);
+int gelu_inplace(void* x, int dtype, size_t n, hipStream_t s);
+int residual_add(const void* a, int a_dtype, const void* b, int b_dtype, float* out, size_t n, hipStream_t s);
+int euler_step(const float* x, const float* v, float delta, size_t n, float* out, hipStream_t s);
+int finite_flags(const float* x, size_t n, int* flag, hipStream_t s);
+int convert(const void* in, int in_dtype, void* out, int out_dtype, size_t n, hipStream_t s);
+int fill_normal(void* out, int dtype, size_t n, uint64_t seed, uint64_t offset, float mean, float std_dev,
+                hipStream_t s);
+// y[n] = act(x)[k] . W[n][k] + b[n] in FP32 accumulation (matrix-vector).
+int gemv(const void* W, int w_dtype, const float* b, const float* x, int N, int K, int silu_input, float* y,
+         hipStream_t s);
+// latent [ch][hw] f32 -> tokens [hw][ch] in dtype.
+int transpose_to_tokens(const float* latent, int ch, int hw, void* out, int dtype, hipStream_t s);
+// proj [hw][ch] (f32, bias applied) -> pred [ch][hw] f32.
+int tokens_to_latent(const float* proj, int hw, int ch, float* pred, hipStream_t s);
+
+// Host FP32 up or gate matrix [rows][cols] -> its rows of the interleaved W_ug (parity 0 = up).
+int interleave_up_gate(const float* in, void* out, int dt, int rows, int cols, int parity, hipStream_t s);
+
+}  // namespace ehip

@@ -1,0 +1,411 @@
+"""ctypes binding of the ernie_hip C ABI (include/ernie_hip.h) and the C entry
+points of the C++ facade (include/ernie.h).
+
+Device buffers are torch tensors on the HIP device (torch is only the
+allocator/stream plumbing here); every computation runs in the in-tree gfx950
+library. Loading fails loudly when the library has not been built -- there is
+no other implementation behind this module.
+"""
+import ctypes
+import re
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent.parent
+ROOT = PKG.parent
+LIB_DIR = PKG / "lib"
+HIP_LIB = LIB_DIR / "libernie_hip.so"
+FACADE_LIB = LIB_DIR / "libernie.so"
+HEADERS = [ROOT / "include" / "ernie_hip.h", ROOT / "include" / "ernie.h"]
+
+FP32, FP16, BF16 = 0, 1, 2
+OK, ERROR, ALLOCATION_FAILED, INVALID_REQUEST = 0, -1, -100, -22
+PROFILE_CLASSES = ("gemm_qkv", "sdpa", "gemm_out", "gemm_up_gate", "gemm_down", "rmsnorm_modulate", "qk_norm_rope",
+                   "heads")
+
+_hip = None
+_facade = None
+
+c_int, c_long, c_float, c_double, c_size_t, c_u64, c_vp = (ctypes.c_int, ctypes.c_long, ctypes.c_float,
+                                                          ctypes.c_double, ctypes.c_size_t, ctypes.c_uint64,
+                                                          ctypes.c_void_p)
+
+
+class ErnieError(RuntimeError):
+    def __init__(self, status, message):
+        super().__init__(f"status {status}: {message}")
+        self.status = status
+
+
+class ErnieAllocationError(ErnieError):
+    pass
+
+
+class ErnieInvalidRequest(ErnieError, ValueError):
+    pass
+
+
+def build():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("ernie_build", PKG / "build.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.build()
+
+
+def declared_functions():
+    """Every function name declared in the public headers."""
+    names = []
+    for h in HEADERS:
+        text = h.read_text()
+        names += re.findall(r"^[A-Za-z_][\w\s\*]*?\b(ernie_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def hip():
+    global _hip
+    if _hip is None:
+        if not HIP_LIB.exists():
+            raise RuntimeError(f"{HIP_LIB} is missing: run `python {PKG / 'build.py'}` first")
+        L = ctypes.CDLL(str(HIP_LIB), mode=ctypes.RTLD_GLOBAL)
+        sig = {
+            "ernie_hip_create": (c_int, [c_int, ctypes.POINTER(c_vp)]),
+            "ernie_hip_destroy": (None, [c_vp]),
+            "ernie_hip_last_error": (ctypes.c_char_p, [c_vp]),
+            "ernie_hip_set_stream": (c_int, [c_vp, c_vp]),
+            "ernie_hip_get_stream": (c_vp, [c_vp]),
+            "ernie_hip_own_stream": (c_vp, [c_vp]),
+            "ernie_hip_synchronize": (c_int, [c_vp]),
+            "ernie_hip_malloc": (c_int, [c_vp, c_size_t, ctypes.POINTER(c_vp)]),
+            "ernie_hip_free": (c_int, [c_vp, c_vp]),
+            "ernie_hip_memcpy_h2d": (c_int, [c_vp, c_vp, c_vp, c_size_t]),
+            "ernie_hip_memcpy_d2h": (c_int, [c_vp, c_vp, c_vp, c_size_t]),
+            "ernie_hip_rmsnorm": (c_int, [c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_int, c_int, c_float, c_vp, c_int]),
+            "ernie_hip_layernorm_modulate": (c_int, [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_float, c_vp, c_int]),
+            "ernie_hip_gelu": (c_int, [c_vp, c_vp, c_int, c_size_t]),
+            "ernie_hip_residual_add": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_vp, c_size_t]),
+            "ernie_hip_gemm": (c_int, [c_vp, c_vp, c_long, c_vp, c_long, c_vp, c_vp, c_long, c_int, c_int, c_int,
+                                       c_int, c_int]),
+            "ernie_hip_sdpa": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int] +
+                               [c_long] * 8 + [c_vp, c_int, c_int, c_int, c_float]),
+            "ernie_hip_set_attention_query_rows": (c_int, [c_vp, c_int]),
+            "ernie_hip_attention_internal_submissions": (c_u64, [c_vp]),
+            "ernie_hip_qk_norm_rope": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_long, c_vp, c_vp, c_vp]),
+            "ernie_hip_euler_step": (c_int, [c_vp, c_vp, c_vp, c_float, c_size_t, c_vp]),
+            "ernie_hip_finite": (c_int, [c_vp, c_vp, c_size_t, ctypes.POINTER(c_int)]),
+            "ernie_hip_fill_normal": (c_int, [c_vp, c_vp, c_int, c_size_t, c_u64, c_u64, c_float, c_float]),
+            "ernie_hip_convert": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_size_t]),
+            "ernie_hip_block_upload": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int]),
+            "ernie_hip_block_init_random": (c_int, [c_vp, c_int, c_int, c_int, c_int, c_u64, c_float]),
+            "ernie_hip_block_release": (c_int, [c_vp, c_int]),
+            "ernie_hip_block_count": (c_int, [c_vp]),
+            "ernie_hip_block_forward": (c_int, [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int]),
+            "ernie_hip_block_sequence": (c_int, [c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int,
+                                                 c_vp]),
+            "ernie_hip_heads_upload": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int]),
+            "ernie_hip_heads_init_random": (c_int, [c_vp, c_int, c_int, c_int, c_int, c_u64, c_float]),
+            "ernie_hip_input_head": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_vp]),
+            "ernie_hip_output_head": (c_int, [c_vp, c_vp, c_int, c_int, c_vp, c_vp]),
+            "ernie_hip_dit_forward": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_int, c_vp,
+                                              c_int, c_vp]),
+            "ernie_hip_profile_enable": (c_int, [c_vp, c_int]),
+            "ernie_hip_profile_collect": (c_int, [c_vp]),
+            "ernie_hip_profile_reset": (c_int, [c_vp]),
+            "ernie_hip_profile_query": (c_int, [c_vp, c_int, ctypes.POINTER(c_long), ctypes.POINTER(c_double),
+                                                ctypes.POINTER(c_double), ctypes.POINTER(c_double)]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _hip = L
+    return _hip
+
+
+def facade():
+    global _facade
+    if _facade is None:
+        hip()
+        if not FACADE_LIB.exists():
+            raise RuntimeError(f"{FACADE_LIB} is missing: run `python {PKG / 'build.py'}` first")
+        L = ctypes.CDLL(str(FACADE_LIB))
+        cp = ctypes.c_char_p
+        sig = {
+            "ernie_device_create": (c_int, [c_int, ctypes.POINTER(c_vp)]),
+            "ernie_device_destroy": (None, [c_vp]),
+            "ernie_device_ctx": (c_vp, [c_vp]),
+            "ernie_timestep_features": (c_int, [c_float, c_vp, cp, c_size_t]),
+            "ernie_flow_schedule_turbo": (c_int, [c_int, c_vp, c_vp, cp, c_size_t]),
+            "ernie_rope_frequencies": (c_int, [c_vp]),
+            "ernie_dit_constants": (c_int, [c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp, c_vp, cp, c_size_t]),
+            "ernie_run_block_sequence": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_int,
+                                                 c_int, c_vp, c_vp, cp, c_size_t]),
+            "ernie_denoise": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_int,
+                                      c_int, c_int, c_int, c_vp, c_vp, cp, c_size_t]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _facade = L
+    return _facade
+
+
+def _raise(status, message):
+    msg = message.decode() if isinstance(message, bytes) else str(message)
+    if status == ALLOCATION_FAILED:
+        raise ErnieAllocationError(status, msg)
+    if status == INVALID_REQUEST:
+        raise ErnieInvalidRequest(status, msg)
+    raise ErnieError(status, msg)
+
+
+def ptr(t):
+    """Device (or host numpy) pointer of a tensor / array, None passes through."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    if hasattr(t, "data_ptr"):
+        return t.data_ptr()
+    return t.ctypes.data
+
+
+# ---- host helpers of the facade (no device needed) -------------------------------
+def _err():
+    return ctypes.create_string_buffer(512)
+
+
+def timestep_features(t):
+    import numpy as np
+    out = np.empty(4096, np.float32)
+    e = _err()
+    rc = facade().ernie_timestep_features(float(t), out.ctypes.data, e, 512)
+    if rc:
+        _raise(rc, e.value)
+    return out
+
+
+def flow_schedule_turbo(steps=8):
+    import numpy as np
+    sig = np.empty(steps + 1 if steps > 0 else 1, np.float32)
+    ts = np.empty(max(steps, 1), np.float32)
+    e = _err()
+    rc = facade().ernie_flow_schedule_turbo(int(steps), sig.ctypes.data, ts.ctypes.data, e, 512)
+    if rc:
+        _raise(rc, e.value)
+    return sig, ts[:steps]
+
+
+def rope_frequencies():
+    import numpy as np
+    out = np.empty(64, np.float32)
+    facade().ernie_rope_frequencies(out.ctypes.data)
+    return out
+
+
+def dit_constants(freqs, w, h, valid, text):
+    import numpy as np
+    freqs = np.ascontiguousarray(freqs, np.float32)
+    S = w * h + text
+    cos = np.empty((max(S, 1), 128), np.float32)
+    sin = np.empty((max(S, 1), 128), np.float32)
+    mask = np.empty(max(S, 1), np.float32)
+    e = _err()
+    rc = facade().ernie_dit_constants(freqs.ctypes.data, w, h, valid, text, cos.ctypes.data, sin.ctypes.data,
+                                      mask.ctypes.data, e, 512)
+    if rc < 0:
+        _raise(rc, e.value)
+    return cos, sin, mask, rc
+
+
+class Context:
+    """One ernie_hip context bound to torch's current stream on `device`."""
+
+    def __init__(self, device=0, use_torch_stream=True):
+        L = hip()
+        p = c_vp()
+        rc = L.ernie_hip_create(device, ctypes.byref(p))
+        if rc:
+            raise ErnieError(rc, f"ernie_hip_create({device}) failed: no usable HIP device")
+        self.ctx = p.value
+        self.L = L
+        if use_torch_stream:
+            import torch
+            L.ernie_hip_set_stream(self.ctx, c_vp(torch.cuda.current_stream().cuda_stream))
+
+    def close(self):
+        if self.ctx:
+            self.L.ernie_hip_destroy(self.ctx)
+            self.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def check(self, rc):
+        if rc:
+            _raise(rc, self.L.ernie_hip_last_error(self.ctx) or b"")
+        return rc
+
+    def call(self, name, *args):
+        return self.check(getattr(self.L, "ernie_hip_" + name)(self.ctx, *args))
+
+    def synchronize(self):
+        self.call("synchronize")
+
+    # ---- ops -------------------------------------------------------------
+    def rmsnorm(self, x, x_dtype, gamma, rows, width, out, out_dtype, shift=None, scale=None, eps=1e-6):
+        self.call("rmsnorm", ptr(x), x_dtype, ptr(gamma), ptr(shift), ptr(scale), rows, width, eps, ptr(out),
+                  out_dtype)
+
+    def layernorm_modulate(self, x, shift, scale, rows, width, out, out_dtype, eps=1e-6):
+        self.call("layernorm_modulate", ptr(x), ptr(shift), ptr(scale), rows, width, eps, ptr(out), out_dtype)
+
+    def gelu(self, x, dtype, count):
+        self.call("gelu", ptr(x), dtype, count)
+
+    def residual_add(self, a, adt, b, bdt, out, count):
+        self.call("residual_add", ptr(a), adt, ptr(b), bdt, ptr(out), count)
+
+    def gemm(self, a, lda, w, ldw, c, ldc, m, n, k, dtype, out_dtype, bias=None):
+        self.call("gemm", ptr(a), lda, ptr(w), ldw, ptr(bias), ptr(c), ldc, m, n, k, dtype, out_dtype)
+
+    def sdpa(self, q, k, v, out, dtype, heads, kv_heads, sq, sk, d, strides, mask=None, mask_heads=1, mask_rows=1,
+             valid_keys=0, scale=0.0):
+        self.call("sdpa", ptr(q), ptr(k), ptr(v), ptr(out), dtype, heads, kv_heads, sq, sk, d, *strides, ptr(mask),
+                  mask_heads, mask_rows, valid_keys, scale)
+
+    def qk_norm_rope(self, x, dtype, rows, heads, row_stride, gamma, cos, sin):
+        self.call("qk_norm_rope", ptr(x), dtype, rows, heads, row_stride, ptr(gamma), ptr(cos), ptr(sin))
+
+    def euler_step(self, x, v, delta, count, out):
+        self.call("euler_step", ptr(x), ptr(v), delta, count, ptr(out))
+
+    def finite(self, x, count):
+        f = c_int()
+        self.call("finite", ptr(x), count, ctypes.byref(f))
+        return bool(f.value)
+
+    def fill_normal(self, out, dtype, count, seed, offset=0, mean=0.0, std=1.0):
+        self.call("fill_normal", ptr(out), dtype, count, seed, offset, mean, std)
+
+    # ---- blocks / heads -----------------------------------------------------
+    def block_upload(self, index, weights, dim, ffn, dtype):
+        """weights: dict of FP32 numpy arrays keyed like ernie_block_host_weights."""
+        import numpy as np
+        fields = ("norm1", "wq", "wk", "wv", "norm_q", "norm_k", "wo", "norm2", "w_up", "w_gate", "w_down")
+        keep = [np.ascontiguousarray(weights[f], np.float32) for f in fields]
+        arr = (c_vp * len(fields))(*[a.ctypes.data for a in keep])
+        self.call("block_upload", index, ctypes.cast(arr, c_vp), dim, ffn, dtype)
+
+    def block_init_random(self, index, dim, ffn, dtype, seed, std=0.02):
+        self.call("block_init_random", index, dim, ffn, dtype, seed, std)
+
+    def block_forward(self, index, x, out, mods, cos, sin, S, mask=None, valid_keys=0):
+        self.call("block_forward", index, ptr(x), ptr(out), ptr(mods), ptr(cos), ptr(sin), ptr(mask), valid_keys, S)
+
+    def block_sequence(self, blocks, x, out, mods, cos, sin, S, mask=None, valid_keys=0, timing=False):
+        import numpy as np
+        ids = (c_int * len(blocks))(*blocks)
+        secs = np.zeros(len(blocks), np.float64) if timing else None
+        self.call("block_sequence", ctypes.cast(ids, c_vp), len(blocks), ptr(x), ptr(out), ptr(mods), ptr(cos),
+                  ptr(sin), ptr(mask), valid_keys, S, secs.ctypes.data if timing else None)
+        return secs
+
+    def heads_upload(self, weights, dim, latent_ch, text_dim, dtype):
+        import numpy as np
+        fields = ("x_w", "x_b", "text_w", "t1_w", "t1_b", "t2_w", "t2_b", "mod_w", "mod_b", "out_mod_w",
+                  "out_mod_b", "proj_w", "proj_b")
+        keep = [np.ascontiguousarray(weights[f], np.float32) for f in fields]
+        arr = (c_vp * len(fields))(*[a.ctypes.data for a in keep])
+        self.call("heads_upload", ctypes.cast(arr, c_vp), dim, latent_ch, text_dim, dtype)
+
+    def heads_init_random(self, dim, latent_ch, text_dim, dtype, seed, std=0.02):
+        self.call("heads_init_random", dim, latent_ch, text_dim, dtype, seed, std)
+
+    def input_head(self, latent, hw, text, text_tokens, features, x, c, mods):
+        self.call("input_head", ptr(latent), hw, ptr(text), text_tokens, ptr(features), ptr(x), ptr(c), ptr(mods))
+
+    def output_head(self, x, S, hw, c, pred):
+        self.call("output_head", ptr(x), S, hw, ptr(c), ptr(pred))
+
+    def dit_forward(self, latent, hw, text, text_tokens, features, cos, sin, blocks, pred, mask=None, valid_keys=0):
+        ids = (c_int * len(blocks))(*blocks)
+        self.call("dit_forward", ptr(latent), hw, ptr(text), text_tokens, ptr(features), ptr(cos), ptr(sin),
+                  ptr(mask), valid_keys, ctypes.cast(ids, c_vp), len(blocks), ptr(pred))
+
+    # ---- profiling -----------------------------------------------------------
+    def profile(self, enable):
+        self.call("profile_enable", 1 if enable else 0)
+
+    def profile_reset(self):
+        self.call("profile_reset")
+
+    def profile_query(self):
+        self.call("profile_collect")
+        out = {}
+        for i, name in enumerate(PROFILE_CLASSES):
+            n, ms, fl, by = c_long(), c_double(), c_double(), c_double()
+            self.call("profile_query", i, ctypes.byref(n), ctypes.byref(ms), ctypes.byref(fl), ctypes.byref(by))
+            out[name] = {"launches": n.value, "ms": ms.value, "flop": fl.value, "bytes": by.value}
+        return out
+
+
+class Facade:
+    """ernie::Device plus the C entry points of the C++ facade."""
+
+    def __init__(self, device=0):
+        L = facade()
+        p = c_vp()
+        rc = L.ernie_device_create(device, ctypes.byref(p))
+        if rc:
+            raise ErnieError(rc, "ernie_device_create failed: no usable HIP device")
+        self.dev = p.value
+        self.L = L
+        self.hip = Context.__new__(Context)
+        self.hip.ctx = L.ernie_device_ctx(self.dev)
+        self.hip.L = hip()
+        import torch
+        hip().ernie_hip_set_stream(self.hip.ctx, c_vp(torch.cuda.current_stream().cuda_stream))
+
+    def close(self):
+        if self.dev:
+            self.hip.ctx = None
+            self.L.ernie_device_destroy(self.dev)
+            self.dev = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def run_block_sequence(self, blocks, x, S, dim, mods, cos, sin, out, mask=None, valid_prefix=0, dtype=FP32):
+        import numpy as np
+        ids = (c_int * len(blocks))(*blocks)
+        mp = (c_vp * 6)(*[ptr(m) for m in mods])
+        secs = np.zeros(max(len(blocks), 1), np.float64)
+        e = _err()
+        rc = self.L.ernie_run_block_sequence(self.dev, ctypes.cast(ids, c_vp), len(blocks), ptr(x), S, dim,
+                                             ctypes.cast(mp, c_vp), ptr(cos), ptr(sin), ptr(mask), valid_prefix,
+                                             dtype, ptr(out), secs.ctypes.data, e, 512)
+        if rc:
+            _raise(rc, e.value)
+        return secs[:len(blocks)]
+
+    def denoise(self, blocks, latent, height, width, text, text_tokens, cos, sin, mask, valid_prefix, steps,
+                start_step=0, dtype=FP16):
+        import numpy as np
+        ids = (c_int * max(len(blocks), 1))(*blocks)
+        n = max(steps, 1)
+        secs = np.zeros(n, np.float64)
+        ts = np.zeros(n, np.float32)
+        e = _err()
+        rc = self.L.ernie_denoise(self.dev, ctypes.cast(ids, c_vp), len(blocks), ptr(latent), height, width,
+                                  ptr(text), text_tokens, ptr(cos), ptr(sin), ptr(mask), valid_prefix, steps,
+                                  start_step, dtype, secs.ctypes.data, ts.ctypes.data, e, 512)
+        if rc:
+            _raise(rc, e.value)
+        return secs[:max(steps - start_step, 0)], ts[:max(steps - start_step, 0)]

@@ -1,0 +1,185 @@
+// SPDX-License-Identifier: MIT
+// C entry points over the C++ facade (declared in include/ernie.h).
+#include "ernie.h"
+
+#include <cstring>
+#include <exception>
+#include <stdexcept>
+
+#include "ernie/conditioning.h"
+#include "ernie/denoiser.h"
+
+struct ernie_device {
+    ernie::Device device;
+    explicit ernie_device(int index) : device(index) {}
+};
+
+namespace {
+
+void set_err(char* err, size_t len, const char* msg)
+{
+    if (!err || !len) return;
+    std::strncpy(err, msg, len - 1);
+    err[len - 1] = '\0';
+}
+
+template <class F>
+int guarded(char* err, size_t len, F&& body)
+{
+    try {
+        return body();
+    } catch (const ernie::GpuAllocationError& e) {
+        set_err(err, len, e.what());
+        return ERNIE_ALLOCATION_FAILED;
+    } catch (const std::invalid_argument& e) {
+        set_err(err, len, e.what());
+        return ERNIE_INVALID_REQUEST;
+    } catch (const std::out_of_range& e) {
+        set_err(err, len, e.what());
+        return ERNIE_INVALID_REQUEST;
+    } catch (const std::exception& e) {
+        set_err(err, len, e.what());
+        return ERNIE_ERROR;
+    }
+}
+
+// Non-owning device view of caller memory.
+ernie::DeviceMat wrap(const float* p, int w, int h = 1, int c = 1, int dims = 0)
+{
+    ernie::DeviceMat m;
+    m.data = const_cast<float*>(p);
+    m.w = w;
+    m.h = h;
+    m.c = c;
+    m.dims = dims ? dims : (c > 1 ? 3 : (h > 1 ? 2 : 1));
+    return m;
+}
+
+ernie::Option option_for(const ernie::Device& d, int dtype)
+{
+    ernie::Option o;
+    o.device = &d;
+    o.use_fp16_storage = dtype == ERNIE_DTYPE_FP16;
+    o.use_bf16_storage = dtype == ERNIE_DTYPE_BF16;
+    return o;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ernie_device_create(int index, ernie_device** out)
+{
+    if (!out) return ERNIE_INVALID_REQUEST;
+    *out = nullptr;
+    return guarded(nullptr, 0, [&] {
+        *out = new ernie_device(index);
+        return ERNIE_OK;
+    });
+}
+
+void ernie_device_destroy(ernie_device* device) { delete device; }
+
+ernie_hip_ctx* ernie_device_ctx(ernie_device* device) { return device ? device->device.ctx() : nullptr; }
+
+int ernie_timestep_features(float timestep, float* out, char* err, size_t errlen)
+{
+    return guarded(err, errlen, [&] {
+        const auto f = ernie::timestep_features(timestep);
+        std::memcpy(out, f.data(), f.size() * sizeof(float));
+        return ERNIE_OK;
+    });
+}
+
+int ernie_flow_schedule_turbo(int steps, float* sigmas, float* timesteps, char* err, size_t errlen)
+{
+    return guarded(err, errlen, [&] {
+        const auto s = ernie::FlowSchedule::turbo(steps);
+        std::memcpy(sigmas, s.sigmas.data(), s.sigmas.size() * sizeof(float));
+        std::memcpy(timesteps, s.timesteps.data(), s.timesteps.size() * sizeof(float));
+        return ERNIE_OK;
+    });
+}
+
+int ernie_rope_frequencies(float* out)
+{
+    const auto f = ernie::rope_frequencies();
+    std::memcpy(out, f.data(), f.size() * sizeof(float));
+    return ERNIE_OK;
+}
+
+int ernie_dit_constants(const float* frequencies, int width, int height, int valid_text, int text_bucket,
+                        float* cos_out, float* sin_out, float* mask_out, char* err, size_t errlen)
+{
+    return guarded(err, errlen, [&] {
+        const auto k = ernie::dit_constants(std::vector<float>(frequencies, frequencies + 64), width, height,
+                                            valid_text, text_bucket);
+        std::memcpy(cos_out, k.cos.data(), k.cos.size() * sizeof(float));
+        std::memcpy(sin_out, k.sin.data(), k.sin.size() * sizeof(float));
+        std::memcpy(mask_out, k.mask.data(), k.mask.size() * sizeof(float));
+        return k.valid_keys;
+    });
+}
+
+int ernie_run_block_sequence(ernie_device* device, const int* blocks, int count, const float* x, int S, int dim,
+                             const float* const* mods, const float* cos_t, const float* sin_t, const float* mask,
+                             int valid_prefix, int storage_dtype, float* out, double* compute_seconds, char* err,
+                             size_t errlen)
+{
+    return guarded(err, errlen, [&]() -> int {
+        if (!device || !blocks || !mods || count < 0) throw std::invalid_argument("null block sequence argument");
+        std::vector<ernie::BlockModel> models;
+        for (int i = 0; i < count; ++i) models.push_back({blocks[i]});
+        std::vector<ernie::DeviceMat> constants;
+        for (int i = 0; i < 6; ++i) constants.push_back(wrap(mods[i], dim));
+        constants.push_back(wrap(cos_t, 128, S));
+        constants.push_back(wrap(sin_t, 128, S));
+        ernie::DeviceMat m = mask ? wrap(mask, S) : ernie::DeviceMat{};
+        m.valid_prefix = valid_prefix;
+        constants.push_back(m);
+        ernie::BlockSequenceStats stats;
+        const auto& d = device->device;
+        const auto result = ernie::run_block_sequence(models, wrap(x, dim, S, 1, 2), constants,
+                                                      option_for(d, storage_dtype), ernie::WeightPolicy::Stream, stats);
+        ernie::check_status(ernie_hip_convert(d.ctx(), result.data, ERNIE_DTYPE_FP32, out, ERNIE_DTYPE_FP32,
+                                              result.total()),
+                            d.ctx(), "copy block output");
+        d.synchronize();
+        if (compute_seconds)
+            for (size_t i = 0; i < stats.compute_seconds.size(); ++i) compute_seconds[i] = stats.compute_seconds[i];
+        return ERNIE_OK;
+    });
+}
+
+int ernie_denoise(ernie_device* device, const int* blocks, int count, float* latent, int height, int width,
+                  const float* text, int text_tokens, const float* cos_t, const float* sin_t, const float* mask,
+                  int valid_prefix, int steps, int start_step, int storage_dtype, double* step_seconds,
+                  float* step_timesteps, char* err, size_t errlen)
+{
+    return guarded(err, errlen, [&]() -> int {
+        if (!device || !blocks || count < 0) throw std::invalid_argument("null denoise argument");
+        ernie::DenoiseModel model;
+        for (int i = 0; i < count; ++i) model.blocks.push_back({blocks[i]});
+        const int S = height * width + text_tokens;
+        ernie::DeviceMat m = mask ? wrap(mask, S) : ernie::DeviceMat{};
+        m.valid_prefix = valid_prefix;
+        const std::vector<ernie::DeviceMat> constants{
+            text_tokens ? wrap(text, 3072, text_tokens, 1, 2) : ernie::DeviceMat{}, wrap(cos_t, 128, S),
+            wrap(sin_t, 128, S), m};
+        std::vector<ernie::DenoiseStepStats> stats;
+        const auto& d = device->device;
+        const auto result = ernie::denoise(model, wrap(latent, width, height, 128, 3), constants, steps,
+                                           option_for(d, storage_dtype), stats, {}, start_step);
+        ernie::check_status(ernie_hip_convert(d.ctx(), result.data, ERNIE_DTYPE_FP32, latent, ERNIE_DTYPE_FP32,
+                                              result.total()),
+                            d.ctx(), "copy denoised latent");
+        d.synchronize();
+        for (size_t i = 0; i < stats.size(); ++i) {
+            if (step_seconds) step_seconds[i] = stats[i].elapsed_seconds;
+            if (step_timesteps) step_timesteps[i] = stats[i].timestep;
+        }
+        return ERNIE_OK;
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,65 @@
+/* SPDX-License-Identifier: MIT
+ *
+ * C entry points of the ernie C++ facade (libernie.so). They drive the same
+ * host code a C++ caller reaches through ernie/denoiser.h, ernie/dit.h and
+ * ernie/block_sequence.h, for bindings that cannot call C++ (ctypes, cgo...).
+ *
+ * Status: 0 ok, -1 runtime/device error, -100 GpuAllocationError,
+ * -22 std::invalid_argument / std::out_of_range (request rejected before any
+ * device work, like the reference's argument checks). `err` (nullable) receives
+ * the exception message.
+ */
+#ifndef ERNIE_H
+#define ERNIE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "ernie_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ERNIE_INVALID_REQUEST (-22)
+
+typedef struct ernie_device ernie_device;
+
+/* ernie::Device (the device context standing in for the Vulkan device). */
+int ernie_device_create(int index, ernie_device** out);
+void ernie_device_destroy(ernie_device* device);
+ernie_hip_ctx* ernie_device_ctx(ernie_device* device);
+
+/* timestep_features (src/denoiser.cpp:22-39) -> out[4096]. */
+int ernie_timestep_features(float timestep, float* out, char* err, size_t errlen);
+/* FlowSchedule::turbo (src/latent_ops.cpp:31-51): sigmas[steps+1], timesteps[steps]. */
+int ernie_flow_schedule_turbo(int steps, float* sigmas, float* timesteps, char* err, size_t errlen);
+/* rope frequency table (tools/prepare_pipeline.py:63) -> out[64]. */
+int ernie_rope_frequencies(float* out);
+/* dit_constants (src/conditioning.cpp:10-43) on the host: cos/sin [S][128], mask [S];
+ * returns the valid key count (> 0) or a negative status. */
+int ernie_dit_constants(const float* frequencies, int width, int height, int valid_text, int text_bucket,
+                        float* cos_out, float* sin_out, float* mask_out, char* err, size_t errlen);
+
+/* run_block_sequence (src/block_sequence.h:38-41): x [S][dim] device FP32,
+ * mods = six [dim] device vectors, cos/sin [S][128], mask [S] with valid_prefix
+ * hint (0 = none). out [S][dim] device FP32. compute_seconds (nullable) gets
+ * per-block device time. */
+int ernie_run_block_sequence(ernie_device* device, const int* blocks, int count, const float* x, int S, int dim,
+                             const float* const* mods, const float* cos_t, const float* sin_t, const float* mask,
+                             int valid_prefix, int storage_dtype, float* out, double* compute_seconds, char* err,
+                             size_t errlen);
+
+/* denoise (src/denoiser.h:30-33): latent [128][height][width] device FP32 is
+ * replaced by the denoised latent. Constants: text [text_tokens][3072], cos,
+ * sin, mask (device). step_seconds / step_timesteps (nullable) get one entry
+ * per executed step. */
+int ernie_denoise(ernie_device* device, const int* blocks, int count, float* latent, int height, int width,
+                  const float* text, int text_tokens, const float* cos_t, const float* sin_t, const float* mask,
+                  int valid_prefix, int steps, int start_step, int storage_dtype, double* step_seconds,
+                  float* step_timesteps, char* err, size_t errlen);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ERNIE_H */

@@ -1,0 +1,236 @@
+"""Block, sequence, heads, DiT and denoise parity on the device against the
+oracle, under the reference's own per-precision gates (kat.py)."""
+import numpy as np
+import pytest
+
+import ernie_amd as E
+import kat
+import oracle as O
+from gpu_util import ALL_DT, NAMES, dev, empty, host
+from test_oracle import small_block, small_heads, small_inputs
+
+pytestmark = pytest.mark.gpu
+
+BLOCK_FIELDS = O.BLOCK_FIELDS
+
+
+def run_block(ctx, index, x, mods, cos, sin, mask, valid):
+    S, dim = x.shape
+    xd, out = dev(x), empty((S, dim))
+    ctx.block_forward(index, xd, out, dev(mods), dev(cos), dev(sin), S, mask=dev(mask), valid_keys=valid)
+    return host(out)
+
+
+@pytest.mark.parametrize("dt", ALL_DT, ids=lambda d: NAMES[d])
+def test_block_small_against_oracle(ctx, dt):
+    w = small_block(dim=256, ffn=512)
+    x, mods, cos, sin, mask = small_inputs(S=40, dim=256)
+    ctx.block_upload(0, w, 256, 512, dt)
+    valid = int(np.sum(mask == 0))
+    got = run_block(ctx, 0, x, mods, cos, sin, mask, valid)
+    ref = O.block_forward(w, x, mods, cos, sin, mask)
+    g = kat.gate(got, ref, *kat.BLOCK_GATES[NAMES[dt]])
+    assert g["passed"], g
+    if dt == E.FP32:
+        assert kat.north_star_fp32(got, ref)["passed"]
+    # The mask alone (valid_keys = 0) and the count alone give the same block.
+    again = run_block(ctx, 0, x, mods, cos, sin, mask, 0)
+    g2 = kat.gate(again, ref, *kat.BLOCK_GATES[NAMES[dt]])
+    assert g2["passed"], g2
+
+
+@pytest.mark.parametrize("dt", ALL_DT, ids=lambda d: NAMES[d])
+def test_block_config0_against_oracle(ctx, dt):
+    # One ERNIE block at full width (4096, 32 heads, FFN 12288), S = 1056
+    # (32x32 image tokens + 32 text tokens, all valid), weights N(0, 0.02).
+    dim, ffn = 4096, 12288
+    w = small_block(dim=dim, ffn=ffn, seed=0)
+    x, mods, cos, sin, mask = small_inputs(S=1056, dim=dim, image=(32, 32), valid=32, seed=1)
+    ctx.block_upload(1, w, dim, ffn, dt)
+    got = run_block(ctx, 1, x, mods, cos, sin, mask, 1056)
+    ref = O.block_forward(w, x, mods, cos, sin, mask)
+    g = kat.gate(got, ref, *kat.BLOCK_GATES[NAMES[dt]])
+    assert g["passed"], g
+    if dt == E.FP32:
+        m = kat.north_star_fp32(got, ref)
+        assert m["passed"], m
+    # Repeat-determinism (probes/block_runner.cpp:196-203): bitwise identical.
+    np.testing.assert_array_equal(run_block(ctx, 1, x, mods, cos, sin, mask, 1056), got)
+    ctx.call("block_release", 1)
+
+
+def test_block_zero_gates_is_identity_full_size(ctx):
+    # S = 4160 fp16 (the 1024x1024 token count); gate_sa = gate_mlp = 0 leaves x untouched.
+    S, dim, ffn = 4160, 4096, 12288
+    ctx.block_init_random(2, dim, ffn, E.FP16, seed=5)
+    x = O.normal((S, dim), 3)
+    mods = O.normal((6, dim), 4, std=0.5)
+    mods[2] = 0.0
+    mods[5] = 0.0
+    freqs = O.rope_frequencies()
+    cos, sin, mask = O.dit_constants(freqs, 64, 64, 40, 64)
+    got = run_block(ctx, 2, x, mods, cos, sin, mask, 4136)
+    np.testing.assert_array_equal(got, x)
+    # With gates on, the output is finite, deterministic and differs from x.
+    mods = O.normal((6, dim), 4, std=0.5)
+    a = run_block(ctx, 2, x, mods, cos, sin, mask, 4136)
+    b = run_block(ctx, 2, x, mods, cos, sin, mask, 4136)
+    assert np.isfinite(a).all() and not np.array_equal(a, x)
+    np.testing.assert_array_equal(a, b)
+    ctx.call("block_release", 2)
+
+
+@pytest.mark.parametrize("dt", ALL_DT, ids=lambda d: NAMES[d])
+def test_block_sequence_against_oracle(ctx, dt):
+    dim, ffn = 256, 512
+    ws = [small_block(dim, ffn, seed=10 + i) for i in range(3)]
+    for i, w in enumerate(ws):
+        ctx.block_upload(10 + i, w, dim, ffn, dt)
+    x, mods, cos, sin, mask = small_inputs(S=40, dim=dim)
+    valid = int(np.sum(mask == 0))
+    xd, out = dev(x), empty(x.shape)
+    secs = ctx.block_sequence([10, 11, 12], xd, out, dev(mods), dev(cos), dev(sin), 40, mask=dev(mask),
+                              valid_keys=valid, timing=True)
+    assert secs.shape == (3,) and np.all(secs > 0)
+    ref = x
+    for w in ws:
+        ref = O.block_forward(w, ref, mods, cos, sin, mask)
+    g = kat.gate(host(out), ref, *kat.SEQUENCE_GATES[NAMES[dt]])
+    assert g["passed"], g
+
+
+def test_block_call_validation(ctx):
+    x = empty((8, 256))
+    with pytest.raises(E.ErnieError):
+        ctx.block_forward(999, x, x, x, x, x, 8)  # not loaded
+    with pytest.raises(E.ErnieError):
+        ctx.block_sequence([], x, x, x, x, x, 8)
+    with pytest.raises(E.ErnieError):
+        ctx.block_init_random(3, 200, 512, E.FP16, 1)  # width not a multiple of 128
+
+
+def heads_for(dim):
+    return small_heads(dim=dim, latent_ch=128, text_dim=3072)
+
+
+@pytest.mark.parametrize("dt", ALL_DT, ids=lambda d: NAMES[d])
+def test_heads_against_oracle(ctx, dt):
+    dim = 256
+    hw_ = heads_for(dim)
+    ctx.heads_upload(hw_, dim, 128, 3072, dt)
+    latent = O.normal((128, 6, 5), 3)
+    text = O.normal((8, 3072), 4)
+    feat = O.timestep_features(500.0)[:dim].copy()
+    S = 30 + 8
+    x, c, mods = empty((S, dim)), empty((dim,)), empty((6, dim))
+    ctx.input_head(dev(latent), 30, dev(text), 8, dev(feat), x, c, mods)
+    xr, cr, mr = O.input_head({k: hw_[k] for k in O.INPUT_HEAD_FIELDS}, latent, text, feat)
+    gates = kat.HEAD_GATES[NAMES[dt]]
+    for got, ref in ((x, xr), (c, cr), (mods, mr)):
+        g = kat.gate(host(got), ref, *gates)
+        assert g["passed"], g
+    pred = empty((128, 30))
+    ctx.output_head(dev(xr), S, 30, dev(cr), pred)
+    out_w = {"mod_w": hw_["out_mod_w"], "mod_b": hw_["out_mod_b"], "proj_w": hw_["proj_w"], "proj_b": hw_["proj_b"]}
+    g = kat.gate(host(pred), O.output_head(out_w, xr, cr, 30), *gates)
+    assert g["passed"], g
+
+
+def oracle_dit(blocks_w, heads_w, latent, text, feat, cos, sin, mask):
+    x, c, mods = O.input_head({k: heads_w[k] for k in O.INPUT_HEAD_FIELDS}, latent, text, feat)
+    for w in blocks_w:
+        x = O.block_forward(w, x, mods, cos, sin, mask)
+    out_w = {"mod_w": heads_w["out_mod_w"], "mod_b": heads_w["out_mod_b"], "proj_w": heads_w["proj_w"],
+             "proj_b": heads_w["proj_b"]}
+    hw = latent[0].size
+    return O.output_head(out_w, x, c, hw).reshape(latent.shape)
+
+
+def dit_setup(ctx, dt, nblocks=2, dim=256, ffn=512, grid=(4, 4), text=8, valid=5):
+    hw_ = heads_for(dim)
+    ctx.heads_upload(hw_, dim, 128, 3072, dt)
+    ws = [small_block(dim, ffn, seed=20 + i) for i in range(nblocks)]
+    for i, w in enumerate(ws):
+        ctx.block_upload(20 + i, w, dim, ffn, dt)
+    H, W = grid
+    latent = O.normal((128, H, W), 31)
+    tx = O.normal((text, 3072), 32)
+    tx[valid:] = 0.0  # pad_text zero rows
+    cos, sin, mask = O.dit_constants(O.rope_frequencies(), W, H, valid, text)
+    return hw_, ws, latent, tx, cos, sin, mask
+
+
+@pytest.mark.parametrize("dt", ALL_DT, ids=lambda d: NAMES[d])
+def test_dit_forward_against_oracle(ctx, dt):
+    dim = 256
+    hw_, ws, latent, tx, cos, sin, mask = dit_setup(ctx, dt)
+    feat = O.timestep_features(705.8824)[:dim].copy()
+    pred = empty(latent.shape)
+    valid = int(np.sum(mask == 0))
+    ctx.dit_forward(dev(latent), 16, dev(tx), tx.shape[0], dev(feat), dev(cos), dev(sin), [20, 21], pred,
+                    mask=dev(mask), valid_keys=valid)
+    ref = oracle_dit(ws, hw_, latent, tx, feat, cos, sin, mask)
+    g = kat.gate(host(pred), ref, *kat.SEQUENCE_GATES[NAMES[dt]])
+    assert g["passed"], g
+
+
+@pytest.mark.parametrize("dt", [E.FP32, E.FP16], ids=lambda d: NAMES[d])
+def test_facade_denoise_against_oracle(dt):
+    # denoise (src/denoiser.cpp:41-86) through the C++ facade: schedule, time
+    # features, run_dit, Euler and the finite check; 3 of 4 steps from start_step 1.
+    import torch
+    fac = E.Facade(0)
+    dim = 4096  # time features are 4096 wide (ERNIE Timesteps(4096))
+    ffn = 512
+    hw_ = small_heads(dim=dim, latent_ch=128, text_dim=3072, seed=40)
+    fac.hip.heads_upload(hw_, dim, 128, 3072, dt)
+    ws = [small_block(dim, ffn, seed=41)]
+    fac.hip.block_upload(0, ws[0], dim, ffn, dt)
+    H = W = 4
+    text, valid = 8, 5
+    latent = O.normal((128, H, W), 43)
+    tx = O.normal((text, 3072), 44)
+    tx[valid:] = 0.0
+    cos, sin, mask = O.dit_constants(O.rope_frequencies(), W, H, valid, text)
+    steps, start = 4, 1
+    lat = dev(latent)
+    secs, ts = fac.denoise([0], lat, H, W, dev(tx), text, dev(cos), dev(sin), dev(mask), H * W + valid, steps,
+                           start_step=start, dtype=dt)
+    sig, tsteps = O.flow_schedule_turbo(steps)
+    np.testing.assert_array_equal(ts, tsteps[start:])
+    assert np.all(secs > 0)
+    ref = latent.copy()
+    for i in range(start, steps):
+        pred = oracle_dit(ws, hw_, ref, tx, O.timestep_features(float(tsteps[i])), cos, sin, mask)
+        ref = O.euler_step(ref, pred, sig[i + 1] - sig[i])
+    nrmse, rtol, atol = kat.DENOISER_GATES[NAMES[dt]]
+    g = kat.gate(host(lat), ref, atol, rtol, nrmse)
+    assert g["passed"], g
+    # Argument contracts of the facade (src/denoiser.cpp:12-19, 50-51).
+    with pytest.raises(E.ErnieInvalidRequest):
+        fac.denoise([0], lat, H, W, dev(tx), text, dev(cos), dev(sin), dev(mask), 0, steps, start_step=5, dtype=dt)
+    with pytest.raises(E.ErnieInvalidRequest):
+        fac.denoise([], lat, H, W, dev(tx), text, dev(cos), dev(sin), dev(mask), 0, steps, dtype=dt)
+    torch.cuda.synchronize()
+    fac.close()
+
+
+def test_facade_block_sequence_validation_and_parity():
+    fac = E.Facade(0)
+    dim, ffn = 256, 512
+    w = small_block(dim, ffn, seed=50)
+    fac.hip.block_upload(0, w, dim, ffn, E.FP32)
+    x, mods, cos, sin, mask = small_inputs(S=40, dim=dim)
+    md = [dev(m) for m in mods]
+    out = empty(x.shape)
+    valid = int(np.sum(mask == 0))
+    secs = fac.run_block_sequence([0], dev(x), 40, dim, md, dev(cos), dev(sin), out, mask=dev(mask),
+                                  valid_prefix=valid)
+    assert secs.shape == (1,) and secs[0] > 0
+    m = kat.north_star_fp32(host(out), O.block_forward(w, x, mods, cos, sin, mask))
+    assert m["passed"], m
+    with pytest.raises(E.ErnieInvalidRequest):
+        fac.run_block_sequence([0] * 37, dev(x), 40, dim, md, dev(cos), dev(sin), out)
+    with pytest.raises(E.ErnieInvalidRequest):
+        fac.run_block_sequence([], dev(x), 40, dim, md, dev(cos), dev(sin), out)
+    fac.close()
