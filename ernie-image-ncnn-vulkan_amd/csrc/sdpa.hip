@@ -54,31 +54,53 @@ template <> struct Mfma16<bf16> {
 };
 
 // 8 consecutive elements starting at column c8*8 of a row of length d (zero past d).
-template <typename T>
-__device__ __forceinline__ u32x4 load_row8(const T* row, int c8, int d, int vec_ok)
+// FAST: d == 128 and every row / head stride and base is 16-byte aligned.
+template <typename T, bool FAST>
+__device__ __forceinline__ u32x4 load_row8(const T* row, int c8, int d)
 {
-    const int c = c8 * 8;
-    if (vec_ok && c + 8 <= d) return *reinterpret_cast<const u32x4*>(row + c);
-    union { u32x4 u; T e[8]; } r;
+    if constexpr (FAST) {
+        return *reinterpret_cast<const u32x4*>(row + c8 * 8);
+    } else {
+        const int c = c8 * 8;
+        union { u32x4 u; T e[8]; } r;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) r.e[i] = (c + i < d) ? row[c + i] : T(0.f);
-    return r.u;
+        for (int i = 0; i < 8; ++i) r.e[i] = (c + i < d) ? row[c + i] : T(0.f);
+        return r.u;
+    }
 }
 
-template <typename T>
-__global__ void __launch_bounds__(256) sdpa16_kernel(SdpaParams p)
+// Keys of one 64-key tile owned by lane (lrow, g) in register r of S^T subtile t.
+__device__ __forceinline__ int tile_key(int t, int r, int g) { return 32 * t + 8 * (r >> 2) + 4 * g + (r & 3); }
+
+// Rescale threshold (log2 units): the running maximum used for exp2 is only
+// raised when a tile's maximum exceeds it by more than this, so P <= 2^8 and the
+// O / l rescale is skipped for almost every tile. Exact: O and l share the offset.
+constexpr float kRescaleSlack = 8.0f;
+
+// Mask modes: none, one additive row broadcast over queries (staged in LDS per
+// tile), or one additive row per query (read by each lane).
+enum MaskMode : int { MASK_NONE = 0, MASK_ROW = 1, MASK_PER_QUERY = 2 };
+
+template <typename T, bool FAST, int MM>
+__global__ void __launch_bounds__(256, 2) sdpa16_kernel(SdpaParams p)
 {
     typedef typename Mfma16<T>::vec vec8;
     __shared__ __attribute__((aligned(16))) T Ks[2][BKV * KS_STRIDE];
     __shared__ __attribute__((aligned(16))) T Vt[2][128 * VT_STRIDE];
+    __shared__ float Ms[2][BKV];
 
-    const int h = blockIdx.y;
+    // XCD-aware placement: the 8 XCDs each take a contiguous range of (head,
+    // query tile) pairs, so a head's K/V stream from HBM into one XCD's L2.
+    const int qtiles = (p.sq + BQ - 1) / BQ;
+    const int total = qtiles * p.heads;
+    int logical = blockIdx.x;
+    if ((total & 7) == 0) logical = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
+    const int h = logical / qtiles;
+    const int q_base = (logical - h * qtiles) * BQ;
     const int kvh = h / p.group;
-    const int q_base = blockIdx.x * BQ;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lrow = lane & 31, g = lane >> 5;
-    const int q0 = q_base + wave * 32;
-    const int my_q = q0 + lrow;
+    const int my_q = q_base + wave * 32 + lrow;
 
     const T* Q = static_cast<const T*>(p.q) + (size_t)h * p.q_hs;
     const T* K = static_cast<const T*>(p.k) + (size_t)kvh * p.k_hs;
@@ -89,29 +111,33 @@ __global__ void __launch_bounds__(256) sdpa16_kernel(SdpaParams p)
     {
         const T* qrow = Q + (size_t)min(my_q, p.sq - 1) * p.q_rs;
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const u32x4 raw = load_row8<T>(qrow, 2 * s + g, p.d, p.vec_ok);
-            qf[s] = __builtin_bit_cast(vec8, raw);
-        }
+        for (int s = 0; s < 8; ++s) qf[s] = __builtin_bit_cast(vec8, load_row8<T, FAST>(qrow, 2 * s + g, p.d));
     }
 
     // Tile loaders. K: thread -> (key = tid/16 + 16*pass, chunk = tid%16).
     // V: thread -> (key pair kp = tid/16 + 16*pass, chunk = tid%16), stored transposed.
     const int ld_chunk = tid & 15, ld_key = tid >> 4;
     u32x4 kreg[4], vreg[2][2];
+    float mreg = 0.f;
     auto load_global = [&](int kv0) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const int key = min(kv0 + ld_key + 16 * s, p.sk - 1);
-            kreg[s] = load_row8<T>(K + (size_t)key * p.k_rs, ld_chunk, p.d, p.vec_ok);
+            kreg[s] = load_row8<T, FAST>(K + (size_t)key * p.k_rs, ld_chunk, p.d);
         }
 #pragma unroll
         for (int s = 0; s < 2; ++s)
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
                 const int key = min(kv0 + 2 * (ld_key + 16 * s) + e, p.sk - 1);
-                vreg[s][e] = load_row8<T>(V + (size_t)key * p.v_rs, ld_chunk, p.d, p.vec_ok);
+                vreg[s][e] = load_row8<T, FAST>(V + (size_t)key * p.v_rs, ld_chunk, p.d);
             }
+        if constexpr (MM == MASK_ROW) {
+            if (tid < BKV) {
+                const int key = kv0 + tid;
+                mreg = key < p.sk ? p.mask[(size_t)h * p.mask_hs + key] : 0.f;
+            }
+        }
     };
     auto store_lds = [&](int buf) {
 #pragma unroll
@@ -120,14 +146,17 @@ __global__ void __launch_bounds__(256) sdpa16_kernel(SdpaParams p)
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             const int kp = ld_key + 16 * s;
-            const uint32_t* v0 = reinterpret_cast<const uint32_t*>(&vreg[s][0]);
-            const uint32_t* v1 = reinterpret_cast<const uint32_t*>(&vreg[s][1]);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t lo = (v0[i >> 1] >> (16 * (i & 1))) & 0xffffu;
-                const uint32_t hi = (v1[i >> 1] >> (16 * (i & 1))) & 0xffffu;
-                *reinterpret_cast<uint32_t*>(&Vt[buf][(ld_chunk * 8 + i) * VT_STRIDE + 2 * kp]) = lo | (hi << 16);
+            for (int ii = 0; ii < 8; ++ii) {
+                // Rotate the d order by chunk to spread the transposed stores over banks.
+                const int i = (ii + ld_chunk) & 7;
+                const uint32_t a = vreg[s][0][i >> 1], b = vreg[s][1][i >> 1];
+                const uint32_t packed = __builtin_amdgcn_perm(b, a, (i & 1) ? 0x07060302u : 0x05040100u);
+                *reinterpret_cast<uint32_t*>(&Vt[buf][(ld_chunk * 8 + i) * VT_STRIDE + 2 * kp]) = packed;
             }
+        }
+        if constexpr (MM == MASK_ROW) {
+            if (tid < BKV) Ms[buf][tid] = mreg * kLog2e;
         }
     };
 
@@ -137,7 +166,11 @@ __global__ void __launch_bounds__(256) sdpa16_kernel(SdpaParams p)
 #pragma unroll
         for (int r = 0; r < 16; ++r) oacc[t][r] = 0.f;
     float m_run = -INFINITY, l_run = 0.f;
-    const float* mrow = p.mask ? p.mask + (size_t)h * p.mask_hs + (size_t)min(my_q, p.sq - 1) * p.mask_rs : nullptr;
+    const float c = p.scale_log2;
+    const float* qmask = MM == MASK_PER_QUERY
+                             ? p.mask + (size_t)h * p.mask_hs + (size_t)min(my_q, p.sq - 1) * p.mask_rs
+                             : nullptr;
+    constexpr bool MASK = MM != MASK_NONE;
 
     const int ntiles = (p.kv_end + BKV - 1) / BKV;
     load_global(0);
@@ -161,41 +194,63 @@ __global__ void __launch_bounds__(256) sdpa16_kernel(SdpaParams p)
                 sacc[t] = Mfma16<T>::run(kf, qf[s], sacc[t]);
             }
         }
-        // Scale, mask, online softmax. Register r of subtile t holds key
-        // kv0 + 32t + 8(r/4) + 4g + r%4 for query lrow.
+        // Scores in log2 units: s * c (+ mask * log2 e); keys >= kv_end excluded.
+        const bool partial = kv0 + BKV > p.kv_end;
+        if (MASK || partial) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int kk = tile_key(t, r, g);
+                    float v = sacc[t][r] * c;
+                    if constexpr (MM == MASK_ROW) v += Ms[buf][kk];
+                    if constexpr (MM == MASK_PER_QUERY) v += (kv0 + kk < p.sk ? qmask[kv0 + kk] : 0.f) * kLog2e;
+                    sacc[t][r] = kv0 + kk < p.kv_end ? v : -INFINITY;
+                }
+        }
         float tmax = -INFINITY;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = kv0 + 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
-                float s = sacc[t][r] * p.scale_log2;
-                if (mrow) s += (key < p.sk ? mrow[key] : 0.f) * kLog2e;
-                s = key < p.kv_end ? s : -INFINITY;
-                sacc[t][r] = s;
-                tmax = fmaxf(tmax, s);
-            }
+            for (int r = 0; r < 16; r += 2) tmax = fmaxf(tmax, fmaxf(sacc[t][r], sacc[t][r + 1]));
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-        const float m_new = fmaxf(m_run, tmax);
-        const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        const float alpha = exp2f(m_run - m_use);
+        if (!(MASK || partial)) tmax *= c;  // unscaled scores: c > 0 preserves the order
+        // Raise the running offset only past the slack (wave-uniform decision).
+        const bool raise = tmax > m_run + kRescaleSlack;
+        if (__any(raise)) {
+            const float m_new = raise ? tmax : m_run;
+            const float alpha = m_run == -INFINITY ? 0.f : exp2f(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+            m_run = m_new;
+        }
+        const float m_use = m_run == -INFINITY ? 0.f : m_run;
         float psum = 0.f;
         vec8 pf[2][2];
+        if (MASK || partial) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+            for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float pv = exp2f(sacc[t][r] - m_use);
-                psum += pv;
-                pf[t][r >> 3][r & 7] = T(pv);
-            }
+                for (int r = 0; r < 16; ++r) {
+                    const float pv = exp2f(sacc[t][r] - m_use);
+                    psum += pv;
+                    pf[t][r >> 3][r & 7] = T(pv);
+                }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float pv = exp2f(__builtin_fmaf(sacc[t][r], c, -m_use));
+                    psum += pv;
+                    pf[t][r >> 3][r & 7] = T(pv);
+                }
+        }
         psum += __shfl_xor(psum, 32, 64);
-        l_run = l_run * alpha + psum;
-        m_run = m_new;
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+        l_run += psum;
 
         // O^T += V^T P^T: A operand = V^T[d][keys], keys matching pf's layout.
 #pragma unroll
@@ -225,7 +280,7 @@ __global__ void __launch_bounds__(256) sdpa16_kernel(SdpaParams p)
 #pragma unroll
         for (int rq = 0; rq < 4; ++rq) {
             const int d0 = 32 * dt + 8 * rq + 4 * g;
-            if (p.vec_ok && d0 + 4 <= p.d) {
+            if constexpr (FAST) {
                 union { u32x2 u; T e[4]; } pk;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) pk.e[e] = T(oacc[dt][4 * rq + e] * inv);
@@ -413,10 +468,29 @@ int sdpa(const SdpaArgs& a, hipStream_t s)
     p.vec_ok = (bases % 16 == 0) && a.q_hs % vec == 0 && a.q_rs % vec == 0 && a.k_hs % vec == 0 &&
                a.k_rs % vec == 0 && a.v_hs % vec == 0 && a.v_rs % vec == 0 && a.o_hs % vec == 0 &&
                a.o_rs % vec == 0;
-    const dim3 grid((a.sq + BQ - 1) / BQ, a.heads), block(256);
-    if (a.dtype == DT_F32) hipLaunchKernelGGL(sdpa32_kernel, grid, block, 0, s, p);
-    else if (a.dtype == DT_F16) hipLaunchKernelGGL(sdpa16_kernel<f16>, grid, block, 0, s, p);
-    else hipLaunchKernelGGL(sdpa16_kernel<bf16>, grid, block, 0, s, p);
+    const dim3 block(256);
+    if (a.dtype == DT_F32) {
+        hipLaunchKernelGGL(sdpa32_kernel, dim3((a.sq + BQ - 1) / BQ, a.heads), block, 0, s, p);
+    } else {
+        const bool fast = p.vec_ok && a.d == 128;
+        const int mm = !a.mask ? MASK_NONE : (a.mask_rows > 1 ? MASK_PER_QUERY : MASK_ROW);
+        const dim3 grid(((a.sq + BQ - 1) / BQ) * a.heads);
+#define EHIP_SDPA16(T)                                                                                     \
+    do {                                                                                                   \
+        if (fast) {                                                                                        \
+            if (mm == MASK_NONE) hipLaunchKernelGGL((sdpa16_kernel<T, true, MASK_NONE>), grid, block, 0, s, p); \
+            else if (mm == MASK_ROW) hipLaunchKernelGGL((sdpa16_kernel<T, true, MASK_ROW>), grid, block, 0, s, p); \
+            else hipLaunchKernelGGL((sdpa16_kernel<T, true, MASK_PER_QUERY>), grid, block, 0, s, p);      \
+        } else {                                                                                           \
+            if (mm == MASK_NONE) hipLaunchKernelGGL((sdpa16_kernel<T, false, MASK_NONE>), grid, block, 0, s, p); \
+            else if (mm == MASK_ROW) hipLaunchKernelGGL((sdpa16_kernel<T, false, MASK_ROW>), grid, block, 0, s, p); \
+            else hipLaunchKernelGGL((sdpa16_kernel<T, false, MASK_PER_QUERY>), grid, block, 0, s, p);     \
+        }                                                                                                  \
+    } while (0)
+        if (a.dtype == DT_F16) EHIP_SDPA16(f16);
+        else EHIP_SDPA16(bf16);
+#undef EHIP_SDPA16
+    }
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : -int(e);
 }

@@ -67,7 +67,7 @@ DeviceMat run_block_sequence(const std::vector<BlockModel>& models, const Device
         double seconds = 0;
         const int index = models[i].index;
         const int rc = ernie_hip_block_sequence(ctx, &index, 1, in, current.data, mods.data, cos.data, sin.data,
-                                                mask.empty() ? nullptr : mask.data, mask.valid_prefix, S, &seconds);
+                                                mask_arg(mask), mask.valid_prefix, S, &seconds);
         if (rc) {
             if (stats.collect_details)
                 stats.details.push_back({int(i), "extract_compute_composite", "failed",

@@ -57,7 +57,7 @@ DeviceMat run_dit(const DitModel& model, const std::vector<DeviceMat>& inputs, c
     for (const auto& b : model.blocks) indices.push_back(b.index);
     std::vector<double> seconds(indices.size(), 0.0);
     check_status(ernie_hip_block_sequence(ctx, indices.data(), int(indices.size()), x.data, x.data, mods.data, cos.data,
-                                          sin.data, mask.empty() ? nullptr : mask.data, mask.valid_prefix, S,
+                                          sin.data, mask_arg(mask), mask.valid_prefix, S,
                                           seconds.data()),
                  ctx, "extract block output");
     stats.blocks.peak_loaded_nets = int(indices.size());

@@ -55,6 +55,14 @@ struct DeviceMat {
     std::vector<float> download(const Device& device) const;
 };
 
+// Attention mask argument for the device: a mask built by dit_constants is
+// canonical (0 below valid_prefix, -1e30 from it), so the key count alone
+// carries it and the kernel skips the additive mask entirely.
+inline const float* mask_arg(const DeviceMat& mask)
+{
+    return (mask.empty() || mask.valid_prefix > 0) ? nullptr : mask.data;
+}
+
 // Mirrors the ncnn::Option fields the block path reads (probes/block_runner.cpp:102-109):
 // storage precision, FP32 arithmetic, and the device standing in for the Vulkan device.
 struct Option {

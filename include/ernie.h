@@ -42,9 +42,11 @@ int ernie_dit_constants(const float* frequencies, int width, int height, int val
                         float* cos_out, float* sin_out, float* mask_out, char* err, size_t errlen);
 
 /* run_block_sequence (src/block_sequence.h:38-41): x [S][dim] device FP32,
- * mods = six [dim] device vectors, cos/sin [S][128], mask [S] with valid_prefix
- * hint (0 = none). out [S][dim] device FP32. compute_seconds (nullable) gets
- * per-block device time. */
+ * mods = six [dim] device vectors, cos/sin [S][128], mask [S]. valid_prefix > 0
+ * declares the mask canonical (0 below it, -1e30 from it, as dit_constants
+ * builds it): the key count then replaces the mask, whose contents are not
+ * read; 0 applies the mask as given. out [S][dim] device FP32.
+ * compute_seconds (nullable) gets per-block device time. */
 int ernie_run_block_sequence(ernie_device* device, const int* blocks, int count, const float* x, int S, int dim,
                              const float* const* mods, const float* cos_t, const float* sin_t, const float* mask,
                              int valid_prefix, int storage_dtype, float* out, double* compute_seconds, char* err,
