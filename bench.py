@@ -23,6 +23,11 @@ sys.path.insert(0, str(ROOT / "ernie-image-ncnn-vulkan_amd"))
 METRIC = "DiT denoise steps/s at 1024×1024 fp16 (36 blk); SDPA+GEMM % MFMA peak"
 PEAK = {"fp16": 2.5e15, "bf16": 2.5e15, "fp32": 157.3e12}
 HBM_PEAK = 8.0e12
+# HBM bytes per launch of each kernel class at this workload (FP16, S=4160), from
+# two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) scaled by the same counters'
+# reading for a plain 512 MiB FP32 copy (x2.000 fetch, x1.000 write); the runs and
+# the per-dispatch table are in profiles/denoise_1024_fp16_hbm_traffic.md.
+MEASURED_TRAFFIC = {"fp16": {"gemm_up_gate": 1.351e9, "gemm_qkv": 7.796e8, "sdpa": 1.79e8}}
 DIM, FFN, LATENT_CH, TEXT_DIM = 4096, 12288, 128, 3072
 
 
@@ -38,6 +43,9 @@ def parse():
     ap.add_argument("--valid-text", type=int, default=40)
     ap.add_argument("--cpu-baseline", choices=("on", "off"), default="on")
     ap.add_argument("--cpu-tokens", type=int, default=4160, help="tokens of the single-block CPU sample")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="first run a plain FP32 copy kernel of this many MiB three times (the reference "
+                         "dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
     return ap.parse_args()
 
 
@@ -83,6 +91,17 @@ def main():
     S = hw + args.text
     fac = E.Facade(0)
     ctx = fac.hip
+    if args.copy_calibration_mib > 0:
+        n = args.copy_calibration_mib << 18  # FP32 elements
+        src = torch.empty(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        ctx.fill_normal(src, E.FP32, n, seed=11)
+        for _ in range(3):
+            ctx.call("convert", E.ptr(src), E.FP32, E.ptr(dst), E.FP32, n)
+        torch.cuda.synchronize()
+        print(f"bench: copy calibration {args.copy_calibration_mib} MiB read + {args.copy_calibration_mib} MiB "
+              f"written per dispatch (convert_kernel), 3 dispatches", file=sys.stderr, flush=True)
+        del src, dst
     for b in range(args.blocks):
         ctx.block_init_random(b, DIM, FFN, dt, seed=1000 + b, std=0.02)
     ctx.heads_init_random(DIM, LATENT_CH, TEXT_DIM, dt, seed=7, std=0.02)
@@ -143,7 +162,8 @@ def main():
                    "blocks": args.blocks, "tokens": S, "latent": [LATENT_CH, H, W], "text_tokens": args.text,
                    "valid_text": args.valid_text},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved / 1e12, "peak": peak / 1e12,
-                     "unit": "TFLOP/s", "frac": achieved / peak, "traffic": None,
+                     "unit": "TFLOP/s", "frac": achieved / peak,
+                     "traffic": MEASURED_TRAFFIC.get(args.precision, {}).get(dom) if args.grid == 64 else None,
                      "flop_per_launch": flop_per_launch, "avg_launch_us": avg_s * 1e6},
         "mfma_util_sdpa_gemm": (tot_flop / (tot_ms * 1e-3)) / peak if tot_ms else None,
         "sdpa_gemm_tflops": (tot_flop / (tot_ms * 1e-3)) / 1e12 if tot_ms else None,
