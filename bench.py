@@ -27,7 +27,7 @@ HBM_PEAK = 8.0e12
 # two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) scaled by the same counters'
 # reading for a plain 512 MiB FP32 copy (x2.000 fetch, x1.000 write); the runs and
 # the per-dispatch table are in profiles/denoise_1024_fp16_hbm_traffic.md.
-MEASURED_TRAFFIC = {"fp16": {"gemm_up_gate": 1.351e9, "gemm_qkv": 7.796e8, "sdpa": 1.79e8}}
+MEASURED_TRAFFIC = {"fp16": {"gemm_up_gate": 1.517e9, "gemm_qkv": 8.119e8, "sdpa": 1.786e8}}
 DIM, FFN, LATENT_CH, TEXT_DIM = 4096, 12288, 128, 3072
 
 

@@ -3,6 +3,8 @@
 // (the reference's Gemm layers use transB=1 with constant B, block.ncnn.param
 // lines 19/22/25/61/70/71/74), FP32 accumulation and fused epilogues.
 //
+// 16-bit operands go to the ping-pong kernel (gemm16_pp.hip); the register-staged
+// kernel below serves operands of 2 GiB or more, which need 64-bit addressing.
 // 16-bit kernel (FP16 / BF16 operands, v_mfma_f32_32x32x16_{f16,bf16}):
 //   * 512 threads = 8 waves arranged 2 (M) x 4 (N); N tile 256, K step 32.
 //   * M tiles have a variable height of 1..10 subtiles of 32 rows, chosen on
@@ -370,6 +372,8 @@ int gemm(const GemmArgs& a, hipStream_t s)
         if (a.epilogue == EPI_STORE) hipLaunchKernelGGL((gemm32_kernel<EPI_STORE>), grid, block, 0, s, p);
         else if (a.epilogue == EPI_GATE_RESID) hipLaunchKernelGGL((gemm32_kernel<EPI_GATE_RESID>), grid, block, 0, s, p);
         else hipLaunchKernelGGL((gemm32_kernel<EPI_GEGLU>), grid, block, 0, s, p);
+    } else if ((rc = gemm16_pingpong(a, s)) != 1) {
+        return rc;
     } else if (a.dtype == DT_F16) {
         rc = launch16<f16>(a, p, s);
     } else {

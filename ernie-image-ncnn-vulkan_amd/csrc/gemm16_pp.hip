@@ -1,0 +1,308 @@
+// SPDX-License-Identifier: MIT
+// 16-bit GEMM for gfx950, C[M,N] = A[M,K] * W[N,K]^T with FP32 accumulation and the
+// fused epilogues of the DiT block (the reference's Gemm layers, transB with
+// constant B: block.ncnn.param lines 19/22/25/61/70/71/74).
+//
+// Design (256 x 256 output tile per 512-thread workgroup, K step 32):
+//   * Operands reach LDS through direct global->LDS buffer loads (16 bytes per lane,
+//     1 KiB per instruction), so no VGPR staging and no ds_write is involved. A ring
+//     of 4 stages (128 KiB) keeps three K steps in flight.
+//   * Staged rows are 64 bytes; their four 16-byte chunks are XOR-swizzled by a
+//     function of the low five row bits, chosen by measuring every GF(2)-linear
+//     candidate with the fragment read pattern on gfx950.
+//   * The 8 waves form two groups with one wave of each per SIMD. The groups run half
+//     a K step apart: while one executes a cluster of 16 v_mfma_f32_32x32x16 from
+//     registers, the other reads its next fragments from LDS and issues its share of
+//     the next stage's loads; they swap at each workgroup barrier (ping-pong), so the
+//     matrix cores are fed while LDS latency is taken by the other group.
+//   * Each wave owns a 128 x 64 sub-tile (4 x 2 accumulators of 32 x 32). Rows past
+//     M and columns past N read as zero through the buffer range checks; tail tiles
+//     (M % 256) compute only their 64-row multiples.
+//   * Workgroup b runs on XCD b % 8: each XCD gets a contiguous range of tiles
+//     (4 M tiles per N sweep, sharing its own L2), and the tail row of tiles last.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace ehip {
+namespace pingpong {
+
+constexpr int BM = 256, BN = 256, BK = 32, NS = 4;
+constexpr int ROWB = BK * 2;                // 64 bytes per staged row
+constexpr int A_BYTES = BM * ROWB;          // 16 KiB
+constexpr int STAGE = A_BYTES + BN * ROWB;  // 32 KiB
+constexpr uint32_t kRsrcFlags = 0x00020000;
+
+struct Params {
+    const void* A; long lda;
+    const void* W; long ldw;
+    int M, N, K;
+    int m_full, tail_sub, n_tiles;
+    void* C; long ldc;
+    const float* bias;
+    const float* resid; long ld_resid;
+    const float* gate;
+    uint32_t a_bytes, w_bytes;
+};
+
+template <typename T> struct Mfma;
+template <> struct Mfma<f16> {
+    typedef f16x8 vec;
+    static __device__ __forceinline__ f32x16 run(vec a, vec b, f32x16 c)
+    { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
+};
+template <> struct Mfma<bf16> {
+    typedef bf16x8 vec;
+    static __device__ __forceinline__ f32x16 run(vec a, vec b, f32x16 c)
+    { return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0); }
+};
+
+// Physical chunk = logical chunk ^ fsw(row), with fsw's two bits the parities of
+// row bits {0,3,4} and {1,2,3}: the fastest of all GF(2)-linear swizzles of the
+// low five row bits for this fragment read pattern, measured on gfx950 LDS.
+__device__ __forceinline__ int fsw(int r) { return (__builtin_popcount(r & 25) & 1) | ((__builtin_popcount(r & 14) & 1) << 1); }
+
+__device__ __forceinline__ void tile_of(const Params& p, int bid, int& mt, int& nt)
+{
+    const int full = p.m_full * p.n_tiles;
+    int f;
+    if ((full & 7) == 0 && (p.n_tiles & 7) == 0) {
+        const int x = bid & 7, j = bid >> 3;
+        const int per = full >> 3;
+        if (j >= per) {
+            mt = p.m_full;
+            nt = x * (p.n_tiles >> 3) + (j - per);
+            return;
+        }
+        f = x * per + j;
+    } else {
+        if (bid >= full) {
+            mt = p.m_full;
+            nt = bid - full;
+            return;
+        }
+        f = bid;
+    }
+    constexpr int GM = 4;
+    const int group_size = GM * p.n_tiles;
+    const int group = f / group_size;
+    const int first_m = group * GM;
+    const int gm = min(p.m_full - first_m, GM);
+    const int in_group = f - group * group_size;
+    mt = first_m + in_group % gm;
+    nt = in_group / gm;
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Phase boundary: LDS reads issued before it have returned, every wave of the
+// workgroup has arrived, and neither the compiler's scheduler nor its memory
+// model moves instructions across it. No release fence: that would also wait for
+// the stages still being loaded.
+__device__ __forceinline__ void phase_barrier()
+{
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// s_waitcnt vmcnt(n) for n in {0, 4, 8} (gfx9 encoding, other counters at max).
+__device__ __forceinline__ void wait_vm(int n)
+{
+    if (n >= 8) __builtin_amdgcn_s_waitcnt(8 | (7 << 4) | (15 << 8));
+    else if (n >= 4) __builtin_amdgcn_s_waitcnt(4 | (7 << 4) | (15 << 8));
+    else __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
+}
+
+template <typename T, typename OutT, int EPI, int MSUB>
+__device__ __forceinline__ void tile(const Params& p, int mt, int nt, uint8_t* smem)
+{
+    typedef typename Mfma<T>::vec vec8;
+    const int m0 = mt * BM, n0 = nt * BN;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int group = wave >> 2;              // waves 0-3 and 4-7: one of each per SIMD
+    const int wm = wave & 1, wn = wave >> 1;  // output sub-tile of this wave
+    const int lrow = lane & 31, lgrp = lane >> 5;
+
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.A), (short)0, p.a_bytes, kRsrcFlags);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.W), (short)0, p.w_bytes, kRsrcFlags);
+
+    // Direct loads: wave w fills rows [32w, 32w+32) of the A and W halves of a stage
+    // with two 1-KiB instructions each; lane l lands at bytes [16l, 16l+16), i.e.
+    // row (l >> 2), physical chunk l & 3 = logical chunk (l & 3) ^ fsw(row).
+    uint32_t a_src[2], w_src[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int row = wave * 32 + q * 16 + (lane >> 2);
+        const int c = (lane & 3) ^ fsw(row);
+        a_src[q] = (uint32_t)(((long)(m0 + row) * p.lda + c * 8) * 2);
+        w_src[q] = (uint32_t)(((long)(n0 + row) * p.ldw + c * 8) * 2);
+    }
+    const int nk = p.K / BK;
+    auto issue = [&](int kt) {
+        uint8_t* st = smem + (kt & (NS - 1)) * STAGE;
+        const int koff = kt * ROWB;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(st + (wave * 32 + q * 16) * ROWB), 16, a_src[q],
+                                                     koff, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(st + A_BYTES + (wave * 32 + q * 16) * ROWB), 16,
+                                                     w_src[q], koff, 0, 0);
+        }
+    };
+
+    uint32_t frag[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) frag[kk] = lrow * ROWB + (((2 * kk + lgrp) ^ fsw(lrow)) << 4);
+
+    f32x16 acc[MSUB][2];
+#pragma unroll
+    for (int i = 0; i < MSUB; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    vec8 af[2][MSUB], bf[2][2];
+    // Memory cluster: this wave's fragments of stage kt into registers.
+    auto read_frags = [&](int kt) {
+        const uint8_t* st = smem + (kt & (NS - 1)) * STAGE;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                bf[kk][j] = *reinterpret_cast<const vec8*>(st + A_BYTES + (wn * 64 + j * 32) * ROWB + frag[kk]);
+#pragma unroll
+            for (int i = 0; i < MSUB; ++i)
+                af[kk][i] = *reinterpret_cast<const vec8*>(st + (wm * 32 * MSUB + i * 32) * ROWB + frag[kk]);
+        }
+    };
+    // MFMA cluster on the registers.
+    auto mfma_cluster = [&]() {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int i = 0; i < MSUB; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = Mfma<T>::run(af[kk][i], bf[kk][j], acc[i][j]);
+    };
+    // Loads requested after stage s, per wave, when s must have landed: 4 x min(NS-2, nk-1-s).
+    auto wait_stage = [&](int s) { wait_vm(4 * min(NS - 2, nk - 1 - s)); };
+
+    // Prologue: request stages 0..NS-1, wait for stage 0 everywhere.
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+        if (s < nk) issue(s);
+    wait_vm(4 * min(NS - 1, nk - 1));
+    phase_barrier();
+
+    // Phase 2t+1: group 0 computes stage t, group 1 reads stage t and requests
+    // stage t-1+NS. Phase 2t+2: group 1 computes stage t, group 0 reads stage t+1
+    // and requests stage t+NS. Stage s is read in phases 2s and 2s+1, so its slot
+    // is refilled from phase 2s+2 on; it must land before phase 2s.
+    if (group == 0) {
+        read_frags(0);
+        phase_barrier();  // end of phase 0
+        for (int t = 0; t < nk; ++t) {
+            mfma_cluster();
+            if (t + 1 < nk) wait_stage(t + 1);
+            phase_barrier();  // end of phase 2t+1
+            if (t + 1 < nk) {
+                read_frags(t + 1);
+                if (t + NS < nk) issue(t + NS);
+            }
+            phase_barrier();  // end of phase 2t+2
+        }
+    } else {
+        phase_barrier();  // end of phase 0
+        for (int t = 0; t < nk; ++t) {
+            read_frags(t);
+            if (t >= 1 && t - 1 + NS < nk) issue(t - 1 + NS);
+            if (t + 1 < nk) wait_stage(t + 1);
+            phase_barrier();  // end of phase 2t+1
+            mfma_cluster();
+            phase_barrier();  // end of phase 2t+2
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < MSUB; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = m0 + wm * 32 * MSUB + i * 32 + 8 * (r >> 2) + 4 * lgrp + (r & 3);
+            if (m >= p.M) continue;
+            if (EPI == EPI_GEGLU) {
+                const int nout = (n0 + wn * 64) / 2 + lrow;
+                if (2 * nout < p.N)
+                    static_cast<OutT*>(p.C)[(size_t)m * p.ldc + nout] = OutT(acc[i][0][r] * gelu_erf(acc[i][1][r]));
+            } else {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int n = n0 + wn * 64 + j * 32 + lrow;
+                    if (n >= p.N) continue;
+                    float v = acc[i][j][r];
+                    if (EPI == EPI_STORE) {
+                        if (p.bias) v += p.bias[n];
+                        static_cast<OutT*>(p.C)[(size_t)m * p.ldc + n] = OutT(v);
+                    } else {
+                        const float rr = p.resid[(size_t)m * p.ld_resid + n];
+                        static_cast<float*>(p.C)[(size_t)m * p.ldc + n] = rr + p.gate[n] * v;
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <typename T, typename OutT, int EPI>
+__global__ void __launch_bounds__(512, 1) kernel(Params p)
+{
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
+    int mt, nt;
+    tile_of(p, blockIdx.x, mt, nt);
+    if (mt < p.m_full) tile<T, OutT, EPI, 4>(p, mt, nt, smem);
+    else if (p.tail_sub == 1) tile<T, OutT, EPI, 1>(p, mt, nt, smem);
+    else if (p.tail_sub == 2) tile<T, OutT, EPI, 2>(p, mt, nt, smem);
+    else tile<T, OutT, EPI, 3>(p, mt, nt, smem);
+}
+
+}  // namespace pingpong
+
+int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
+{
+    if (a.dtype == DT_F32 || a.K % pingpong::BK) return 1;
+    if (a.epilogue == EPI_STORE && a.c_dtype != DT_F32 && a.c_dtype != a.dtype) return -1;
+    if (a.epilogue == EPI_GEGLU && a.c_dtype != a.dtype) return -1;
+    // Buffer offsets are 32-bit: every staged row of every tile (rounded up to 256)
+    // must lie below 2^31 bytes; larger operands take the register-staged kernel.
+    const double ab = ((a.M + 255) / 256 * 256.0) * a.lda * 2, wb = ((a.N + 255) / 256 * 256.0) * a.ldw * 2;
+    if (ab >= 2147483647.0 || wb >= 2147483647.0) return 1;
+    pingpong::Params p{};
+    p.A = a.A; p.lda = a.lda; p.W = a.W; p.ldw = a.ldw; p.M = a.M; p.N = a.N; p.K = a.K;
+    p.C = a.C; p.ldc = a.ldc; p.bias = a.bias; p.resid = a.resid; p.ld_resid = a.ld_resid; p.gate = a.gate;
+    p.a_bytes = (uint32_t)((long)a.M * a.lda * 2);
+    p.w_bytes = (uint32_t)((long)a.N * a.ldw * 2);
+    p.m_full = a.M / pingpong::BM;
+    p.tail_sub = (a.M % pingpong::BM + 63) / 64;
+    p.n_tiles = (a.N + pingpong::BN - 1) / pingpong::BN;
+    const int tiles = (p.m_full + (p.tail_sub ? 1 : 0)) * p.n_tiles;
+    const dim3 grid(tiles), block(512);
+#define EHIP_PINGPONG(T)                                                                                            \
+    do {                                                                                                      \
+        if (a.epilogue == EPI_STORE) {                                                                        \
+            if (a.c_dtype == DT_F32) hipLaunchKernelGGL((pingpong::kernel<T, float, EPI_STORE>), grid, block, 0, s, p); \
+            else hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_STORE>), grid, block, 0, s, p);                     \
+        } else if (a.epilogue == EPI_GATE_RESID) {                                                            \
+            hipLaunchKernelGGL((pingpong::kernel<T, float, EPI_GATE_RESID>), grid, block, 0, s, p);                 \
+        } else {                                                                                              \
+            hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_GEGLU>), grid, block, 0, s, p);                          \
+        }                                                                                                     \
+    } while (0)
+    if (a.dtype == DT_F16) EHIP_PINGPONG(f16);
+    else EHIP_PINGPONG(bf16);
+#undef EHIP_PINGPONG
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : -int(e);
+}
+
+}  // namespace ehip

@@ -33,6 +33,9 @@ struct GemmArgs {
     const float* gate = nullptr;   // [N]
 };
 int gemm(const GemmArgs& a, hipStream_t stream);
+// The ping-pong 16-bit kernel (gemm16_pp.hip); returns 1 without launching when
+// the shape needs the register-staged kernel instead (operands of 2 GiB or more).
+int gemm16_pingpong(const GemmArgs& a, hipStream_t stream);
 
 // ---- flash SDPA ---------------------------------------------------------------
 struct SdpaArgs {
