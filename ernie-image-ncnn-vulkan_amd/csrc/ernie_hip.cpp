@@ -314,12 +314,9 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
     // rmsn_9 / rmsn_10 + rotary, in place on the Q and K column blocks
     {
         Timed t(ctx, P_ROPE, 0, dS * 2 * D * e * 2 + dS * 128 * 8);
-        rc = kernel_status(ctx, qk_norm_rope(ws.qkv, dt, S, H, 3L * D, static_cast<const float*>(w.norm_q.ptr), cos_t,
-                                             sin_t, s), "qk_norm_rope q");
-        if (rc) return rc;
-        rc = kernel_status(ctx, qk_norm_rope(static_cast<char*>(ws.qkv) + (size_t)D * esize(dt), dt, S, H, 3L * D,
-                                             static_cast<const float*>(w.norm_k.ptr), cos_t, sin_t, s),
-                           "qk_norm_rope k");
+        rc = kernel_status(ctx, qk_norm_rope_qk(ws.qkv, dt, S, H, H, 3L * D, D, static_cast<const float*>(w.norm_q.ptr),
+                                                static_cast<const float*>(w.norm_k.ptr), cos_t, sin_t, s),
+                           "qk_norm_rope");
         if (rc) return rc;
     }
     // sdpa_22

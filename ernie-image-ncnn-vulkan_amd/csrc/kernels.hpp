@@ -61,6 +61,10 @@ int layernorm_modulate(const float* x, const float* shift, const float* scale, i
 // `nheads` heads of `rows` tokens at x + t*row_stride + h*128.
 int qk_norm_rope(void* x, int dtype, int rows, int nheads, long row_stride, const float* gamma,
                  const float* cos_t, const float* sin_t, hipStream_t s);
+// The same for the q heads (nq, gamma gq, at the row start) and the k heads (nk,
+// gamma gk, at k_offset) of each row in one launch.
+int qk_norm_rope_qk(void* x, int dtype, int rows, int nq, int nk, long row_stride, long k_offset, const float* gq,
+                    const float* gk, const float* cos_t, const float* sin_t, hipStream_t s);
 int gelu_inplace(void* x, int dtype, size_t n, hipStream_t s);
 int residual_add(const void* a, int a_dtype, const void* b, int b_dtype, float* out, size_t n, hipStream_t s);
 int euler_step(const float* x, const float* v, float delta, size_t n, float* out, hipStream_t s);

@@ -46,43 +46,63 @@ __device__ __forceinline__ float block_sum(float v, float* red)
     return t;
 }
 
-// One 256-thread block per row; width % 4 == 0 and width <= 4 * 256 * kMaxPer.
+// One 256-thread block per row; width % 4 == 0 and width <= 4 * 256 * kMaxPer
+// (the layernorm kernel below keeps this shape).
 constexpr int kMaxPer = 4;  // float4 groups per thread -> width up to 4096
+
+// RMSNorm + modulate over rows of `width` values, one wave per row. Each
+// workgroup first folds gamma * (1 + scale) and shift into LDS, so every row
+// reads only its own values from memory (the per-column vectors are read once
+// per workgroup instead of once per row); no workgroup barrier inside the row
+// loop, the statistics are a single wave reduction.
+constexpr int kRowWaves = 4, kRowMaxWidth = 4096;
 template <typename TIn, typename TOut>
-__global__ void __launch_bounds__(256) rmsnorm_mod_kernel(const TIn* __restrict__ x, const float* __restrict__ gamma,
-                                                          const float* __restrict__ shift,
-                                                          const float* __restrict__ scale, int width, float eps,
-                                                          TOut* __restrict__ out)
+__global__ void __launch_bounds__(256) rmsnorm_rows_kernel(const TIn* __restrict__ x, const float* __restrict__ gamma,
+                                                           const float* __restrict__ shift,
+                                                           const float* __restrict__ scale, int rows, int width,
+                                                           int rows_per_block, float eps, TOut* __restrict__ out)
 {
-    __shared__ float red[4];
-    const size_t row = blockIdx.x;
-    const TIn* xr = x + row * width;
-    TOut* orow = out + row * width;
-    f32x4 v[kMaxPer];
-    float ss = 0.f;
+    __shared__ f32x4 mul4[kRowMaxWidth / 4], add4[kRowMaxWidth / 4];
+    const int w4 = width >> 2;
+    for (int c4 = threadIdx.x; c4 < w4; c4 += blockDim.x) {
+        f32x4 m, a;
 #pragma unroll
-    for (int i = 0; i < kMaxPer; ++i) {
-        const int c = (threadIdx.x + i * 256) * 4;
-        if (c < width) {
-            v[i] = Vec4<TIn>::load(xr + c);
-            ss += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
+        for (int e = 0; e < 4; ++e) {
+            const int c = 4 * c4 + e;
+            const float g = gamma ? gamma[c] : 1.0f;
+            m[e] = scale ? g * (scale[c] + 1.0f) : g;
+            a[e] = shift ? shift[c] : 0.0f;
         }
+        mul4[c4] = m;
+        add4[c4] = a;
     }
-    ss = block_sum(ss, red);
-    const float inv = 1.0f / sqrtf(ss / float(width) + eps);
+    __syncthreads();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r_end = min((blockIdx.x + 1) * rows_per_block, rows);
+    for (int r = blockIdx.x * rows_per_block + wave; r < r_end; r += kRowWaves) {
+        const TIn* xr = x + (size_t)r * width;
+        f32x4 v[kRowMaxWidth / 256];
+        float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < kMaxPer; ++i) {
-        const int c = (threadIdx.x + i * 256) * 4;
-        if (c < width) {
-            f32x4 y;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                float n = v[i][e] * inv;
-                if (gamma) n = n * gamma[c + e];
-                if (scale) n = n * (scale[c + e] + 1.0f) + shift[c + e];
-                y[e] = n;
+        for (int i = 0; i < kRowMaxWidth / 256; ++i) {
+            const int c4 = lane + 64 * i;
+            if (c4 < w4) {
+                v[i] = Vec4<TIn>::load(xr + 4 * c4);
+                ss += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
             }
-            Vec4<TOut>::store(orow + c, y);
+        }
+        const float inv = 1.0f / sqrtf(wave_sum(ss) / float(width) + eps);
+        TOut* orow = out + (size_t)r * width;
+#pragma unroll
+        for (int i = 0; i < kRowMaxWidth / 256; ++i) {
+            const int c4 = lane + 64 * i;
+            if (c4 < w4) {
+                const f32x4 m = mul4[c4], a = add4[c4];
+                f32x4 y;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) y[e] = (v[i][e] * inv) * m[e] + a[e];
+                Vec4<TOut>::store(orow + 4 * c4, y);
+            }
         }
     }
 }
@@ -128,26 +148,47 @@ __global__ void __launch_bounds__(256) layernorm_mod_kernel(const float* __restr
     }
 }
 
-// One wave per (token, head); lane d holds elements d and d + 64.
+// Per-head RMSNorm over 128 values + ERNIE rotary, in place, for one token row
+// per workgroup: the q heads (gamma gq, at the row start) and then the k heads
+// (gamma gk, at k_offset). A head is handled by 16 lanes, lane l owning values
+// [4l, 4l+4) and [64+4l, 64+4l+4), the rotary pairs (d, d+64); the token's cos /
+// sin and the two gammas are loaded once per lane and reused for every head.
 template <typename T>
-__global__ void __launch_bounds__(256) qk_norm_rope_kernel(T* __restrict__ x, int rows, int nheads, long row_stride,
-                                                           const float* __restrict__ gamma,
+__global__ void __launch_bounds__(256) qk_norm_rope_kernel(T* __restrict__ x, int nq, int nk, long row_stride,
+                                                           long k_offset, const float* __restrict__ gq,
+                                                           const float* __restrict__ gk,
                                                            const float* __restrict__ cos_t,
                                                            const float* __restrict__ sin_t)
 {
-    const long item = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (item >= (long)rows * nheads) return;
-    const int lane = threadIdx.x & 63;
-    const long row = item / nheads;
-    const int head = (int)(item - row * nheads);
-    T* v = x + row * row_stride + head * 128;
-    const float a = float(v[lane]), b = float(v[lane + 64]);
-    const float inv = 1.0f / sqrtf(wave_sum(a * a + b * b) / 128.f + 1e-6f);
-    const float na = a * inv * gamma[lane], nb = b * inv * gamma[lane + 64];
-    const float* c = cos_t + row * 128;
-    const float* s = sin_t + row * 128;
-    v[lane] = T(na * c[lane] - nb * s[lane]);
-    v[lane + 64] = T(nb * c[lane + 64] + na * s[lane + 64]);
+    const size_t t = blockIdx.x;
+    const int lane = threadIdx.x & 63, l = lane & 15;
+    const int slot = threadIdx.x >> 4;  // 16 heads in flight per workgroup
+    const int d = 4 * l;
+    const f32x4 c_lo = Vec4<float>::load(cos_t + t * 128 + d), c_hi = Vec4<float>::load(cos_t + t * 128 + 64 + d);
+    const f32x4 s_lo = Vec4<float>::load(sin_t + t * 128 + d), s_hi = Vec4<float>::load(sin_t + t * 128 + 64 + d);
+    T* row = x + t * row_stride;
+    for (int h = slot; h < nq + nk; h += 16) {
+        const bool is_k = h >= nq;
+        T* v = row + (is_k ? k_offset + (long)(h - nq) * 128 : (long)h * 128);
+        const float* g = is_k ? gk : gq;
+        const f32x4 a = Vec4<T>::load(v + d), b = Vec4<T>::load(v + 64 + d);
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ss += a[e] * a[e] + b[e] * b[e];
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 16);
+        const float inv = 1.0f / sqrtf(ss / 128.f + 1e-6f);
+        const f32x4 ga = Vec4<float>::load(g + d), gb = Vec4<float>::load(g + 64 + d);
+        f32x4 lo, hi;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float na = a[e] * inv * ga[e], nb = b[e] * inv * gb[e];
+            lo[e] = na * c_lo[e] - nb * s_lo[e];
+            hi[e] = nb * c_hi[e] + na * s_hi[e];
+        }
+        Vec4<T>::store(v + d, lo);
+        Vec4<T>::store(v + 64 + d, hi);
+    }
 }
 
 template <typename T>
@@ -281,15 +322,19 @@ template <typename TIn>
 int rms_dispatch_out(const TIn* x, const float* gamma, const float* shift, const float* scale, int rows, int width,
                      float eps, void* out, int odt, hipStream_t s)
 {
+    // Rows per workgroup: enough workgroups to cover the CUs several times over,
+    // with the per-column vectors staged once per workgroup.
+    const int rpb = rows >= 2048 ? 8 : (rows >= 512 ? 4 : 1);
+    const dim3 grid((rows + rpb - 1) / rpb), block(64 * kRowWaves);
     if (odt == DT_F32)
-        hipLaunchKernelGGL((rmsnorm_mod_kernel<TIn, float>), dim3(rows), dim3(256), 0, s, x, gamma, shift, scale,
-                           width, eps, static_cast<float*>(out));
+        hipLaunchKernelGGL((rmsnorm_rows_kernel<TIn, float>), grid, block, 0, s, x, gamma, shift, scale, rows, width,
+                           rpb, eps, static_cast<float*>(out));
     else if (odt == DT_F16)
-        hipLaunchKernelGGL((rmsnorm_mod_kernel<TIn, f16>), dim3(rows), dim3(256), 0, s, x, gamma, shift, scale, width,
-                           eps, static_cast<f16*>(out));
+        hipLaunchKernelGGL((rmsnorm_rows_kernel<TIn, f16>), grid, block, 0, s, x, gamma, shift, scale, rows, width,
+                           rpb, eps, static_cast<f16*>(out));
     else
-        hipLaunchKernelGGL((rmsnorm_mod_kernel<TIn, bf16>), dim3(rows), dim3(256), 0, s, x, gamma, shift, scale,
-                           width, eps, static_cast<bf16*>(out));
+        hipLaunchKernelGGL((rmsnorm_rows_kernel<TIn, bf16>), grid, block, 0, s, x, gamma, shift, scale, rows, width,
+                           rpb, eps, static_cast<bf16*>(out));
     return launch_status();
 }
 
@@ -298,7 +343,7 @@ int rms_dispatch_out(const TIn* x, const float* gamma, const float* shift, const
 int rmsnorm_modulate(const void* x, int xdt, const float* gamma, const float* shift, const float* scale, int rows,
                      int width, float eps, void* out, int odt, hipStream_t s)
 {
-    if (!x || !out || rows < 1 || width < 4 || width % 4 || width > 1024 * kMaxPer) return -1;
+    if (!x || !out || rows < 1 || width < 4 || width % 4 || width > kRowMaxWidth) return -1;
     if (!valid_dt(xdt) || !valid_dt(odt) || (!shift) != (!scale)) return -1;
     if (xdt == DT_F32) return rms_dispatch_out(static_cast<const float*>(x), gamma, shift, scale, rows, width, eps, out, odt, s);
     if (xdt == DT_F16) return rms_dispatch_out(static_cast<const f16*>(x), gamma, shift, scale, rows, width, eps, out, odt, s);
@@ -322,23 +367,34 @@ int layernorm_modulate(const float* x, const float* shift, const float* scale, i
     return launch_status();
 }
 
+int qk_norm_rope_qk(void* x, int dt, int rows, int nq, int nk, long row_stride, long k_offset, const float* gq,
+                    const float* gk, const float* cos_t, const float* sin_t, hipStream_t s)
+{
+    if (!x || !gq || (nk && !gk) || !cos_t || !sin_t || rows < 1 || nq < 0 || nk < 0 || nq + nk < 1) return -1;
+    if (row_stride < (long)nq * 128 || (nk && (k_offset < (long)nq * 128 || row_stride < k_offset + (long)nk * 128)))
+        return -1;
+    // Four-value vector accesses: 16-byte (FP32) or 8-byte (16-bit) alignment of every head.
+    const uintptr_t align = dt == DT_F32 ? 16 : 8;
+    const long vec = dt == DT_F32 ? 4 : 4;
+    if ((reinterpret_cast<uintptr_t>(x) % align) || row_stride % vec || k_offset % vec) return -1;
+    const dim3 grid((unsigned)rows), block(256);
+    if (dt == DT_F32)
+        hipLaunchKernelGGL(qk_norm_rope_kernel<float>, grid, block, 0, s, static_cast<float*>(x), nq, nk, row_stride,
+                           k_offset, gq, gk, cos_t, sin_t);
+    else if (dt == DT_F16)
+        hipLaunchKernelGGL(qk_norm_rope_kernel<f16>, grid, block, 0, s, static_cast<f16*>(x), nq, nk, row_stride,
+                           k_offset, gq, gk, cos_t, sin_t);
+    else if (dt == DT_BF16)
+        hipLaunchKernelGGL(qk_norm_rope_kernel<bf16>, grid, block, 0, s, static_cast<bf16*>(x), nq, nk, row_stride,
+                           k_offset, gq, gk, cos_t, sin_t);
+    else return -1;
+    return launch_status();
+}
+
 int qk_norm_rope(void* x, int dt, int rows, int nheads, long row_stride, const float* gamma, const float* cos_t,
                  const float* sin_t, hipStream_t s)
 {
-    if (!x || !gamma || !cos_t || !sin_t || rows < 1 || nheads < 1 || row_stride < (long)nheads * 128) return -1;
-    const long items = (long)rows * nheads;
-    const dim3 grid((unsigned)((items + 3) / 4)), block(256);
-    if (dt == DT_F32)
-        hipLaunchKernelGGL(qk_norm_rope_kernel<float>, grid, block, 0, s, static_cast<float*>(x), rows, nheads,
-                           row_stride, gamma, cos_t, sin_t);
-    else if (dt == DT_F16)
-        hipLaunchKernelGGL(qk_norm_rope_kernel<f16>, grid, block, 0, s, static_cast<f16*>(x), rows, nheads, row_stride,
-                           gamma, cos_t, sin_t);
-    else if (dt == DT_BF16)
-        hipLaunchKernelGGL(qk_norm_rope_kernel<bf16>, grid, block, 0, s, static_cast<bf16*>(x), rows, nheads,
-                           row_stride, gamma, cos_t, sin_t);
-    else return -1;
-    return launch_status();
+    return qk_norm_rope_qk(x, dt, rows, nheads, 0, row_stride, 0, gamma, nullptr, cos_t, sin_t, s);
 }
 
 int gelu_inplace(void* x, int dt, size_t n, hipStream_t s)
