@@ -49,6 +49,9 @@ struct SdpaArgs {
     float scale = 0.f;
 };
 int sdpa(const SdpaArgs& a, hipStream_t stream);
+// The head_dim-128 16-bit kernel (sdpa16_dl.hip); returns 1 without launching for
+// problems the general kernel in sdpa.hip has to take.
+int sdpa16_d128(const SdpaArgs& a, hipStream_t stream);
 
 // ---- bandwidth-bound kernels ------------------------------------------------------
 // out = RMSNorm(x) * gamma [* (1 + scale) + shift]; FP32 statistics.

@@ -5,6 +5,8 @@
 // and GQA (kv head = h / (heads / kv_heads)). No score matrix is materialised, so
 // the reference's query-row chunking (set_attention_query_rows) is unnecessary.
 //
+// 16-bit problems with head_dim 128 and no per-query mask go to sdpa16_dl.hip; the
+// kernels below take the rest (FP32, other head sizes, per-query masks).
 // Work split: one workgroup = 4 waves = 128 queries of one head; K/V tiles of 64
 // keys are staged in double-buffered LDS. Each wave computes S^T = K Q^T for its
 // 32 queries (MFMA M = keys, N = queries), so every lane ends up owning one query
@@ -471,6 +473,8 @@ int sdpa(const SdpaArgs& a, hipStream_t s)
     const dim3 block(256);
     if (a.dtype == DT_F32) {
         hipLaunchKernelGGL(sdpa32_kernel, dim3((a.sq + BQ - 1) / BQ, a.heads), block, 0, s, p);
+    } else if (const int rc = sdpa16_d128(a, s); rc != 1) {
+        return rc;
     } else {
         const bool fast = p.vec_ok && a.d == 128;
         const int mm = !a.mask ? MASK_NONE : (a.mask_rows > 1 ? MASK_PER_QUERY : MASK_ROW);

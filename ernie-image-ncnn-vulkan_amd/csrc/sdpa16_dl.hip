@@ -1,0 +1,318 @@
+// SPDX-License-Identifier: MIT
+// Flash SDPA for 16-bit operands with head_dim 128 on gfx950: the path the DiT
+// block takes (ErnieSDPA, src/ernie_attention.cpp:35-233; sdpa_22 in
+// block.ncnn.param line 58) with no mask or one additive mask row broadcast over
+// the queries (src/ernie_attention.cpp:201-221), plus a valid-key bound.
+//
+//   * One workgroup = 4 waves = 128 queries of one head; each wave holds its 32
+//     queries' Q fragments in registers and computes S^T = K Q^T, so each lane owns
+//     one query column (softmax statistics need one lane^32 exchange) and the
+//     probabilities are already the B operand of O^T = V^T P^T.
+//   * K and V tiles (64 keys) reach LDS through direct global->LDS loads into a
+//     two-stage ring: no VGPR staging, no transpose on the way in. Key rows at or
+//     past the valid-key bound lie past the buffer range and load as zeros.
+//   * V^T fragments come from ds_read_b64_tr_b16: within each 16-lane group, lane
+//     i receives the (i % 4)-th 16-bit value at the addresses of lanes 4e + i/4
+//     (e = 0..3), so lanes pointing at 4 consecutive key rows deliver 4 keys of
+//     one head-dim column per lane.
+//   * K rows are chunk-swizzled by (key & 15), V rows by 2 (key & 7) (32-byte
+//     pairs kept together for the transposing reads): both measured conflict-free
+//     for these read patterns.
+//   * Online softmax in the log2 domain; the running offset is raised only when a
+//     tile's maximum exceeds it by more than 8, so the O / l rescale is almost
+//     always skipped (exact: O and l share the offset).
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace ehip {
+namespace sdl {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int BQ = 128, BKV = 64, D = 128;
+constexpr int ROWB = D * 2;                 // 256 bytes per staged key row
+constexpr int KV_BYTES = BKV * ROWB;        // 16 KiB
+constexpr int STAGE = 2 * KV_BYTES + BKV * 4;  // K, V, mask row
+constexpr uint32_t kRsrcFlags = 0x00020000;
+constexpr float kRescaleSlack = 8.0f;
+
+struct Params {
+    const void* q; const void* k; const void* v; void* o;
+    int heads, group, sq, sk, kv_end;
+    long q_hs, q_rs, k_hs, k_rs, v_hs, v_rs, o_hs, o_rs;
+    const float* mask; long mask_hs;
+    float scale_log2;
+};
+
+template <typename T> struct Mfma;
+template <> struct Mfma<f16> {
+    typedef f16x8 vec;
+    typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 tr4;
+    static __device__ __forceinline__ f32x16 run(vec a, vec b, f32x16 c)
+    { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
+    static __device__ __forceinline__ u32x2 tr(const void* p)
+    {
+        return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) tr4*)p));
+    }
+};
+template <> struct Mfma<bf16> {
+    typedef bf16x8 vec;
+    typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 tr4;
+    static __device__ __forceinline__ f32x16 run(vec a, vec b, f32x16 c)
+    { return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0); }
+    static __device__ __forceinline__ u32x2 tr(const void* p)
+    {
+        return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) tr4*)p));
+    }
+};
+
+// K rows: 16-byte chunk c of key row r at physical chunk c ^ (r & 15).
+// V rows: chunk c at c ^ 2(r & 7), which keeps each 32-byte pair together for the
+// transposing reads (4 keys x 32 bytes per 16-lane group).
+__device__ __forceinline__ int kswz(int r) { return r & 15; }
+__device__ __forceinline__ int vswz(int r) { return 2 * (r & 7); }
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Workgroup barrier without the release fence of __syncthreads() (that fence would
+// also wait for the tile still being loaded): LDS reads issued before it have
+// returned and the memory clobber keeps LDS accesses on their side.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <typename T, bool MASKROW>
+__global__ void __launch_bounds__(256, 2) kernel(Params p)
+{
+    typedef typename Mfma<T>::vec vec8;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+
+    const int qtiles = (p.sq + BQ - 1) / BQ;
+    const int total = qtiles * p.heads;
+    int logical = blockIdx.x;
+    if ((total & 7) == 0) logical = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
+    const int h = logical / qtiles;
+    const int q_base = (logical - h * qtiles) * BQ;
+    const int kvh = h / p.group;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lrow = lane & 31, g = lane >> 5;
+    const int my_q = q_base + wave * 32 + lrow;
+
+    const T* Q = static_cast<const T*>(p.q) + (size_t)h * p.q_hs;
+    vec8 qf[8];
+    {
+        const T* qrow = Q + (size_t)min(my_q, p.sq - 1) * p.q_rs;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) qf[s] = *reinterpret_cast<const vec8*>(qrow + (2 * s + g) * 8);
+    }
+
+    // Key rows past kv_end lie past the buffer range and load as zeros.
+    const T* Kh = static_cast<const T*>(p.k) + (size_t)kvh * p.k_hs;
+    const T* Vh = static_cast<const T*>(p.v) + (size_t)kvh * p.v_hs;
+    const uint32_t k_bytes = (uint32_t)(((long)(p.kv_end - 1) * p.k_rs + D) * 2);
+    const uint32_t v_bytes = (uint32_t)(((long)(p.kv_end - 1) * p.v_rs + D) * 2);
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(Kh), (short)0, k_bytes, kRsrcFlags);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(Vh), (short)0, v_bytes, kRsrcFlags);
+    __amdgpu_buffer_rsrc_t rm;
+    if constexpr (MASKROW)
+        rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.mask + (size_t)h * p.mask_hs), (short)0,
+                                               (uint32_t)(p.sk * 4), kRsrcFlags);
+
+    // Direct loads: wave w fills key rows [16w, 16w+16) of the K and V tiles with
+    // four 1-KiB instructions each (4 rows x 256 bytes); lane l lands at row l >> 4,
+    // physical chunk l & 15.
+    uint32_t k_src[4], v_src[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int row = wave * 16 + q * 4 + (lane >> 4);
+        k_src[q] = (uint32_t)(((long)row * p.k_rs * 2) + (((lane & 15) ^ kswz(row)) << 4));
+        v_src[q] = (uint32_t)(((long)row * p.v_rs * 2) + (((lane & 15) ^ vswz(row)) << 4));
+    }
+    const uint32_t k_tile = (uint32_t)(BKV * p.k_rs * 2), v_tile = (uint32_t)(BKV * p.v_rs * 2);
+    auto issue = [&](int it, int slot) {
+        uint8_t* st = smem + slot * STAGE;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr_t)(st + (wave * 16 + q * 4) * ROWB), 16, k_src[q],
+                                                     it * k_tile, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_ptr_t)(st + KV_BYTES + (wave * 16 + q * 4) * ROWB), 16,
+                                                     v_src[q], it * v_tile, 0, 0);
+        }
+        if constexpr (MASKROW) {
+            if (wave == 0)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_ptr_t)(st + 2 * KV_BYTES), 4, lane * 4,
+                                                         it * BKV * 4, 0, 0);
+        }
+    };
+
+    // K fragment (A of S^T = K Q^T): key 32t + lrow, logical chunk 2s + g.
+    uint32_t k_rd[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int key = 32 * t + lrow;
+        k_rd[t] = key * ROWB;
+    }
+    const int ksw = kswz(lrow);  // same for key 32t + lrow
+    // V^T fragment (A of O^T = V^T P^T) by transposing reads: 16-lane group G = lane >> 4
+    // (k-half g = G >> 1, d half 16 (G & 1)), lane j = lane & 15 points at key
+    // kb + (j >> 2), values d0 + 16 (G & 1) + 4 (j & 3) .. + 3.
+    const int G = lane >> 4, j = lane & 15;
+    const int v_key_off = 4 * (G >> 1) + (j >> 2);
+    const int v_d = 16 * (G & 1) + 4 * (j & 3);
+
+    f32x16 oacc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[t][r] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;
+    const float c = p.scale_log2;
+
+    const int ntiles = (p.kv_end + BKV - 1) / BKV;
+    issue(0, 0);
+    for (int it = 0; it < ntiles; ++it) {
+        const int buf = it & 1;
+        const int kv0 = it * BKV;
+        __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // this wave's loads of tile it have landed
+        lds_barrier();                                         // ... and every wave's; tile it-1 is consumed
+        if (it + 1 < ntiles) issue(it + 1, buf ^ 1);
+        const uint8_t* st = smem + buf * STAGE;
+
+        f32x16 sacc[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sacc[t][r] = 0.f;
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const vec8 kf = *reinterpret_cast<const vec8*>(st + k_rd[t] + (((2 * s + g) ^ ksw) << 4));
+                sacc[t] = Mfma<T>::run(kf, qf[s], sacc[t]);
+            }
+        }
+        const bool partial = kv0 + BKV > p.kv_end;
+        if (MASKROW || partial) {
+            const float* ms = reinterpret_cast<const float*>(st + 2 * KV_BYTES);
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int kk = 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
+                    float v = sacc[t][r] * c;
+                    if constexpr (MASKROW) v += ms[kk] * kLog2e;
+                    sacc[t][r] = kv0 + kk < p.kv_end ? v : -INFINITY;
+                }
+        }
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) tmax = fmaxf(tmax, fmaxf(sacc[t][r], sacc[t][r + 1]));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        if (!(MASKROW || partial)) tmax *= c;
+        const bool raise = tmax > m_run + kRescaleSlack;
+        if (__any(raise)) {
+            const float m_new = raise ? tmax : m_run;
+            const float alpha = m_run == -INFINITY ? 0.f : exp2f(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+            m_run = m_new;
+        }
+        const float m_use = m_run == -INFINITY ? 0.f : m_run;
+        float psum = 0.f;
+        vec8 pf[2][2];
+        if (MASKROW || partial) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float pv = exp2f(sacc[t][r] - m_use);
+                    psum += pv;
+                    pf[t][r >> 3][r & 7] = T(pv);
+                }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float pv = exp2f(__builtin_fmaf(sacc[t][r], c, -m_use));
+                    psum += pv;
+                    pf[t][r >> 3][r & 7] = T(pv);
+                }
+        }
+        psum += __shfl_xor(psum, 32, 64);
+        l_run += psum;
+
+        // O^T += V^T P^T; P's register r of (t, hh) is key 32t + 16hh + 8(r/4 & 1) + 4g + r%4.
+        const uint8_t* vt = st + KV_BYTES;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int kb = 32 * t + 16 * hh;
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) {
+                    const int d = 32 * dt + v_d;
+                    const int k_lo = kb + v_key_off, k_hi = kb + 8 + v_key_off;
+                    const u32x2 lo = Mfma<T>::tr(vt + k_lo * ROWB + (((d >> 3) ^ vswz(k_lo)) << 4) + (d & 7) * 2);
+                    const u32x2 hi = Mfma<T>::tr(vt + k_hi * ROWB + (((d >> 3) ^ vswz(k_hi)) << 4) + (d & 7) * 2);
+                    const u32x4 packed = {lo[0], lo[1], hi[0], hi[1]};
+                    oacc[dt] = Mfma<T>::run(__builtin_bit_cast(vec8, packed), pf[t][hh], oacc[dt]);
+                }
+            }
+    }
+
+    if (my_q >= p.sq) return;
+    const float inv = 1.f / l_run;
+    T* orow = static_cast<T*>(p.o) + (size_t)h * p.o_hs + (size_t)my_q * p.o_rs;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+            const int d0 = 32 * dt + 8 * rq + 4 * g;
+            union { u32x2 u; T e[4]; } pk;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) pk.e[e] = T(oacc[dt][4 * rq + e] * inv);
+            *reinterpret_cast<u32x2*>(orow + d0) = pk.u;
+        }
+}
+
+}  // namespace sdl
+
+// Returns 1 without launching when the problem is not one this kernel takes
+// (FP32, head_dim != 128, per-query masks, unaligned strides, >= 2 GiB K/V spans).
+int sdpa16_d128(const SdpaArgs& a, hipStream_t s)
+{
+    if (a.dtype == DT_F32 || a.d != 128) return 1;
+    if (a.mask && a.mask_rows != 1) return 1;
+    const long vec = 8;
+    const uintptr_t bases = reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.k) |
+                            reinterpret_cast<uintptr_t>(a.v) | reinterpret_cast<uintptr_t>(a.o);
+    if (bases % 16 || a.q_hs % vec || a.q_rs % vec || a.k_hs % vec || a.k_rs % vec || a.v_hs % vec || a.v_rs % vec ||
+        a.o_hs % vec || a.o_rs % vec)
+        return 1;
+    const int kv_end = a.valid_keys > 0 ? a.valid_keys : a.sk;
+    const int ntiles = (kv_end + sdl::BKV - 1) / sdl::BKV;
+    if ((double)ntiles * sdl::BKV * (double)std::max(a.k_rs, a.v_rs) * 2 >= 2147483647.0) return 1;
+    sdl::Params p{};
+    p.q = a.q; p.k = a.k; p.v = a.v; p.o = a.o;
+    p.heads = a.heads; p.group = a.heads / a.kv_heads; p.sq = a.sq; p.sk = a.sk; p.kv_end = kv_end;
+    p.q_hs = a.q_hs; p.q_rs = a.q_rs; p.k_hs = a.k_hs; p.k_rs = a.k_rs;
+    p.v_hs = a.v_hs; p.v_rs = a.v_rs; p.o_hs = a.o_hs; p.o_rs = a.o_rs;
+    p.mask = a.mask;
+    p.mask_hs = a.mask && a.mask_heads > 1 ? (long)a.sk : 0;
+    const float scale = a.scale > 0.f ? a.scale : 1.f / sqrtf(128.f);
+    p.scale_log2 = scale * sdl::kLog2e;
+    const dim3 grid(((a.sq + sdl::BQ - 1) / sdl::BQ) * a.heads), block(256);
+    if (a.dtype == DT_F16) {
+        if (a.mask) hipLaunchKernelGGL((sdl::kernel<f16, true>), grid, block, 0, s, p);
+        else hipLaunchKernelGGL((sdl::kernel<f16, false>), grid, block, 0, s, p);
+    } else {
+        if (a.mask) hipLaunchKernelGGL((sdl::kernel<bf16, true>), grid, block, 0, s, p);
+        else hipLaunchKernelGGL((sdl::kernel<bf16, false>), grid, block, 0, s, p);
+    }
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : -int(e);
+}
+
+}  // namespace ehip
