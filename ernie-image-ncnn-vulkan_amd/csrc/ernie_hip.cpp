@@ -62,6 +62,7 @@ struct ernie_hip_ctx {
     DeviceBuffer staging;  // FP32 upload staging
     DeviceBuffer head_ws;  // head intermediates
     DeviceBuffer dit_act;  // run_dit activations: x [S][dim], c, mods
+    DeviceBuffer split_ws;   // GEMM tail-row split-K partial sums
     // Event timing.
     bool profiling = false;
     std::vector<hipEvent_t> event_pool;
@@ -284,6 +285,22 @@ int block_workspace(ernie_hip_ctx* ctx, int S, int dim, int ffn, int dtype, Bloc
     return ERNIE_OK;
 }
 
+// Split-K scratch of the block GEMMs' tail row of tiles (S % 256 rows): at most 256
+// items of (64 * tail_sub) x 256 FP32 partials.
+constexpr int kSplitItems = 256;
+
+int split_workspace(ernie_hip_ctx* ctx, int S, GemmArgs& g)
+{
+    const int tail_sub = (S % 256 + 63) / 64;
+    if (!tail_sub) return ERNIE_OK;
+    const size_t bytes = (size_t)kSplitItems * 64 * tail_sub * 256 * sizeof(float);
+    const int rc = dev_alloc(ctx, ctx->split_ws, bytes, "gemm split workspace");
+    if (rc) return rc;
+    g.split_ws = ctx->split_ws.ptr;
+    g.split_ws_bytes = ctx->split_ws.bytes;
+    return ERNIE_OK;
+}
+
 int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, float* out, const float* mods,
                   const float* cos_t, const float* sin_t, const float* mask, int valid_keys, int S)
 {
@@ -307,6 +324,8 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
         GemmArgs g;
         g.A = ws.h; g.lda = D; g.W = w.wqkv.ptr; g.ldw = D; g.M = S; g.N = 3 * D; g.K = D; g.dtype = dt;
         g.epilogue = EPI_STORE; g.C = ws.qkv; g.ldc = 3 * D; g.c_dtype = dt;
+        rc = split_workspace(ctx, S, g);
+        if (rc) return rc;
         Timed t(ctx, P_QKV, 2.0 * dS * 3 * D * D, gemm_bytes(dS, 3.0 * D, D, e, e));
         rc = kernel_status(ctx, gemm(g, s), "gemm qkv");
         if (rc) return rc;
@@ -338,6 +357,8 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
         g.A = ws.attn; g.lda = D; g.W = w.wo.ptr; g.ldw = D; g.M = S; g.N = D; g.K = D; g.dtype = dt;
         g.epilogue = EPI_GATE_RESID; g.C = ws.x1; g.ldc = D; g.c_dtype = ERNIE_DTYPE_FP32; g.resid = x; g.ld_resid = D;
         g.gate = gate_sa;
+        rc = split_workspace(ctx, S, g);
+        if (rc) return rc;
         Timed t(ctx, P_OUT, 2.0 * dS * D * D, gemm_bytes(dS, D, D, e, 8));
         rc = kernel_status(ctx, gemm(g, s), "gemm out");
         if (rc) return rc;
@@ -354,6 +375,8 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
         GemmArgs g;
         g.A = ws.h; g.lda = D; g.W = w.w_ug.ptr; g.ldw = D; g.M = S; g.N = 2 * F; g.K = D; g.dtype = dt;
         g.epilogue = EPI_GEGLU; g.C = ws.p; g.ldc = F; g.c_dtype = dt;
+        rc = split_workspace(ctx, S, g);
+        if (rc) return rc;
         Timed t(ctx, P_UG, 2.0 * dS * 2 * F * D, gemm_bytes(dS, 2.0 * F, D, e, 0) + dS * F * e);
         rc = kernel_status(ctx, gemm(g, s), "gemm up/gate");
         if (rc) return rc;
@@ -364,6 +387,8 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
         g.A = ws.p; g.lda = F; g.W = w.w_down.ptr; g.ldw = F; g.M = S; g.N = D; g.K = F; g.dtype = dt;
         g.epilogue = EPI_GATE_RESID; g.C = out; g.ldc = D; g.c_dtype = ERNIE_DTYPE_FP32; g.resid = ws.x1; g.ld_resid = D;
         g.gate = gate_mlp;
+        rc = split_workspace(ctx, S, g);
+        if (rc) return rc;
         Timed t(ctx, P_DOWN, 2.0 * dS * D * F, gemm_bytes(dS, D, F, e, 8));
         rc = kernel_status(ctx, gemm(g, s), "gemm down");
         if (rc) return rc;
@@ -488,6 +513,7 @@ void ernie_hip_destroy(ernie_hip_ctx* ctx)
     dev_free(ctx->staging);
     dev_free(ctx->head_ws);
     dev_free(ctx->dit_act);
+    dev_free(ctx->split_ws);
     for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;

@@ -23,7 +23,13 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+#include <algorithm>
+
 namespace ehip {
+namespace {
+// Target number of tail-row items: one per CU of an MI355X.
+constexpr int kSplitTargetItems = 256;
+}
 namespace pingpong {
 
 constexpr int BM = 256, BN = 256, BK = 32, NS = 4;
@@ -42,7 +48,41 @@ struct Params {
     const float* resid; long ld_resid;
     const float* gate;
     uint32_t a_bytes, w_bytes;
+    int split;        // K parts per tail tile (1 = no split)
+    float* part;      // [n_tiles][split][64 * tail_sub][BN] FP32 partial sums of split tail tiles
 };
+
+// Sums the K parts of the split tail tiles and applies the epilogue: one thread per
+// output column (GEGLU: per up/gate column pair) and tail row.
+template <typename OutT, int EPI>
+__global__ void __launch_bounds__(256) split_reduce_kernel(Params p)
+{
+    const int rows = 64 * p.tail_sub;
+    const int cols = EPI == EPI_GEGLU ? p.N / 2 : p.N;
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long)rows * cols) return;
+    const int rl = (int)(idx / cols), c = (int)(idx - (long)rl * cols);
+    const int m = p.m_full * BM + rl;
+    if (m >= p.M) return;
+    // Column n of the tile grid; GEGLU output column c holds up column (c / 32) * 64 + c % 32
+    // and gate column + 32 of the interleaved W rows.
+    const int n = EPI == EPI_GEGLU ? (c / 32) * 64 + (c % 32) : c;
+    const int nt = n / BN, cl = n - nt * BN;
+    const float* base = p.part + (size_t)nt * p.split * rows * BN + (size_t)rl * BN + cl;
+    float v = 0.f, g = 0.f;
+    for (int q = 0; q < p.split; ++q) {
+        v += base[(size_t)q * rows * BN];
+        if (EPI == EPI_GEGLU) g += base[(size_t)q * rows * BN + 32];
+    }
+    if (EPI == EPI_GEGLU) {
+        static_cast<OutT*>(p.C)[(size_t)m * p.ldc + c] = OutT(v * gelu_erf(g));
+    } else if (EPI == EPI_STORE) {
+        if (p.bias) v += p.bias[n];
+        static_cast<OutT*>(p.C)[(size_t)m * p.ldc + n] = OutT(v);
+    } else {
+        static_cast<float*>(p.C)[(size_t)m * p.ldc + n] = p.resid[(size_t)m * p.ld_resid + n] + p.gate[n] * v;
+    }
+}
 
 template <typename T> struct Mfma;
 template <> struct Mfma<f16> {
@@ -61,23 +101,33 @@ template <> struct Mfma<bf16> {
 // low five row bits for this fragment read pattern, measured on gfx950 LDS.
 __device__ __forceinline__ int fsw(int r) { return (__builtin_popcount(r & 25) & 1) | ((__builtin_popcount(r & 14) & 1) << 1); }
 
-__device__ __forceinline__ void tile_of(const Params& p, int bid, int& mt, int& nt)
+// Tile order: workgroup b runs on XCD b % 8. Each XCD gets a contiguous share of
+// the full-height tiles (walked 4 M tiles per N sweep) and then its share of the
+// tail-row items (a tail tile split into `split` K parts), so the short items run
+// last and spread over all XCDs; the parts of one tile stay on one XCD.
+__device__ __forceinline__ void tile_of(const Params& p, int bid, int& mt, int& nt, int& part)
 {
     const int full = p.m_full * p.n_tiles;
+    const int tail_items = p.tail_sub ? p.n_tiles * p.split : 0;
+    part = 0;
     int f;
-    if ((full & 7) == 0 && (p.n_tiles & 7) == 0) {
+    if ((full & 7) == 0 && (tail_items & 7) == 0) {
         const int x = bid & 7, j = bid >> 3;
         const int per = full >> 3;
         if (j >= per) {
+            const int u = x * (tail_items >> 3) + (j - per);
             mt = p.m_full;
-            nt = x * (p.n_tiles >> 3) + (j - per);
+            nt = u / p.split;
+            part = u - nt * p.split;
             return;
         }
         f = x * per + j;
     } else {
         if (bid >= full) {
+            const int u = bid - full;
             mt = p.m_full;
-            nt = bid - full;
+            nt = u / p.split;
+            part = u - nt * p.split;
             return;
         }
         f = bid;
@@ -114,7 +164,7 @@ __device__ __forceinline__ void wait_vm(int n)
 }
 
 template <typename T, typename OutT, int EPI, int MSUB>
-__device__ __forceinline__ void tile(const Params& p, int mt, int nt, uint8_t* smem)
+__device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, uint8_t* smem)
 {
     typedef typename Mfma<T>::vec vec8;
     const int m0 = mt * BM, n0 = nt * BN;
@@ -138,10 +188,14 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, uint8_t* s
         a_src[q] = (uint32_t)(((long)(m0 + row) * p.lda + c * 8) * 2);
         w_src[q] = (uint32_t)(((long)(n0 + row) * p.ldw + c * 8) * 2);
     }
-    const int nk = p.K / BK;
+    // K steps of this item: all of them, or part `part` of `split` for a tail tile.
+    const int nk_all = p.K / BK;
+    const int parts = mt == p.m_full ? p.split : 1;
+    const int kt0 = (int)((long)nk_all * part / parts);
+    const int nk = (int)((long)nk_all * (part + 1) / parts) - kt0;
     auto issue = [&](int kt) {
         uint8_t* st = smem + (kt & (NS - 1)) * STAGE;
-        const int koff = kt * ROWB;
+        const int koff = (kt0 + kt) * ROWB;
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(st + (wave * 32 + q * 16) * ROWB), 16, a_src[q],
@@ -225,6 +279,23 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, uint8_t* s
         }
     }
 
+    if (p.split > 1 && mt == p.m_full) {
+        // Split tail tile: store this part's FP32 partial; split_reduce_kernel, the
+        // next launch on the stream, adds the parts and applies the epilogue.
+        const int rows = 64 * p.tail_sub;
+        float* base = p.part + ((size_t)nt * p.split + part) * rows * BN;
+#pragma unroll
+        for (int i = 0; i < MSUB; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int rl = wm * 32 * MSUB + i * 32 + 8 * (r >> 2) + 4 * lgrp + (r & 3);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) base[(size_t)rl * BN + wn * 64 + j * 32 + lrow] = acc[i][j][r];
+            }
+        return;
+    }
+
+    // Accumulator (32x32 f32): lane -> column lane%32; register r -> row 8(r/4) + 4(lane/32) + r%4.
 #pragma unroll
     for (int i = 0; i < MSUB; ++i) {
 #pragma unroll
@@ -258,12 +329,12 @@ template <typename T, typename OutT, int EPI>
 __global__ void __launch_bounds__(512, 1) kernel(Params p)
 {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
-    int mt, nt;
-    tile_of(p, blockIdx.x, mt, nt);
-    if (mt < p.m_full) tile<T, OutT, EPI, 4>(p, mt, nt, smem);
-    else if (p.tail_sub == 1) tile<T, OutT, EPI, 1>(p, mt, nt, smem);
-    else if (p.tail_sub == 2) tile<T, OutT, EPI, 2>(p, mt, nt, smem);
-    else tile<T, OutT, EPI, 3>(p, mt, nt, smem);
+    int mt, nt, part;
+    tile_of(p, blockIdx.x, mt, nt, part);
+    if (mt < p.m_full) tile<T, OutT, EPI, 4>(p, mt, nt, part, smem);
+    else if (p.tail_sub == 1) tile<T, OutT, EPI, 1>(p, mt, nt, part, smem);
+    else if (p.tail_sub == 2) tile<T, OutT, EPI, 2>(p, mt, nt, part, smem);
+    else tile<T, OutT, EPI, 3>(p, mt, nt, part, smem);
 }
 
 }  // namespace pingpong
@@ -285,7 +356,18 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     p.m_full = a.M / pingpong::BM;
     p.tail_sub = (a.M % pingpong::BM + 63) / 64;
     p.n_tiles = (a.N + pingpong::BN - 1) / pingpong::BN;
-    const int tiles = (p.m_full + (p.tail_sub ? 1 : 0)) * p.n_tiles;
+    // Split the tail row of tiles along K so that its items cover the CUs once
+    // (at most 16 parts, at least 4 K steps each), within the caller's workspace.
+    p.split = 1;
+    if (p.tail_sub && p.m_full && a.split_ws) {
+        const size_t per_part = (size_t)p.n_tiles * 64 * p.tail_sub * pingpong::BN * sizeof(float);
+        int sp = std::min(16, std::max(1, kSplitTargetItems / p.n_tiles));
+        sp = std::min(sp, std::max(1, a.K / pingpong::BK / 4));
+        while (sp > 1 && (size_t)sp * per_part > a.split_ws_bytes) --sp;
+        p.split = sp;
+        p.part = static_cast<float*>(a.split_ws);
+    }
+    const int tiles = p.m_full * p.n_tiles + (p.tail_sub ? p.n_tiles * p.split : 0);
     const dim3 grid(tiles), block(512);
 #define EHIP_PINGPONG(T)                                                                                            \
     do {                                                                                                      \
@@ -301,6 +383,22 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     if (a.dtype == DT_F16) EHIP_PINGPONG(f16);
     else EHIP_PINGPONG(bf16);
 #undef EHIP_PINGPONG
+    if (p.split > 1) {
+        const long items = (long)64 * p.tail_sub * (a.epilogue == EPI_GEGLU ? a.N / 2 : a.N);
+        const dim3 rgrid((unsigned)((items + 255) / 256)), rblock(256);
+#define EHIP_REDUCE(OUT, EPI) hipLaunchKernelGGL((pingpong::split_reduce_kernel<OUT, EPI>), rgrid, rblock, 0, s, p)
+        if (a.epilogue == EPI_STORE) {
+            if (a.c_dtype == DT_F32) EHIP_REDUCE(float, EPI_STORE);
+            else if (a.dtype == DT_F16) EHIP_REDUCE(f16, EPI_STORE);
+            else EHIP_REDUCE(bf16, EPI_STORE);
+        } else if (a.epilogue == EPI_GATE_RESID) {
+            EHIP_REDUCE(float, EPI_GATE_RESID);
+        } else {
+            if (a.dtype == DT_F16) EHIP_REDUCE(f16, EPI_GEGLU);
+            else EHIP_REDUCE(bf16, EPI_GEGLU);
+        }
+#undef EHIP_REDUCE
+    }
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : -int(e);
 }

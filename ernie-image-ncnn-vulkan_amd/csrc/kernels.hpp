@@ -31,6 +31,11 @@ struct GemmArgs {
     const float* resid = nullptr;  // [M][ld_resid] f32 (EPI_GATE_RESID; may alias C)
     long ld_resid = 0;
     const float* gate = nullptr;   // [N]
+    // Optional split-K scratch for the tail row of tiles (M % 256 rows): FP32 partial
+    // sums, summed by a second launch on the same stream. Calls on one stream may
+    // share it; calls that run concurrently must not.
+    void* split_ws = nullptr;
+    size_t split_ws_bytes = 0;
 };
 int gemm(const GemmArgs& a, hipStream_t stream);
 // The ping-pong 16-bit kernel (gemm16_pp.hip); returns 1 without launching when
