@@ -6,6 +6,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -289,15 +290,24 @@ int block_workspace(ernie_hip_ctx* ctx, int S, int dim, int ffn, int dtype, Bloc
 // items of (64 * tail_sub) x 256 FP32 partials.
 constexpr int kSplitItems = 256;
 
-int split_workspace(ernie_hip_ctx* ctx, int S, GemmArgs& g)
+// The same buffer also holds the attention key-range parts of a partial last query
+// tile: up to 16 parts per head of 128 queries x (128 values + m, l) FP32.
+size_t split_bytes(int S, int heads)
 {
     const int tail_sub = (S % 256 + 63) / 64;
-    if (!tail_sub) return ERNIE_OK;
-    const size_t bytes = (size_t)kSplitItems * 64 * tail_sub * 256 * sizeof(float);
-    const int rc = dev_alloc(ctx, ctx->split_ws, bytes, "gemm split workspace");
+    const size_t gemm = (size_t)kSplitItems * 64 * tail_sub * 256 * sizeof(float);
+    const size_t attn = S % 128 ? (size_t)heads * 16 * 128 * (128 + 2) * sizeof(float) : 0;
+    return std::max(gemm, attn);
+}
+
+int split_workspace(ernie_hip_ctx* ctx, int S, int heads, void** ws, size_t* bytes)
+{
+    const size_t need = split_bytes(S, heads);
+    if (!need) return ERNIE_OK;
+    const int rc = dev_alloc(ctx, ctx->split_ws, need, "split workspace");
     if (rc) return rc;
-    g.split_ws = ctx->split_ws.ptr;
-    g.split_ws_bytes = ctx->split_ws.bytes;
+    *ws = ctx->split_ws.ptr;
+    *bytes = ctx->split_ws.bytes;
     return ERNIE_OK;
 }
 
@@ -324,7 +334,7 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
         GemmArgs g;
         g.A = ws.h; g.lda = D; g.W = w.wqkv.ptr; g.ldw = D; g.M = S; g.N = 3 * D; g.K = D; g.dtype = dt;
         g.epilogue = EPI_STORE; g.C = ws.qkv; g.ldc = 3 * D; g.c_dtype = dt;
-        rc = split_workspace(ctx, S, g);
+        rc = split_workspace(ctx, S, H, &g.split_ws, &g.split_ws_bytes);
         if (rc) return rc;
         Timed t(ctx, P_QKV, 2.0 * dS * 3 * D * D, gemm_bytes(dS, 3.0 * D, D, e, e));
         rc = kernel_status(ctx, gemm(g, s), "gemm qkv");
@@ -347,6 +357,8 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
         a.q_hs = a.k_hs = a.v_hs = kHeadDim; a.q_rs = a.k_rs = a.v_rs = 3L * D;
         a.o_hs = kHeadDim; a.o_rs = D;
         a.mask = mask; a.mask_heads = 1; a.mask_rows = 1; a.valid_keys = valid_keys;
+        rc = split_workspace(ctx, S, H, &a.split_ws, &a.split_ws_bytes);
+        if (rc) return rc;
         Timed t(ctx, P_SDPA, 4.0 * dS * dS * kHeadDim * H, 4.0 * dS * D * e);
         rc = kernel_status(ctx, sdpa(a, s), "sdpa");
         if (rc) return rc;
@@ -357,7 +369,7 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
         g.A = ws.attn; g.lda = D; g.W = w.wo.ptr; g.ldw = D; g.M = S; g.N = D; g.K = D; g.dtype = dt;
         g.epilogue = EPI_GATE_RESID; g.C = ws.x1; g.ldc = D; g.c_dtype = ERNIE_DTYPE_FP32; g.resid = x; g.ld_resid = D;
         g.gate = gate_sa;
-        rc = split_workspace(ctx, S, g);
+        rc = split_workspace(ctx, S, H, &g.split_ws, &g.split_ws_bytes);
         if (rc) return rc;
         Timed t(ctx, P_OUT, 2.0 * dS * D * D, gemm_bytes(dS, D, D, e, 8));
         rc = kernel_status(ctx, gemm(g, s), "gemm out");
@@ -375,7 +387,7 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
         GemmArgs g;
         g.A = ws.h; g.lda = D; g.W = w.w_ug.ptr; g.ldw = D; g.M = S; g.N = 2 * F; g.K = D; g.dtype = dt;
         g.epilogue = EPI_GEGLU; g.C = ws.p; g.ldc = F; g.c_dtype = dt;
-        rc = split_workspace(ctx, S, g);
+        rc = split_workspace(ctx, S, H, &g.split_ws, &g.split_ws_bytes);
         if (rc) return rc;
         Timed t(ctx, P_UG, 2.0 * dS * 2 * F * D, gemm_bytes(dS, 2.0 * F, D, e, 0) + dS * F * e);
         rc = kernel_status(ctx, gemm(g, s), "gemm up/gate");
@@ -387,7 +399,7 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
         g.A = ws.p; g.lda = F; g.W = w.w_down.ptr; g.ldw = F; g.M = S; g.N = D; g.K = F; g.dtype = dt;
         g.epilogue = EPI_GATE_RESID; g.C = out; g.ldc = D; g.c_dtype = ERNIE_DTYPE_FP32; g.resid = ws.x1; g.ld_resid = D;
         g.gate = gate_mlp;
-        rc = split_workspace(ctx, S, g);
+        rc = split_workspace(ctx, S, H, &g.split_ws, &g.split_ws_bytes);
         if (rc) return rc;
         Timed t(ctx, P_DOWN, 2.0 * dS * D * F, gemm_bytes(dS, D, F, e, 8));
         rc = kernel_status(ctx, gemm(g, s), "gemm down");

@@ -52,6 +52,11 @@ struct SdpaArgs {
     int mask_heads = 1, mask_rows = 1;
     int valid_keys = 0;           // keys >= valid_keys are excluded (0 = sk)
     float scale = 0.f;
+    // Optional FP32 scratch for splitting a partial last query tile along the keys
+    // (merged by a second launch on the same stream); calls that run concurrently
+    // must not share it.
+    void* split_ws = nullptr;
+    size_t split_ws_bytes = 0;
 };
 int sdpa(const SdpaArgs& a, hipStream_t stream);
 // The head_dim-128 16-bit kernel (sdpa16_dl.hip); returns 1 without launching for

@@ -25,6 +25,10 @@
 #include "kernels.hpp"
 
 namespace ehip {
+namespace {
+// Workgroup slots of an MI355X for this kernel: 256 CUs x 2.
+constexpr int kSdpaSlots = 512;
+}
 namespace sdl {
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -41,7 +45,39 @@ struct Params {
     long q_hs, q_rs, k_hs, k_rs, v_hs, v_rs, o_hs, o_rs;
     const float* mask; long mask_hs;
     float scale_log2;
+    // Split of the last, partial query tile (sq % 128 queries) along the keys:
+    // tail_parts > 0 parts per head write unnormalised FP32 O and their (m, l) to
+    // part_o [heads * tail_parts][128][128] / part_ml [heads * tail_parts][128][2].
+    int full_qt, tail_parts;
+    float* part_o;
+    float* part_ml;
 };
+
+// Merges the key-range parts of the split query tile: O = sum_p O_p 2^(m_p - M) /
+// sum_p l_p 2^(m_p - M) with M = max_p m_p (log2 domain). One thread per (head,
+// query, value).
+template <typename T>
+__global__ void __launch_bounds__(256) combine_kernel(Params p, int tail_q)
+{
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long)p.heads * tail_q * D) return;
+    const int d = (int)(idx % D);
+    const int ql = (int)((idx / D) % tail_q);
+    const int h = (int)(idx / ((long)D * tail_q));
+    const float* ml = p.part_ml + ((size_t)h * p.tail_parts * BQ + ql) * 2;
+    float M = -INFINITY;
+    for (int q = 0; q < p.tail_parts; ++q) M = fmaxf(M, ml[(size_t)q * BQ * 2]);
+    float L = 0.f, O = 0.f;
+    const float* po = p.part_o + ((size_t)h * p.tail_parts * BQ + ql) * D + d;
+    for (int q = 0; q < p.tail_parts; ++q) {
+        const float m = ml[(size_t)q * BQ * 2];
+        const float w = m == -INFINITY ? 0.f : exp2f(m - M);
+        L += ml[(size_t)q * BQ * 2 + 1] * w;
+        O += po[(size_t)q * BQ * D] * w;
+    }
+    const int qi = p.full_qt * BQ + ql;
+    static_cast<T*>(p.o)[(size_t)h * p.o_hs + (size_t)qi * p.o_rs + d] = T(O / L);
+}
 
 template <typename T> struct Mfma;
 template <> struct Mfma<f16> {
@@ -84,12 +120,37 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
     typedef typename Mfma<T>::vec vec8;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
 
-    const int qtiles = (p.sq + BQ - 1) / BQ;
-    const int total = qtiles * p.heads;
-    int logical = blockIdx.x;
-    if ((total & 7) == 0) logical = (blockIdx.x & 7) * (total >> 3) + (blockIdx.x >> 3);
-    const int h = logical / qtiles;
-    const int q_base = (logical - h * qtiles) * BQ;
+    // Workgroup -> (head, query tile[, key range]). Workgroup b runs on XCD b % 8:
+    // each XCD takes a contiguous range of full query tiles (so a head's K / V stream
+    // into one L2) and then its share of the key-range parts of the split tail tile,
+    // which therefore run last and fill the CUs.
+    const int ntiles = (p.kv_end + BKV - 1) / BKV;
+    int h, q_base, it0 = 0, it1 = ntiles, part = -1;
+    {
+        const int full = p.tail_parts ? p.full_qt * p.heads : ((p.sq + BQ - 1) / BQ) * p.heads;
+        const int tail = p.tail_parts * p.heads;
+        const int qt = p.tail_parts ? p.full_qt : (p.sq + BQ - 1) / BQ;
+        const int bid = blockIdx.x;
+        int f = -1, u = -1;
+        if ((full & 7) == 0 && (tail & 7) == 0) {
+            const int x = bid & 7, j = bid >> 3, per = full >> 3;
+            if (j < per) f = x * per + j;
+            else u = x * (tail >> 3) + (j - per);
+        } else {
+            if (bid < full) f = bid;
+            else u = bid - full;
+        }
+        if (f >= 0) {
+            h = f / qt;
+            q_base = (f - h * qt) * BQ;
+        } else {
+            h = u / p.tail_parts;
+            part = u - h * p.tail_parts;
+            q_base = p.full_qt * BQ;
+            it0 = (int)((long)ntiles * part / p.tail_parts);
+            it1 = (int)((long)ntiles * (part + 1) / p.tail_parts);
+        }
+    }
     const int kvh = h / p.group;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -166,14 +227,13 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
     float m_run = -INFINITY, l_run = 0.f;
     const float c = p.scale_log2;
 
-    const int ntiles = (p.kv_end + BKV - 1) / BKV;
-    issue(0, 0);
-    for (int it = 0; it < ntiles; ++it) {
-        const int buf = it & 1;
+    if (it0 < it1) issue(it0, 0);
+    for (int it = it0; it < it1; ++it) {
+        const int buf = (it - it0) & 1;
         const int kv0 = it * BKV;
         __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // this wave's loads of tile it have landed
         lds_barrier();                                         // ... and every wave's; tile it-1 is consumed
-        if (it + 1 < ntiles) issue(it + 1, buf ^ 1);
+        if (it + 1 < it1) issue(it + 1, buf ^ 1);
         const uint8_t* st = smem + buf * STAGE;
 
         f32x16 sacc[2];
@@ -262,6 +322,24 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
             }
     }
 
+    if (part >= 0) {
+        // Key-range part of the split tail tile: unnormalised O and (m, l) for combine_kernel.
+        const size_t slot = (size_t)h * p.tail_parts + part;
+        const int ql = wave * 32 + lrow;
+        float* po = p.part_o + (slot * BQ + ql) * D;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int rq = 0; rq < 4; ++rq) {
+                const f32x4 v = {oacc[dt][4 * rq], oacc[dt][4 * rq + 1], oacc[dt][4 * rq + 2], oacc[dt][4 * rq + 3]};
+                *reinterpret_cast<f32x4*>(po + 32 * dt + 8 * rq + 4 * g) = v;
+            }
+        if (g == 0) {
+            p.part_ml[(slot * BQ + ql) * 2] = m_run;
+            p.part_ml[(slot * BQ + ql) * 2 + 1] = l_run;
+        }
+        return;
+    }
     if (my_q >= p.sq) return;
     const float inv = 1.f / l_run;
     T* orow = static_cast<T*>(p.o) + (size_t)h * p.o_hs + (size_t)my_q * p.o_rs;
@@ -303,13 +381,34 @@ int sdpa16_d128(const SdpaArgs& a, hipStream_t s)
     p.mask_hs = a.mask && a.mask_heads > 1 ? (long)a.sk : 0;
     const float scale = a.scale > 0.f ? a.scale : 1.f / sqrtf(128.f);
     p.scale_log2 = scale * sdl::kLog2e;
-    const dim3 grid(((a.sq + sdl::BQ - 1) / sdl::BQ) * a.heads), block(256);
+    // A partial last query tile is split along the keys when a workspace is given:
+    // up to 16 parts per head, aiming at one workgroup per CU slot (two per CU).
+    p.full_qt = a.sq / sdl::BQ;
+    const int tail_q = a.sq - p.full_qt * sdl::BQ;
+    if (tail_q && p.full_qt && a.split_ws) {
+        int parts = std::min(std::min(16, ntiles), std::max(1, kSdpaSlots / a.heads));
+        const size_t per_part = (size_t)a.heads * sdl::BQ * (sdl::D + 2) * sizeof(float);
+        while (parts > 1 && (size_t)parts * per_part > a.split_ws_bytes) --parts;
+        if (parts > 1) {
+            p.tail_parts = parts;
+            p.part_o = static_cast<float*>(a.split_ws);
+            p.part_ml = p.part_o + (size_t)a.heads * parts * sdl::BQ * sdl::D;
+        }
+    }
+    const int wgs = p.tail_parts ? (p.full_qt + p.tail_parts) * a.heads : ((a.sq + sdl::BQ - 1) / sdl::BQ) * a.heads;
+    const dim3 grid(wgs), block(256);
     if (a.dtype == DT_F16) {
         if (a.mask) hipLaunchKernelGGL((sdl::kernel<f16, true>), grid, block, 0, s, p);
         else hipLaunchKernelGGL((sdl::kernel<f16, false>), grid, block, 0, s, p);
     } else {
         if (a.mask) hipLaunchKernelGGL((sdl::kernel<bf16, true>), grid, block, 0, s, p);
         else hipLaunchKernelGGL((sdl::kernel<bf16, false>), grid, block, 0, s, p);
+    }
+    if (p.tail_parts) {
+        const long n = (long)a.heads * tail_q * sdl::D;
+        const dim3 cgrid((unsigned)((n + 255) / 256));
+        if (a.dtype == DT_F16) hipLaunchKernelGGL((sdl::combine_kernel<f16>), cgrid, block, 0, s, p, tail_q);
+        else hipLaunchKernelGGL((sdl::combine_kernel<bf16>), cgrid, block, 0, s, p, tail_q);
     }
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : -int(e);
