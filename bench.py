@@ -23,11 +23,13 @@ sys.path.insert(0, str(ROOT / "ernie-image-ncnn-vulkan_amd"))
 METRIC = "DiT denoise steps/s at 1024×1024 fp16 (36 blk); SDPA+GEMM % MFMA peak"
 PEAK = {"fp16": 2.5e15, "bf16": 2.5e15, "fp32": 157.3e12}
 HBM_PEAK = 8.0e12
-# HBM bytes per launch of each kernel class at this workload (FP16, S=4160), from
-# two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) scaled by the same counters'
-# reading for a plain 512 MiB FP32 copy (x2.000 fetch, x1.000 write); the runs and
-# the per-dispatch table are in profiles/denoise_1024_fp16_hbm_traffic.md.
-MEASURED_TRAFFIC = {"fp16": {"gemm_up_gate": 1.517e9, "gemm_qkv": 8.119e8, "sdpa": 1.786e8}}
+# HBM bytes per launch of each kernel class at this workload (FP16, S=4160): the
+# class's main kernel plus its split-K reduction (GEMM) or key-range combine (SDPA)
+# launch, from two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) scaled by the same
+# counters' reading for a plain 512 MiB FP32 copy (x2.000 fetch, x1.000 write); the
+# runs and the per-dispatch table are in profiles/denoise_1024_fp16_hbm_traffic.md.
+MEASURED_TRAFFIC = {"fp16": {"gemm_up_gate": 1.527e9 + 1.42e7, "gemm_qkv": 8.293e8 + 1.733e7,
+                             "sdpa": 2.313e8 + 1.944e7}}
 DIM, FFN, LATENT_CH, TEXT_DIM = 4096, 12288, 128, 3072
 
 
