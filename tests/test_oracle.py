@@ -209,14 +209,15 @@ def test_sdpa_matches_torch_fp64():
 
 
 # ---- block and heads against PyTorch FP64 library routines ----------------------------------
-def small_block(dim=256, ffn=512, seed=0, std=0.02):
+def small_block(dim=256, ffn=512, seed=0, std=0.02, block=0):
+    """One block's weights in .bin order; block b of a stack draws sub-streams 16b + i of the seed."""
     shapes = {"norm1": (dim,), "wq": (dim, dim), "wk": (dim, dim), "wv": (dim, dim), "norm_q": (128,),
               "norm_k": (128,), "wo": (dim, dim), "norm2": (dim,), "w_up": (ffn, dim), "w_gate": (ffn, dim),
               "w_down": (dim, ffn)}
     w = {}
     for i, (name, shape) in enumerate(shapes.items()):
         mean = 1.0 if name.startswith("norm") else 0.0
-        w[name] = O.normal(shape, seed, offset=i << 40, mean=mean, std=std)
+        w[name] = O.normal(shape, seed, offset=(16 * block + i) << 40, mean=mean, std=std)
     return w
 
 
