@@ -201,23 +201,21 @@ enum { P_QKV = 0, P_SDPA = 1, P_OUT = 2, P_UG = 3, P_DOWN = 4, P_NORM = 5, P_ROP
 double gemm_bytes(double M, double N, double K, double e, double eo) { return (M * K + N * K) * e + M * N * eo; }
 
 // ---- uploads ------------------------------------------------------------------------
-int upload_f32(ernie_hip_ctx* ctx, DeviceBuffer& dst, const float* src, size_t count, const char* what)
+// Host tensor (FP32, FP16 or BF16) -> device dtype at `dst` (+ element offset) through the
+// staging buffer; the conversion runs on the device. An FP32 -> FP32 upload copies directly.
+int upload_tensor(ernie_hip_ctx* ctx, void* dst, size_t dst_offset, int dtype, const void* src, int src_dtype,
+                  size_t count, const char* what)
 {
-    int rc = dev_alloc(ctx, dst, count * 4, what);
-    if (rc) return rc;
-    return hip_status(ctx, hipMemcpyAsync(dst.ptr, src, count * 4, hipMemcpyHostToDevice, ctx->stream), what);
-}
-
-// Host FP32 -> device dtype at `dst` (+ element offset) via the staging buffer.
-int upload_convert(ernie_hip_ctx* ctx, void* dst, size_t dst_offset, int dtype, const float* src, size_t count,
-                   const char* what)
-{
-    int rc = dev_alloc(ctx, ctx->staging, count * 4, "staging buffer");
-    if (rc) return rc;
-    rc = hip_status(ctx, hipMemcpyAsync(ctx->staging.ptr, src, count * 4, hipMemcpyHostToDevice, ctx->stream), what);
-    if (rc) return rc;
+    if (!valid_dtype(src_dtype)) return fail(ctx, ERNIE_ERROR, "invalid source dtype");
     char* base = static_cast<char*>(dst) + dst_offset * esize(dtype);
-    rc = kernel_status(ctx, convert(ctx->staging.ptr, ERNIE_DTYPE_FP32, base, dtype, count, ctx->stream), what);
+    if (src_dtype == dtype)
+        return hip_status(ctx, hipMemcpyAsync(base, src, count * esize(dtype), hipMemcpyHostToDevice, ctx->stream), what);
+    int rc = dev_alloc(ctx, ctx->staging, count * esize(src_dtype), "staging buffer");
+    if (rc) return rc;
+    rc = hip_status(ctx, hipMemcpyAsync(ctx->staging.ptr, src, count * esize(src_dtype), hipMemcpyHostToDevice,
+                                        ctx->stream), what);
+    if (rc) return rc;
+    rc = kernel_status(ctx, convert(ctx->staging.ptr, src_dtype, base, dtype, count, ctx->stream), what);
     if (rc) return rc;
     // The staging buffer is reused by the next upload: finish this one first.
     return hip_status(ctx, hipStreamSynchronize(ctx->stream), what);
@@ -688,40 +686,47 @@ int ernie_hip_convert(ernie_hip_ctx* ctx, const void* in, int in_dtype, void* ou
 }
 
 // ---- blocks -----------------------------------------------------------------------------
-int ernie_hip_block_upload(ernie_hip_ctx* ctx, int index, const ernie_block_host_weights* w, int dim, int ffn,
-                           int dtype)
+int ernie_hip_block_upload_tensors(ernie_hip_ctx* ctx, int index, const ernie_block_host_tensors* w, int dim, int ffn,
+                                   int dtype)
 {
     if (!ctx || !w) return ERNIE_ERROR;
     int rc = check_block_dims(ctx, dim, ffn, dtype);
     if (rc) return rc;
-    const float* parts[] = {w->norm1, w->wq, w->wk, w->wv, w->norm_q, w->norm_k, w->wo, w->norm2, w->w_up, w->w_gate, w->w_down};
-    for (const float* p : parts)
-        if (!p) return fail(ctx, ERNIE_ERROR, "null block weight");
+    const ernie_host_tensor* parts[] = {&w->norm1, &w->wq, &w->wk, &w->wv, &w->norm_q, &w->norm_k,
+                                        &w->wo, &w->norm2, &w->w_up, &w->w_gate, &w->w_down};
+    for (const ernie_host_tensor* t : parts) {
+        if (!t->data) return fail(ctx, ERNIE_ERROR, "null block weight");
+        if (!valid_dtype(t->dtype)) return fail(ctx, ERNIE_ERROR, "invalid block weight dtype");
+    }
     BlockWeights* slot = block_slot(ctx, index);
     if (!slot) return fail(ctx, ERNIE_ERROR, "block index out of range");
     free_block(*slot);
     BlockWeights bw;
     rc = alloc_block(ctx, bw, dim, ffn, dtype);
     if (rc) return rc;
-    const size_t DD = (size_t)dim * dim;
-    rc = rc ? rc : upload_f32(ctx, bw.norm1, w->norm1, dim, "norm1");
-    rc = rc ? rc : upload_f32(ctx, bw.norm2, w->norm2, dim, "norm2");
-    rc = rc ? rc : upload_f32(ctx, bw.norm_q, w->norm_q, kHeadDim, "norm_q");
-    rc = rc ? rc : upload_f32(ctx, bw.norm_k, w->norm_k, kHeadDim, "norm_k");
-    rc = rc ? rc : upload_convert(ctx, bw.wqkv.ptr, 0, dtype, w->wq, DD, "wq");
-    rc = rc ? rc : upload_convert(ctx, bw.wqkv.ptr, DD, dtype, w->wk, DD, "wk");
-    rc = rc ? rc : upload_convert(ctx, bw.wqkv.ptr, 2 * DD, dtype, w->wv, DD, "wv");
-    rc = rc ? rc : upload_convert(ctx, bw.wo.ptr, 0, dtype, w->wo, DD, "wo");
-    rc = rc ? rc : upload_convert(ctx, bw.w_down.ptr, 0, dtype, w->w_down, (size_t)dim * ffn, "w_down");
+    const size_t DD = (size_t)dim * dim, DF = (size_t)dim * ffn;
+    constexpr int F32 = ERNIE_DTYPE_FP32;
+    // RMSNorm gammas stay FP32 whatever the storage precision (src/ernie_rmsnorm.cpp:11-17).
+    rc = rc ? rc : upload_tensor(ctx, bw.norm1.ptr, 0, F32, w->norm1.data, w->norm1.dtype, dim, "norm1");
+    rc = rc ? rc : upload_tensor(ctx, bw.norm2.ptr, 0, F32, w->norm2.data, w->norm2.dtype, dim, "norm2");
+    rc = rc ? rc : upload_tensor(ctx, bw.norm_q.ptr, 0, F32, w->norm_q.data, w->norm_q.dtype, kHeadDim, "norm_q");
+    rc = rc ? rc : upload_tensor(ctx, bw.norm_k.ptr, 0, F32, w->norm_k.data, w->norm_k.dtype, kHeadDim, "norm_k");
+    rc = rc ? rc : upload_tensor(ctx, bw.wqkv.ptr, 0, dtype, w->wq.data, w->wq.dtype, DD, "wq");
+    rc = rc ? rc : upload_tensor(ctx, bw.wqkv.ptr, DD, dtype, w->wk.data, w->wk.dtype, DD, "wk");
+    rc = rc ? rc : upload_tensor(ctx, bw.wqkv.ptr, 2 * DD, dtype, w->wv.data, w->wv.dtype, DD, "wv");
+    rc = rc ? rc : upload_tensor(ctx, bw.wo.ptr, 0, dtype, w->wo.data, w->wo.dtype, DD, "wo");
+    rc = rc ? rc : upload_tensor(ctx, bw.w_down.ptr, 0, dtype, w->w_down.data, w->w_down.dtype, DF, "w_down");
     for (int parity = 0; parity < 2 && !rc; ++parity) {
-        const float* src = parity ? w->w_gate : w->w_up;
-        const size_t count = (size_t)ffn * dim;
-        rc = dev_alloc(ctx, ctx->staging, count * 4, "staging buffer");
-        if (!rc) rc = hip_status(ctx, hipMemcpyAsync(ctx->staging.ptr, src, count * 4, hipMemcpyHostToDevice, ctx->stream), "w_ug");
-        if (!rc) rc = kernel_status(ctx, interleave_up_gate(static_cast<const float*>(ctx->staging.ptr), bw.w_ug.ptr,
-                                                            dtype, ffn, dim, parity, ctx->stream), "w_ug");
+        const ernie_host_tensor& src = parity ? w->w_gate : w->w_up;
+        const size_t bytes = DF * esize(src.dtype);
+        rc = dev_alloc(ctx, ctx->staging, bytes, "staging buffer");
+        if (!rc) rc = hip_status(ctx, hipMemcpyAsync(ctx->staging.ptr, src.data, bytes, hipMemcpyHostToDevice, ctx->stream), "w_ug");
+        if (!rc) rc = kernel_status(ctx, interleave_up_gate(ctx->staging.ptr, src.dtype, bw.w_ug.ptr, dtype, ffn, dim,
+                                                            parity, ctx->stream), "w_ug");
         if (!rc) rc = hip_status(ctx, hipStreamSynchronize(ctx->stream), "w_ug");
     }
+    // Host memory may be released once this returns: every copy out of it has finished.
+    if (!rc) rc = hip_status(ctx, hipStreamSynchronize(ctx->stream), "block upload");
     if (rc) {
         free_block(bw);
         return rc;
@@ -729,6 +734,17 @@ int ernie_hip_block_upload(ernie_hip_ctx* ctx, int index, const ernie_block_host
     bw.loaded = true;
     *slot = bw;
     return ERNIE_OK;
+}
+
+int ernie_hip_block_upload(ernie_hip_ctx* ctx, int index, const ernie_block_host_weights* w, int dim, int ffn,
+                           int dtype)
+{
+    if (!ctx || !w) return ERNIE_ERROR;
+    auto f32 = [](const float* p) { return ernie_host_tensor{p, ERNIE_DTYPE_FP32}; };
+    const ernie_block_host_tensors t = {f32(w->norm1), f32(w->wq),     f32(w->wk),     f32(w->wv),
+                                        f32(w->norm_q), f32(w->norm_k), f32(w->wo),     f32(w->norm2),
+                                        f32(w->w_up),  f32(w->w_gate), f32(w->w_down)};
+    return ernie_hip_block_upload_tensors(ctx, index, &t, dim, ffn, dtype);
 }
 
 int ernie_hip_block_init_random(ernie_hip_ctx* ctx, int index, int dim, int ffn, int dtype, uint64_t seed,
@@ -850,12 +866,13 @@ int ernie_hip_heads_upload(ernie_hip_ctx* ctx, const ernie_heads_host_weights* w
         if (rc) return;
         if (!src) { rc = fail(ctx, ERNIE_ERROR, std::string("null ") + what); return; }
         rc = dev_alloc(ctx, b, n * e, what);
-        if (!rc) rc = upload_convert(ctx, b.ptr, 0, dtype, src, n, what);
+        if (!rc) rc = upload_tensor(ctx, b.ptr, 0, dtype, src, ERNIE_DTYPE_FP32, n, what);
     };
     auto vec = [&](DeviceBuffer& b, const float* src, size_t n, const char* what) {
         if (rc) return;
         if (!src) { rc = fail(ctx, ERNIE_ERROR, std::string("null ") + what); return; }
-        rc = upload_f32(ctx, b, src, n, what);
+        rc = dev_alloc(ctx, b, n * 4, what);
+        if (!rc) rc = upload_tensor(ctx, b.ptr, 0, ERNIE_DTYPE_FP32, src, ERNIE_DTYPE_FP32, n, what);
     };
     mat(h.x_w, w->x_w, D * latent_ch, "x_w");
     vec(h.x_b, w->x_b, D, "x_b");

@@ -93,7 +93,7 @@ int transpose_to_tokens(const float* latent, int ch, int hw, void* out, int dtyp
 // proj [hw][ch] (f32, bias applied) -> pred [ch][hw] f32.
 int tokens_to_latent(const float* proj, int hw, int ch, float* pred, hipStream_t s);
 
-// Host FP32 up or gate matrix [rows][cols] -> its rows of the interleaved W_ug (parity 0 = up).
-int interleave_up_gate(const float* in, void* out, int dt, int rows, int cols, int parity, hipStream_t s);
+// Up or gate matrix [rows][cols] (dtype in_dt) -> its rows of the interleaved W_ug (parity 0 = up).
+int interleave_up_gate(const void* in, int in_dt, void* out, int dt, int rows, int cols, int parity, hipStream_t s);
 
 }  // namespace ehip

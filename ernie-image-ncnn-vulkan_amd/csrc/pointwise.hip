@@ -293,14 +293,14 @@ __global__ void tokens_latent_kernel(const float* __restrict__ proj, int hw, int
 
 // W_ug row layout: rows [64c, 64c+32) = up rows [32c, 32c+32), rows [64c+32, 64c+64)
 // = gate rows [32c, 32c+32); lets one 64-column MFMA tile hold matching up/gate columns.
-__global__ void interleave_kernel(const float* __restrict__ in, void* __restrict__ out, int dt, int rows, int cols,
-                                  int parity)
+__global__ void interleave_kernel(const void* __restrict__ in, int idt, void* __restrict__ out, int dt, int rows,
+                                  int cols, int parity)
 {
     const size_t n = (size_t)rows * cols;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
         const int r = (int)(i / cols), c = (int)(i % cols);
         const size_t orow = 64 * (size_t)(r / 32) + 32 * parity + (r % 32);
-        store_any(out, orow * cols + c, dt, in[i]);
+        store_any(out, orow * cols + c, dt, load_any(in, i, idt));
     }
 }
 
@@ -483,11 +483,12 @@ int tokens_to_latent(const float* proj, int hw, int ch, float* pred, hipStream_t
     return launch_status();
 }
 
-int interleave_up_gate(const float* in, void* out, int dt, int rows, int cols, int parity, hipStream_t s)
+int interleave_up_gate(const void* in, int idt, void* out, int dt, int rows, int cols, int parity, hipStream_t s)
 {
-    if (!in || !out || !valid_dt(dt) || rows % 32 || cols < 1 || (parity != 0 && parity != 1)) return -1;
+    if (!in || !out || !valid_dt(idt) || !valid_dt(dt) || rows % 32 || cols < 1 || (parity != 0 && parity != 1))
+        return -1;
     const size_t n = (size_t)rows * cols;
-    hipLaunchKernelGGL(interleave_kernel, dim3(grid_for(n)), dim3(256), 0, s, in, out, dt, rows, cols, parity);
+    hipLaunchKernelGGL(interleave_kernel, dim3(grid_for(n)), dim3(256), 0, s, in, idt, out, dt, rows, cols, parity);
     return launch_status();
 }
 

@@ -95,6 +95,7 @@ def hip():
             "ernie_hip_fill_normal": (c_int, [c_vp, c_vp, c_int, c_size_t, c_u64, c_u64, c_float, c_float]),
             "ernie_hip_convert": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_size_t]),
             "ernie_hip_block_upload": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int]),
+            "ernie_hip_block_upload_tensors": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int]),
             "ernie_hip_block_init_random": (c_int, [c_vp, c_int, c_int, c_int, c_int, c_u64, c_float]),
             "ernie_hip_block_release": (c_int, [c_vp, c_int]),
             "ernie_hip_block_count": (c_int, [c_vp]),
@@ -121,6 +122,35 @@ def hip():
     return _hip
 
 
+class BlockFileInfo(ctypes.Structure):
+    """ernie_block_file_info (include/ernie.h)."""
+    _fields_ = [("tokens", c_int), ("dim", c_int), ("ffn", c_int), ("contract", c_int),
+                ("component_sha256", ctypes.c_char * 65), ("runtime_sha256", ctypes.c_char * 65),
+                ("bin_bytes", c_size_t), ("section_count", c_int), ("section_dtype", c_int * 11),
+                ("section_begin", c_size_t * 11), ("section_data", c_size_t * 11), ("section_end", c_size_t * 11)]
+
+    def as_dict(self):
+        n = self.section_count
+        return {"tokens": self.tokens, "dim": self.dim, "ffn": self.ffn,
+                "contract": GRAPH_CONTRACTS[self.contract],
+                "component_sha256": self.component_sha256.decode(), "runtime_sha256": self.runtime_sha256.decode(),
+                "bin_bytes": self.bin_bytes,
+                "sections": [{"layer": BLOCK_WEIGHT_LAYERS[i], "dtype": self.section_dtype[i],
+                              "begin": self.section_begin[i], "data": self.section_data[i],
+                              "end": self.section_end[i]} for i in range(n)]}
+
+
+class HostTensor(ctypes.Structure):
+    """ernie_host_tensor (include/ernie_hip.h)."""
+    _fields_ = [("data", c_vp), ("dtype", c_int)]
+
+
+GRAPH_CONTRACTS = ("unreviewed", "component", "runtime")
+# Weighted layers of a block graph in .bin order (tools/build_dit_weights.py:19-31).
+BLOCK_WEIGHT_LAYERS = ("rmsn_8", "gemm_0", "gemm_1", "gemm_2", "rmsn_9", "rmsn_10", "gemm_3", "rmsn_11", "gemm_4",
+                       "gemm_5", "gemm_6")
+
+
 def facade():
     global _facade
     if _facade is None:
@@ -141,6 +171,10 @@ def facade():
                                                  c_int, c_vp, c_vp, cp, c_size_t]),
             "ernie_denoise": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_int,
                                       c_int, c_int, c_int, c_vp, c_vp, cp, c_size_t]),
+            "ernie_sha256_hex": (c_int, [c_vp, c_size_t, cp]),
+            "ernie_block_file_inspect": (c_int, [cp, cp, c_int, cp, ctypes.POINTER(BlockFileInfo), cp, c_size_t]),
+            "ernie_block_load": (c_int, [c_vp, c_int, cp, cp, c_int, c_int, cp, ctypes.POINTER(BlockFileInfo), cp,
+                                         c_size_t]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -216,6 +250,31 @@ def dit_constants(freqs, w, h, valid, text):
     if rc < 0:
         _raise(rc, e.value)
     return cos, sin, mask, rc
+
+
+def sha256_hex(data):
+    """SHA-256 of a bytes-like object through the facade's own implementation."""
+    buf = bytes(data)
+    out = ctypes.create_string_buffer(65)
+    rc = facade().ernie_sha256_hex(buf, len(buf), out)
+    if rc:
+        _raise(rc, "sha256")
+    return out.value.decode()
+
+
+def _path(p):
+    return None if p is None else str(p).encode()
+
+
+def block_file_inspect(param_path, bin_path=None, allow_unreviewed=False, expected_bin_sha256=None):
+    """Checks block.ncnn.param (and walks block.ncnn.bin when given) without a device."""
+    info = BlockFileInfo()
+    e = _err()
+    rc = facade().ernie_block_file_inspect(_path(param_path), _path(bin_path), int(bool(allow_unreviewed)),
+                                           _path(expected_bin_sha256), ctypes.byref(info), e, 512)
+    if rc:
+        _raise(rc, e.value)
+    return info.as_dict()
 
 
 class Context:
@@ -299,6 +358,14 @@ class Context:
         keep = [np.ascontiguousarray(weights[f], np.float32) for f in fields]
         arr = (c_vp * len(fields))(*[a.ctypes.data for a in keep])
         self.call("block_upload", index, ctypes.cast(arr, c_vp), dim, ffn, dtype)
+
+    def block_upload_tensors(self, index, tensors, dim, ffn, dtype):
+        """tensors: dict field -> (numpy array, element dtype); FP16/BF16 arrays hold raw uint16 bits."""
+        import numpy as np
+        fields = ("norm1", "wq", "wk", "wv", "norm_q", "norm_k", "wo", "norm2", "w_up", "w_gate", "w_down")
+        keep = [np.ascontiguousarray(tensors[f][0]) for f in fields]
+        arr = (HostTensor * len(fields))(*[HostTensor(a.ctypes.data, tensors[f][1]) for a, f in zip(keep, fields)])
+        self.call("block_upload_tensors", index, ctypes.cast(arr, c_vp), dim, ffn, dtype)
 
     def block_init_random(self, index, dim, ffn, dtype, seed, std=0.02):
         self.call("block_init_random", index, dim, ffn, dtype, seed, std)
@@ -394,6 +461,17 @@ class Facade:
         if rc:
             _raise(rc, e.value)
         return secs[:len(blocks)]
+
+    def block_load(self, index, param_path, bin_path, dtype, allow_unreviewed=False, expected_bin_sha256=None):
+        """Loads block.ncnn.param + block.ncnn.bin into resident block slot `index`."""
+        info = BlockFileInfo()
+        e = _err()
+        rc = self.L.ernie_block_load(self.dev, index, _path(param_path), _path(bin_path), dtype,
+                                     int(bool(allow_unreviewed)), _path(expected_bin_sha256), ctypes.byref(info), e,
+                                     512)
+        if rc:
+            _raise(rc, e.value)
+        return info.as_dict()
 
     def denoise(self, blocks, latent, height, width, text, text_tokens, cos, sin, mask, valid_prefix, steps,
                 start_step=0, dtype=FP16):

@@ -6,8 +6,10 @@
 #include <exception>
 #include <stdexcept>
 
+#include "ernie/block_files.h"
 #include "ernie/conditioning.h"
 #include "ernie/denoiser.h"
+#include "ernie/sha256.h"
 
 struct ernie_device {
     ernie::Device device;
@@ -53,6 +55,26 @@ ernie::DeviceMat wrap(const float* p, int w, int h = 1, int c = 1, int dims = 0)
     m.c = c;
     m.dims = dims ? dims : (c > 1 ? 3 : (h > 1 ? 2 : 1));
     return m;
+}
+
+void fill_info(ernie_block_file_info* info, const ernie::BlockFile& f)
+{
+    if (!info) return;
+    std::memset(info, 0, sizeof(*info));
+    info->tokens = f.graph.tokens;
+    info->dim = f.graph.dim;
+    info->ffn = f.graph.ffn;
+    info->contract = static_cast<int>(f.graph.contract);
+    std::strncpy(info->component_sha256, f.graph.component_sha256.c_str(), 64);
+    std::strncpy(info->runtime_sha256, f.graph.runtime_sha256.c_str(), 64);
+    info->bin_bytes = f.bin_bytes;
+    info->section_count = static_cast<int>(f.sections.size());
+    for (size_t i = 0; i < f.sections.size() && i < 11; ++i) {
+        info->section_dtype[i] = f.sections[i].dtype;
+        info->section_begin[i] = f.sections[i].begin;
+        info->section_data[i] = f.sections[i].data;
+        info->section_end[i] = f.sections[i].end;
+    }
 }
 
 ernie::Option option_for(const ernie::Device& d, int dtype)
@@ -178,6 +200,39 @@ int ernie_denoise(ernie_device* device, const int* blocks, int count, float* lat
             if (step_seconds) step_seconds[i] = stats[i].elapsed_seconds;
             if (step_timesteps) step_timesteps[i] = stats[i].timestep;
         }
+        return ERNIE_OK;
+    });
+}
+
+int ernie_sha256_hex(const void* data, size_t size, char* hex65)
+{
+    if (!hex65 || (!data && size)) return ERNIE_INVALID_REQUEST;
+    const std::string h = ernie::sha256_hex(data, size);
+    std::memcpy(hex65, h.c_str(), 65);
+    return ERNIE_OK;
+}
+
+int ernie_block_file_inspect(const char* param_path, const char* bin_path, int allow_unreviewed,
+                             const char* expected_bin_sha256, ernie_block_file_info* info, char* err, size_t errlen)
+{
+    return guarded(err, errlen, [&]() -> int {
+        if (!param_path) throw std::invalid_argument("null graph path");
+        const auto f = ernie::inspect_block_files(param_path, bin_path ? bin_path : "", allow_unreviewed != 0,
+                                                  expected_bin_sha256 ? expected_bin_sha256 : "");
+        fill_info(info, f);
+        return ERNIE_OK;
+    });
+}
+
+int ernie_block_load(ernie_device* device, int index, const char* param_path, const char* bin_path,
+                     int storage_dtype, int allow_unreviewed, const char* expected_bin_sha256,
+                     ernie_block_file_info* info, char* err, size_t errlen)
+{
+    return guarded(err, errlen, [&]() -> int {
+        if (!device || !param_path || !bin_path) throw std::invalid_argument("null block load argument");
+        const auto f = ernie::load_block_files(device->device, index, param_path, bin_path, storage_dtype,
+                                               allow_unreviewed != 0, expected_bin_sha256 ? expected_bin_sha256 : "");
+        fill_info(info, f);
         return ERNIE_OK;
     });
 }

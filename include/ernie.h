@@ -61,6 +61,34 @@ int ernie_denoise(ernie_device* device, const int* blocks, int count, float* lat
                   int valid_prefix, int steps, int start_step, int storage_dtype, double* step_seconds,
                   float* step_timesteps, char* err, size_t errlen);
 
+/* ---- on-disk blocks (block.ncnn.param + block.ncnn.bin) ----------------------- */
+typedef struct {
+    int tokens, dim, ffn;         /* static token count of the graph, block widths */
+    int contract;                 /* 0 unreviewed, 1 component export, 2 runtime package graph */
+    char component_sha256[65];    /* the two normalised graph hashes, "" where a form does not apply */
+    char runtime_sha256[65];
+    size_t bin_bytes;             /* 0 when no weight file was read */
+    int section_count;            /* 11, or 0 without a weight file */
+    int section_dtype[11];        /* ERNIE_DTYPE_* stored in each section, .bin order */
+    size_t section_begin[11], section_data[11], section_end[11];
+} ernie_block_file_info;
+
+/* SHA-256 of a byte string as 64 lower-case hex digits + NUL (hex65). */
+int ernie_sha256_hex(const void* data, size_t size, char* hex65);
+/* Checks a block graph and, when bin_path is non-NULL, walks its ModelBin
+ * sections (and compares the file's SHA-256 when expected_bin_sha256 is
+ * non-NULL). Replaces the graph checks of src/shape_graph.cpp:37-95 and
+ * tools/build_dit_weights.py:34-50 plus ModelBin parsing for the block. An
+ * unreviewed topology is rejected (-22) unless allow_unreviewed. No device. */
+int ernie_block_file_inspect(const char* param_path, const char* bin_path, int allow_unreviewed,
+                             const char* expected_bin_sha256, ernie_block_file_info* info, char* err, size_t errlen);
+/* ernie_block_file_inspect, then uploads the weights into resident block slot
+ * `index` at storage_dtype: replaces load_component (src/component_files.cpp:37-60)
+ * for a block Net. `info` is nullable. */
+int ernie_block_load(ernie_device* device, int index, const char* param_path, const char* bin_path,
+                     int storage_dtype, int allow_unreviewed, const char* expected_bin_sha256,
+                     ernie_block_file_info* info, char* err, size_t errlen);
+
 #ifdef __cplusplus
 }
 #endif

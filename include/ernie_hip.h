@@ -130,6 +130,25 @@ typedef struct {
 
 int ernie_hip_block_upload(ernie_hip_ctx* ctx, int index, const ernie_block_host_weights* w, int dim, int ffn,
                            int dtype);
+
+/* One host tensor with its own element type (ERNIE_DTYPE_FP32/FP16/BF16). */
+typedef struct {
+    const void* data;
+    int dtype;
+} ernie_host_tensor;
+/* The same eleven tensors, each in the element type it is stored in on disk:
+ * the reference's ModelBin keeps RMSNorm gammas as raw FP32 and tags each Gemm
+ * weight section FP32 or BF16 (tools/pack_block_weights.py:34-69,
+ * tools/build_dit_weights.py:88-121). */
+typedef struct {
+    ernie_host_tensor norm1, wq, wk, wv, norm_q, norm_k, wo, norm2, w_up, w_gate, w_down;
+} ernie_block_host_tensors;
+/* Replaces ModelBin loading of one block Net's weights (load_model of the
+ * RMSNorm and Gemm layers, src/component_files.cpp:55-60): each tensor is
+ * converted on the device to the storage dtype (gammas to FP32). The host
+ * memory may be released when the call returns. */
+int ernie_hip_block_upload_tensors(ernie_hip_ctx* ctx, int index, const ernie_block_host_tensors* w, int dim,
+                                   int ffn, int dtype);
 /* Synthetic block: matrices N(0, std), norm gammas 1 + N(0, std), from `seed`. */
 int ernie_hip_block_init_random(ernie_hip_ctx* ctx, int index, int dim, int ffn, int dtype, uint64_t seed,
                                 float std_dev);
