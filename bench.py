@@ -45,6 +45,9 @@ def parse():
     ap.add_argument("--valid-text", type=int, default=40)
     ap.add_argument("--cpu-baseline", choices=("on", "off"), default="on")
     ap.add_argument("--cpu-tokens", type=int, default=4160, help="tokens of the single-block CPU sample")
+    ap.add_argument("--events", choices=("dominant", "all"), default="dominant",
+                    help="HIP events in the timed steps: around the dominant kernel class only (its roofline), or "
+                         "around every launch; the per-class table always comes from one extra profiled step")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run a plain FP32 copy kernel of this many MiB three times (the reference "
                          "dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
@@ -127,8 +130,18 @@ def main():
     if args.warmup > 0:
         run(max(args.warmup, 1), 0)
     print(f"bench: warmup done ({args.warmup} steps)", file=sys.stderr, flush=True)
+    mfma_cls = ("gemm_qkv", "sdpa", "gemm_out", "gemm_up_gate", "gemm_down")
+    # One untimed step with events around every launch: the per-class table and
+    # the class that dominates device time.
     ctx.profile_reset()
     ctx.profile(True)
+    run(1, 0)
+    ctx.profile(False)
+    table = ctx.profile_query()
+    dom = max(mfma_cls, key=lambda c: table[c]["ms"])
+    # Timed steps: events bracket only the dominant class (or every launch with --events all).
+    ctx.profile_reset()
+    ctx.profile(True, classes=None if args.events == "all" else [dom])
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     step_s, _ = run(args.steps, 0)
@@ -139,19 +152,17 @@ def main():
     finite = bool(torch.isfinite(latent).all().item())
     print(f"bench: timed {args.steps} steps in {elapsed:.3f} s", file=sys.stderr, flush=True)
 
-    mfma_cls = ("gemm_qkv", "sdpa", "gemm_out", "gemm_up_gate", "gemm_down")
-    tot_flop = sum(prof[c]["flop"] for c in mfma_cls)
-    tot_ms = sum(prof[c]["ms"] for c in mfma_cls)
+    tot_flop = sum(table[c]["flop"] for c in mfma_cls)
+    tot_ms = sum(table[c]["ms"] for c in mfma_cls)
     peak = PEAK[args.precision]
-    dom = max(mfma_cls, key=lambda c: prof[c]["ms"])
     d = prof[dom]
     avg_s = d["ms"] / max(d["launches"], 1) * 1e-3
     flop_per_launch = d["flop"] / max(d["launches"], 1)
     achieved = flop_per_launch / avg_s if avg_s > 0 else 0.0
-    kernels = {c: {"launches": prof[c]["launches"], "avg_us": prof[c]["ms"] * 1e3 / max(prof[c]["launches"], 1),
-                   "tflops": (prof[c]["flop"] / (prof[c]["ms"] * 1e-3) / 1e12) if prof[c]["ms"] and prof[c]["flop"]
+    kernels = {c: {"launches": table[c]["launches"], "avg_us": table[c]["ms"] * 1e3 / max(table[c]["launches"], 1),
+                   "tflops": (table[c]["flop"] / (table[c]["ms"] * 1e-3) / 1e12) if table[c]["ms"] and table[c]["flop"]
                    else None,
-                   "gbps": (prof[c]["bytes"] / (prof[c]["ms"] * 1e-3) / 1e9) if prof[c]["ms"] else None}
+                   "gbps": (table[c]["bytes"] / (table[c]["ms"] * 1e-3) / 1e9) if table[c]["ms"] else None}
                for c in E.PROFILE_CLASSES}
     result = {
         "metric": METRIC, "value": args.steps / elapsed, "unit": "steps/s", "n_gpus": 1, "steps": args.steps,
@@ -167,6 +178,7 @@ def main():
                      "unit": "TFLOP/s", "frac": achieved / peak,
                      "traffic": MEASURED_TRAFFIC.get(args.precision, {}).get(dom) if args.grid == 64 else None,
                      "flop_per_launch": flop_per_launch, "avg_launch_us": avg_s * 1e6},
+        "events": args.events,
         "mfma_util_sdpa_gemm": (tot_flop / (tot_ms * 1e-3)) / peak if tot_ms else None,
         "sdpa_gemm_tflops": (tot_flop / (tot_ms * 1e-3)) / 1e12 if tot_ms else None,
         "kernels": kernels,

@@ -66,6 +66,7 @@ struct ernie_hip_ctx {
     DeviceBuffer split_ws;   // GEMM tail-row split-K partial sums
     // Event timing.
     bool profiling = false;
+    unsigned profile_mask = ~0u;  // classes that record events while profiling
     std::vector<hipEvent_t> event_pool;
     size_t event_next = 0;
     std::vector<Launch> pending;
@@ -159,7 +160,7 @@ struct Timed {
     hipEvent_t start = nullptr;
     Timed(ernie_hip_ctx* c, int k, double f, double b) : ctx(c), cls(k), flop(f), bytes(b)
     {
-        if (ctx->profiling) {
+        if (ctx->profiling && (ctx->profile_mask >> cls & 1u)) {
             start = next_event(ctx);
             if (start) (void)hipEventRecord(start, ctx->stream);
         }
@@ -984,6 +985,13 @@ int ernie_hip_profile_enable(ernie_hip_ctx* ctx, int enable)
         return rc;
     }
     ctx->profiling = true;
+    return ERNIE_OK;
+}
+
+int ernie_hip_profile_classes(ernie_hip_ctx* ctx, unsigned class_mask)
+{
+    if (!ctx) return ERNIE_ERROR;
+    ctx->profile_mask = class_mask;
     return ERNIE_OK;
 }
 

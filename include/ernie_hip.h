@@ -199,6 +199,10 @@ int ernie_hip_dit_forward(ernie_hip_ctx* ctx, const float* latent, int hw, const
  * 5 rmsnorm_modulate, 6 qk_norm_rope, 7 heads. */
 #define ERNIE_PROFILE_CLASSES 8
 int ernie_hip_profile_enable(ernie_hip_ctx* ctx, int enable);
+/* Restricts event recording to the classes whose bit is set (default: all), so a
+ * timed run brackets only the kernel it measures. No reference counterpart: the
+ * reference times whole blocks on the host clock (src/block_sequence.cpp:83-88, 247-253). */
+int ernie_hip_profile_classes(ernie_hip_ctx* ctx, unsigned class_mask);
 /* Synchronises and folds recorded launches into the totals. */
 int ernie_hip_profile_collect(ernie_hip_ctx* ctx);
 int ernie_hip_profile_reset(ernie_hip_ctx* ctx);
