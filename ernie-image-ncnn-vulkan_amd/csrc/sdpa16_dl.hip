@@ -6,8 +6,12 @@
 //
 //   * One workgroup = 4 waves = 128 queries of one head; each wave holds its 32
 //     queries' Q fragments in registers and computes S^T = K Q^T, so each lane owns
-//     one query column (softmax statistics need one lane^32 exchange) and the
-//     probabilities are already the B operand of O^T = V^T P^T.
+//     one query column and the probabilities are already the B operand of
+//     O^T = V^T P^T. Lanes l and l ^ 32 share a query: the tile maximum is exchanged
+//     with v_permlane32_swap (VALU, no LDS round trip) and the row sums are kept per
+//     lane and combined once after the last tile.
+//   * exp2 is the bare v_exp_f32: results below 2^-126 flush to zero, which cannot
+//     move a row sum that is at least 1.
 //   * K and V tiles (64 keys) reach LDS through direct global->LDS loads into a
 //     two-stage ring: no VGPR staging, no transpose on the way in. Key rows at or
 //     past the valid-key bound lie past the buffer range and load as zeros.
@@ -108,6 +112,18 @@ __device__ __forceinline__ int kswz(int r) { return r & 15; }
 __device__ __forceinline__ int vswz(int r) { return 2 * (r & 7); }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// max / sum of this lane's value and lane l ^ 32's (identical in both lanes).
+__device__ __forceinline__ float pair_max(float x)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 // Workgroup barrier without the release fence of __syncthreads() (that fence would
 // also wait for the tile still being loaded): LDS reads issued before it have
@@ -265,12 +281,12 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int r = 0; r < 16; r += 2) tmax = fmaxf(tmax, fmaxf(sacc[t][r], sacc[t][r + 1]));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        tmax = pair_max(tmax);
         if (!(MASKROW || partial)) tmax *= c;
         const bool raise = tmax > m_run + kRescaleSlack;
         if (__any(raise)) {
             const float m_new = raise ? tmax : m_run;
-            const float alpha = m_run == -INFINITY ? 0.f : exp2f(m_run - m_new);
+            const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
             l_run *= alpha;
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt)
@@ -286,7 +302,7 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
             for (int t = 0; t < 2; ++t)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const float pv = exp2f(sacc[t][r] - m_use);
+                    const float pv = __builtin_amdgcn_exp2f(sacc[t][r] - m_use);
                     psum += pv;
                     pf[t][r >> 3][r & 7] = T(pv);
                 }
@@ -295,13 +311,12 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
             for (int t = 0; t < 2; ++t)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const float pv = exp2f(__builtin_fmaf(sacc[t][r], c, -m_use));
+                    const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t][r], c, -m_use));
                     psum += pv;
                     pf[t][r >> 3][r & 7] = T(pv);
                 }
         }
-        psum += __shfl_xor(psum, 32, 64);
-        l_run += psum;
+        l_run += psum;  // this lane's keys only; the two halves are summed after the loop
 
         // O^T += V^T P^T; P's register r of (t, hh) is key 32t + 16hh + 8(r/4 & 1) + 4g + r%4.
         const uint8_t* vt = st + KV_BYTES;
@@ -322,6 +337,7 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
             }
     }
 
+    l_run = pair_sum(l_run);
     if (part >= 0) {
         // Key-range part of the split tail tile: unnormalised O and (m, l) for combine_kernel.
         const size_t slot = (size_t)h * p.tail_parts + part;
