@@ -57,7 +57,22 @@ __device__ __forceinline__ float wave_max(float v)
     return v;
 }
 
-// erf-form GELU, 0.5 * x * erfc(-x / sqrt(2)), FP32 arithmetic.
-__device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * erfcf(-0.7071067811865475f * x); }
+// erf-form GELU, x * Phi(x) = 0.5 * x * erfc(-x / sqrt(2)), in FP32 through
+// Abramowitz & Stegun 7.1.26 (|error in erf| <= 1.5e-7), the approximation the
+// reference's GPU layer evaluates (src/ernie_gelu.cpp:12-31): the tail
+// erfc(z) ~= t P(t) exp(-z^2), t = 1 / (1 + 0.3275911 z), z = |x| / sqrt(2), is
+// computed directly, so the negative side keeps its small values. One
+// reciprocal, one exp2 and five FMAs instead of the library erfc's branches.
+__device__ __forceinline__ float gelu_erf(float x)
+{
+    const float z = fabsf(x) * 0.7071067811865475f;
+    const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f, z, 1.0f));
+    float p = __builtin_fmaf(1.061405429f, t, -1.453152027f);
+    p = __builtin_fmaf(p, t, 1.421413741f);
+    p = __builtin_fmaf(p, t, -0.284496736f);
+    p = __builtin_fmaf(p, t, 0.254829592f);
+    const float tail = p * t * __builtin_amdgcn_exp2f(-1.4426950408889634f * z * z);
+    return x * (x >= 0.f ? __builtin_fmaf(-0.5f, tail, 1.0f) : 0.5f * tail);
+}
 
 }  // namespace ehip
