@@ -1,8 +1,10 @@
 // SPDX-License-Identifier: MIT
 // Flash SDPA for 16-bit operands with head_dim 128 on gfx950: the path the DiT
 // block takes (ErnieSDPA, src/ernie_attention.cpp:35-233; sdpa_22 in
-// block.ncnn.param line 58) with no mask or one additive mask row broadcast over
-// the queries (src/ernie_attention.cpp:201-221), plus a valid-key bound.
+// block.ncnn.param line 58) with no mask, one additive mask row broadcast over the
+// queries or a per-query mask (src/ernie_attention.cpp:201-221), plus a
+// valid-key bound. Every mask form goes through the same arithmetic, so a row
+// mask and its dense broadcast give bitwise identical results.
 //
 //   * One workgroup = 4 waves = 128 queries of one head; each wave holds its 32
 //     queries' Q fragments in registers and computes S^T = K Q^T, so each lane owns
@@ -12,9 +14,15 @@
 //     lane and combined once after the last tile.
 //   * exp2 is the bare v_exp_f32: results below 2^-126 flush to zero, which cannot
 //     move a row sum that is at least 1.
-//   * K and V tiles (64 keys) reach LDS through direct global->LDS loads into a
-//     two-stage ring: no VGPR staging, no transpose on the way in. Key rows at or
-//     past the valid-key bound lie past the buffer range and load as zeros.
+//   * K and V tiles (64 keys) reach LDS through direct global->LDS loads into two
+//     two-stage rings, K one tile ahead of V: no VGPR staging, no transpose on the
+//     way in. Key rows at or past the valid-key bound lie past the buffer range and
+//     load as zeros.
+//   * Software pipeline: while the matrix cores compute S of tile i+1, the VALU turns
+//     S of tile i into probabilities (sched_group_barrier interleaves the two), then
+//     P_i V_i accumulates and tile i+1's maximum is taken.
+//   * Row sums use v_dot2_f32_{f16,bf16} on the rounded probabilities the MFMA
+//     consumes, so numerator and denominator see the same weights.
 //   * V^T fragments come from ds_read_b64_tr_b16: within each 16-lane group, lane
 //     i receives the (i % 4)-th 16-bit value at the addresses of lanes 4e + i/4
 //     (e = 0..3), so lanes pointing at 4 consecutive key rows deliver 4 keys of
@@ -39,7 +47,9 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int BQ = 128, BKV = 64, D = 128;
 constexpr int ROWB = D * 2;                 // 256 bytes per staged key row
 constexpr int KV_BYTES = BKV * ROWB;        // 16 KiB
-constexpr int STAGE = 2 * KV_BYTES + BKV * 4;  // K, V, mask row
+constexpr int KSTAGE = KV_BYTES + BKV * 4;  // K tile + its mask row
+constexpr int V_BASE = 2 * KSTAGE;           // the V ring follows the two K stages
+constexpr int LDS_BYTES = V_BASE + 2 * KV_BYTES;
 constexpr uint32_t kRsrcFlags = 0x00020000;
 constexpr float kRescaleSlack = 8.0f;
 
@@ -47,7 +57,7 @@ struct Params {
     const void* q; const void* k; const void* v; void* o;
     int heads, group, sq, sk, kv_end;
     long q_hs, q_rs, k_hs, k_rs, v_hs, v_rs, o_hs, o_rs;
-    const float* mask; long mask_hs;
+    const float* mask; long mask_hs;  // additive FP32 mask: one row [sk] or per query [sq][sk] per head
     float scale_log2;
     // Split of the last, partial query tile (sq % 128 queries) along the keys:
     // tail_parts > 0 parts per head write unnormalised FP32 O and their (m, l) to
@@ -84,8 +94,19 @@ __global__ void __launch_bounds__(256) combine_kernel(Params p, int tail_q)
 }
 
 template <typename T> struct Mfma;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
 template <> struct Mfma<f16> {
     typedef f16x8 vec;
+    // acc + the sum of the 8 probabilities, as stored for the MFMA (v_dot2_f32_f16 against 1).
+    static __device__ __forceinline__ float rowsum(vec p, float acc)
+    {
+        const f16x2 one = {(f16)1.0f, (f16)1.0f};
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) acc = __builtin_amdgcn_fdot2(f16x2{p[i], p[i + 1]}, one, acc, false);
+        return acc;
+    }
     typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 tr4;
     static __device__ __forceinline__ f32x16 run(vec a, vec b, f32x16 c)
     { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
@@ -96,6 +117,13 @@ template <> struct Mfma<f16> {
 };
 template <> struct Mfma<bf16> {
     typedef bf16x8 vec;
+    static __device__ __forceinline__ float rowsum(vec p, float acc)
+    {
+        const bf16x2 one = {(bf16)1.0f, (bf16)1.0f};
+#pragma unroll
+        for (int i = 0; i < 8; i += 2) acc = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{p[i], p[i + 1]}, one, acc, false);
+        return acc;
+    }
     typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 tr4;
     static __device__ __forceinline__ f32x16 run(vec a, vec b, f32x16 c)
     { return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0); }
@@ -112,6 +140,16 @@ __device__ __forceinline__ int kswz(int r) { return r & 15; }
 __device__ __forceinline__ int vswz(int r) { return 2 * (r & 7); }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// max(a, b, c) in one v_max3_f32. Written out because the compiler otherwise
+// canonicalises every MFMA result before a two-input v_max (NaN-quieting that
+// scores never need), tripling the instruction count of the tile maximum.
+__device__ __forceinline__ float max3(float a, float b, float c)
+{
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
 
 // max / sum of this lane's value and lane l ^ 32's (identical in both lanes).
 __device__ __forceinline__ float pair_max(float x)
@@ -130,11 +168,14 @@ __device__ __forceinline__ float pair_sum(float x)
 // returned and the memory clobber keeps LDS accesses on their side.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-template <typename T, bool MASKROW>
+// Mask modes: none, one row broadcast over the queries, one row per query.
+enum { MASK_NONE = 0, MASK_ROW = 1, MASK_DENSE = 2 };
+
+template <typename T, int MM>
 __global__ void __launch_bounds__(256, 2) kernel(Params p)
 {
     typedef typename Mfma<T>::vec vec8;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[LDS_BYTES];
 
     // Workgroup -> (head, query tile[, key range]). Workgroup b runs on XCD b % 8:
     // each XCD takes a contiguous range of full query tiles (so a head's K / V stream
@@ -188,14 +229,19 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
     const uint32_t v_bytes = (uint32_t)(((long)(p.kv_end - 1) * p.v_rs + D) * 2);
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(Kh), (short)0, k_bytes, kRsrcFlags);
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(Vh), (short)0, v_bytes, kRsrcFlags);
+    constexpr bool MASKROW = MM == MASK_ROW, DENSE = MM == MASK_DENSE;
     __amdgpu_buffer_rsrc_t rm;
-    if constexpr (MASKROW)
+    if constexpr (DENSE)
+        rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.mask + (size_t)h * p.mask_hs), (short)0,
+                                               (uint32_t)((size_t)p.sq * p.sk * 4), kRsrcFlags);
+    else if constexpr (MASKROW)
         rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.mask + (size_t)h * p.mask_hs), (short)0,
                                                (uint32_t)(p.sk * 4), kRsrcFlags);
 
     // Direct loads: wave w fills key rows [16w, 16w+16) of the K and V tiles with
     // four 1-KiB instructions each (4 rows x 256 bytes); lane l lands at row l >> 4,
-    // physical chunk l & 15.
+    // physical chunk l & 15. K (with its mask row) and V have rings of their own
+    // because K runs one tile ahead of V.
     uint32_t k_src[4], v_src[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -204,36 +250,46 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
         v_src[q] = (uint32_t)(((long)row * p.v_rs * 2) + (((lane & 15) ^ vswz(row)) << 4));
     }
     const uint32_t k_tile = (uint32_t)(BKV * p.k_rs * 2), v_tile = (uint32_t)(BKV * p.v_rs * 2);
-    auto issue = [&](int it, int slot) {
-        uint8_t* st = smem + slot * STAGE;
+    auto kstage = [&](int slot) { return smem + slot * KSTAGE; };
+    auto vstage = [&](int slot) { return smem + V_BASE + slot * KV_BYTES; };
+    auto issue_k = [&](int it, int slot) {
+        uint8_t* st = kstage(slot);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < 4; ++q)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr_t)(st + (wave * 16 + q * 4) * ROWB), 16, k_src[q],
                                                      it * k_tile, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_ptr_t)(st + KV_BYTES + (wave * 16 + q * 4) * ROWB), 16,
-                                                     v_src[q], it * v_tile, 0, 0);
-        }
         if constexpr (MASKROW) {
             if (wave == 0)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_ptr_t)(st + 2 * KV_BYTES), 4, lane * 4,
-                                                         it * BKV * 4, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rm, (lds_ptr_t)(st + KV_BYTES), 4, lane * 4, it * BKV * 4, 0, 0);
         }
     };
-
-    // K fragment (A of S^T = K Q^T): key 32t + lrow, logical chunk 2s + g.
-    uint32_t k_rd[2];
+    auto issue_v = [&](int it, int slot) {
+        uint8_t* st = vstage(slot);
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const int key = 32 * t + lrow;
-        k_rd[t] = key * ROWB;
-    }
-    const int ksw = kswz(lrow);  // same for key 32t + lrow
+        for (int q = 0; q < 4; ++q)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_ptr_t)(st + (wave * 16 + q * 4) * ROWB), 16, v_src[q],
+                                                     it * v_tile, 0, 0);
+    };
+
+    // K fragment (A of S^T = K Q^T): key 32t + lrow, logical chunk 2s + g. The
+    // swizzle depends on lrow only, so per-lane offsets are fixed and the key-half
+    // and stage offsets fold into the instructions' immediate offsets.
+    uint32_t k_off[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) k_off[s] = lrow * ROWB + (((2 * s + g) ^ kswz(lrow)) << 4);
     // V^T fragment (A of O^T = V^T P^T) by transposing reads: 16-lane group G = lane >> 4
-    // (k-half g = G >> 1, d half 16 (G & 1)), lane j = lane & 15 points at key
-    // kb + (j >> 2), values d0 + 16 (G & 1) + 4 (j & 3) .. + 3.
+    // (k-half G >> 1, d half 16 (G & 1)), lane j = lane & 15 points at key
+    // kb + 4 (G >> 1) + (j >> 2) with kb a multiple of 8, so its swizzle 2 (key & 7)
+    // is fixed per lane; values d0 + 16 (G & 1) + 4 (j & 3) .. + 3.
     const int G = lane >> 4, j = lane & 15;
     const int v_key_off = 4 * (G >> 1) + (j >> 2);
     const int v_d = 16 * (G & 1) + 4 * (j & 3);
+    uint32_t v_off[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+        const int d = 32 * dt + v_d;
+        v_off[dt] = v_key_off * ROWB + (((d >> 3) ^ vswz(v_key_off)) << 4) + (d & 7) * 2;
+    }
 
     f32x16 oacc[4];
 #pragma unroll
@@ -243,46 +299,59 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
     float m_run = -INFINITY, l_run = 0.f;
     const float c = p.scale_log2;
 
-    if (it0 < it1) issue(it0, 0);
-    for (int it = it0; it < it1; ++it) {
-        const int buf = (it - it0) & 1;
-        const int kv0 = it * BKV;
-        __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // this wave's loads of tile it have landed
-        lds_barrier();                                         // ... and every wave's; tile it-1 is consumed
-        if (it + 1 < it1) issue(it + 1, buf ^ 1);
-        const uint8_t* st = smem + buf * STAGE;
-
-        f32x16 sacc[2];
+    // S^T of one key tile: sacc[t] holds keys 32t + 8(r/4) + 4g + r%4 for this lane's
+    // query. With a mask the accumulators start at mask / scale, so the scaled score
+    // is s c + mask log2(e) without holding the mask in registers. A row mask comes
+    // from LDS; a per-query mask row is read straight from memory (its keys past sk
+    // read as zero through the buffer range, and fall past kv_end anyway).
+    const float inv_scale = kLog2e / c;
+    const uint32_t dense_row = (uint32_t)(min(my_q, p.sq - 1) * p.sk) * 4u;
+    auto qk = [&](const uint8_t* ks, int kv0, f32x16 (&sacc)[2]) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
+            if constexpr (MASKROW) {
+                const float* ms = reinterpret_cast<const float*>(ks + KV_BYTES);
 #pragma unroll
-            for (int r = 0; r < 16; ++r) sacc[t][r] = 0.f;
+                for (int r = 0; r < 16; ++r) sacc[t][r] = ms[32 * t + 8 * (r >> 2) + 4 * g + (r & 3)] * inv_scale;
+            } else if constexpr (DENSE) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int kk = 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
+                    const float mv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                                   rm, dense_row + (uint32_t)(kv0 + kk) * 4u, 0, 0));
+                    sacc[t][r] = mv * inv_scale;
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sacc[t][r] = 0.f;
+            }
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
-                const vec8 kf = *reinterpret_cast<const vec8*>(st + k_rd[t] + (((2 * s + g) ^ ksw) << 4));
+                const vec8 kf = *reinterpret_cast<const vec8*>(ks + k_off[s] + t * 32 * ROWB);
                 sacc[t] = Mfma<T>::run(kf, qf[s], sacc[t]);
             }
         }
-        const bool partial = kv0 + BKV > p.kv_end;
-        if (MASKROW || partial) {
-            const float* ms = reinterpret_cast<const float*>(st + 2 * KV_BYTES);
+    };
+    // Mask, bound and tile maximum (log2 domain) of tile `it`; raises the running
+    // offset when the maximum passes it by more than the slack. Returns the factor
+    // the softmax applies to the scores: 1 when they were scaled here, else c.
+    auto prep = [&](f32x16 (&sacc)[2], int it) -> float {
+        const int kv0 = it * BKV;
+        const bool scaled = MM != MASK_NONE || kv0 + BKV > p.kv_end;
+        if (scaled) {
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int kk = 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
-                    float v = sacc[t][r] * c;
-                    if constexpr (MASKROW) v += ms[kk] * kLog2e;
-                    sacc[t][r] = kv0 + kk < p.kv_end ? v : -INFINITY;
+                    sacc[t][r] = kv0 + kk < p.kv_end ? sacc[t][r] * c : -INFINITY;
                 }
         }
-        float tmax = -INFINITY;
+        float tmax = max3(sacc[0][0], sacc[0][1], sacc[0][2]);
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int r = 0; r < 16; r += 2) tmax = fmaxf(tmax, fmaxf(sacc[t][r], sacc[t][r + 1]));
-        tmax = pair_max(tmax);
-        if (!(MASKROW || partial)) tmax *= c;
+        for (int i = 3; i < 31; i += 2) tmax = max3(tmax, sacc[i >> 4][i & 15], sacc[(i + 1) >> 4][(i + 1) & 15]);
+        tmax = pair_max(fmaxf(tmax, sacc[1][15]));
+        if (!scaled) tmax *= c;
         const bool raise = tmax > m_run + kRescaleSlack;
         if (__any(raise)) {
             const float m_new = raise ? tmax : m_run;
@@ -294,32 +363,23 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
                 for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
             m_run = m_new;
         }
+        return scaled ? 1.f : c;
+    };
+    // Probabilities of a prepared tile as MFMA B operands, and their row sum.
+    auto softmax = [&](const f32x16 (&sacc)[2], float cs, vec8 (&pf)[2][2]) {
         const float m_use = m_run == -INFINITY ? 0.f : m_run;
-        float psum = 0.f;
-        vec8 pf[2][2];
-        if (MASKROW || partial) {
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const float pv = __builtin_amdgcn_exp2f(sacc[t][r] - m_use);
-                    psum += pv;
-                    pf[t][r >> 3][r & 7] = T(pv);
-                }
-        } else {
+            for (int r = 0; r < 16; ++r)
+                pf[t][r >> 3][r & 7] = T(__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t][r], cs, -m_use)));
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t][r], c, -m_use));
-                    psum += pv;
-                    pf[t][r >> 3][r & 7] = T(pv);
-                }
-        }
-        l_run += psum;  // this lane's keys only; the two halves are summed after the loop
-
-        // O^T += V^T P^T; P's register r of (t, hh) is key 32t + 16hh + 8(r/4 & 1) + 4g + r%4.
-        const uint8_t* vt = st + KV_BYTES;
+            for (int hh = 0; hh < 2; ++hh) l_run = Mfma<T>::rowsum(pf[t][hh], l_run);
+    };
+    // O^T += V^T P^T; P's register r of (t, hh) is key 32t + 16hh + 8(r/4 & 1) + 4g + r%4.
+    auto pv = [&](const uint8_t* vt, const vec8 (&pf)[2][2]) {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -327,14 +387,70 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
                 const int kb = 32 * t + 16 * hh;
 #pragma unroll
                 for (int dt = 0; dt < 4; ++dt) {
-                    const int d = 32 * dt + v_d;
-                    const int k_lo = kb + v_key_off, k_hi = kb + 8 + v_key_off;
-                    const u32x2 lo = Mfma<T>::tr(vt + k_lo * ROWB + (((d >> 3) ^ vswz(k_lo)) << 4) + (d & 7) * 2);
-                    const u32x2 hi = Mfma<T>::tr(vt + k_hi * ROWB + (((d >> 3) ^ vswz(k_hi)) << 4) + (d & 7) * 2);
+                    const u32x2 lo = Mfma<T>::tr(vt + v_off[dt] + kb * ROWB);
+                    const u32x2 hi = Mfma<T>::tr(vt + v_off[dt] + (kb + 8) * ROWB);
                     const u32x4 packed = {lo[0], lo[1], hi[0], hi[1]};
                     oacc[dt] = Mfma<T>::run(__builtin_bit_cast(vec8, packed), pf[t][hh], oacc[dt]);
                 }
             }
+    };
+
+    // Software pipeline over the key tiles i = 0 .. n-1 of [it0, it1): step i computes
+    // S of tile i+1 on the matrix cores while the VALU turns the prepared S of tile i
+    // into probabilities, then accumulates P_i V_i and prepares tile i+1. K_{i+1} and
+    // V_i are in LDS at the top of step i; it loads K_{i+2} and V_{i+1} into the
+    // stages tiles i and i-1 left.
+    const int n = it1 - it0;
+    f32x16 sa[2], sb[2];
+    vec8 pf[2][2];
+    float cs_cur = c, cs_nxt = c;
+    auto step = [&](int i, f32x16 (&cur)[2], f32x16 (&nxt)[2], auto has_next) {
+        __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // this wave's loads of K_{i+1}, V_i landed
+        lds_barrier();                                         // ... every wave's; tile i-1 fully consumed
+        if constexpr (decltype(has_next)::value) {
+            if (i + 2 < n) issue_k(it0 + i + 2, i & 1);
+            issue_v(it0 + i + 1, (i + 1) & 1);
+            qk(kstage((i + 1) & 1), (it0 + i + 1) * BKV, nxt);
+            softmax(cur, cs_cur, pf);
+            // Interleave the 16 K-fragment reads and MFMAs of the next tile with the
+            // softmax of this one (independent work for the VALU under each MFMA).
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);  // VALU incl. transcendental
+            }
+            pv(vstage(i & 1), pf);
+            cs_nxt = prep(nxt, it0 + i + 1);
+        } else {
+            softmax(cur, cs_cur, pf);
+            pv(vstage(i & 1), pf);
+        }
+    };
+    typedef std::integral_constant<bool, true> more;
+    typedef std::integral_constant<bool, false> last;
+    if (n > 0) {
+        issue_k(it0, 0);
+        issue_v(it0, 0);
+        if (n > 1) issue_k(it0 + 1, 1);
+        __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
+        lds_barrier();
+        qk(kstage(0), it0 * BKV, sa);
+        cs_cur = prep(sa, it0);
+        int i = 0;
+        for (; i + 2 < n; i += 2) {
+            step(i, sa, sb, more());
+            cs_cur = cs_nxt;
+            step(i + 1, sb, sa, more());
+            cs_cur = cs_nxt;
+        }
+        if (n - i == 2) {
+            step(i, sa, sb, more());
+            cs_cur = cs_nxt;
+            step(i + 1, sb, sa, last());
+        } else {
+            step(i, sa, sb, last());
+        }
     }
 
     l_run = pair_sum(l_run);
@@ -374,11 +490,11 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
 }  // namespace sdl
 
 // Returns 1 without launching when the problem is not one this kernel takes
-// (FP32, head_dim != 128, per-query masks, unaligned strides, >= 2 GiB K/V spans).
+// (FP32, head_dim != 128, unaligned strides, >= 2 GiB K/V spans or per-query masks).
 int sdpa16_d128(const SdpaArgs& a, hipStream_t s)
 {
     if (a.dtype == DT_F32 || a.d != 128) return 1;
-    if (a.mask && a.mask_rows != 1) return 1;
+    if (a.mask && a.mask_rows != 1 && (size_t)a.sq * a.sk * 4 >= 2147483648ull) return 1;
     const long vec = 8;
     const uintptr_t bases = reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.k) |
                             reinterpret_cast<uintptr_t>(a.v) | reinterpret_cast<uintptr_t>(a.o);
@@ -394,7 +510,8 @@ int sdpa16_d128(const SdpaArgs& a, hipStream_t s)
     p.q_hs = a.q_hs; p.q_rs = a.q_rs; p.k_hs = a.k_hs; p.k_rs = a.k_rs;
     p.v_hs = a.v_hs; p.v_rs = a.v_rs; p.o_hs = a.o_hs; p.o_rs = a.o_rs;
     p.mask = a.mask;
-    p.mask_hs = a.mask && a.mask_heads > 1 ? (long)a.sk : 0;
+    const bool dense = a.mask && a.mask_rows > 1;
+    p.mask_hs = a.mask && a.mask_heads > 1 ? (long)a.sk * (dense ? a.sq : 1) : 0;
     const float scale = a.scale > 0.f ? a.scale : 1.f / sqrtf(128.f);
     p.scale_log2 = scale * sdl::kLog2e;
     // A partial last query tile is split along the keys when a workspace is given:
@@ -414,11 +531,13 @@ int sdpa16_d128(const SdpaArgs& a, hipStream_t s)
     const int wgs = p.tail_parts ? (p.full_qt + p.tail_parts) * a.heads : ((a.sq + sdl::BQ - 1) / sdl::BQ) * a.heads;
     const dim3 grid(wgs), block(256);
     if (a.dtype == DT_F16) {
-        if (a.mask) hipLaunchKernelGGL((sdl::kernel<f16, true>), grid, block, 0, s, p);
-        else hipLaunchKernelGGL((sdl::kernel<f16, false>), grid, block, 0, s, p);
+        if (dense) hipLaunchKernelGGL((sdl::kernel<f16, sdl::MASK_DENSE>), grid, block, 0, s, p);
+        else if (a.mask) hipLaunchKernelGGL((sdl::kernel<f16, sdl::MASK_ROW>), grid, block, 0, s, p);
+        else hipLaunchKernelGGL((sdl::kernel<f16, sdl::MASK_NONE>), grid, block, 0, s, p);
     } else {
-        if (a.mask) hipLaunchKernelGGL((sdl::kernel<bf16, true>), grid, block, 0, s, p);
-        else hipLaunchKernelGGL((sdl::kernel<bf16, false>), grid, block, 0, s, p);
+        if (dense) hipLaunchKernelGGL((sdl::kernel<bf16, sdl::MASK_DENSE>), grid, block, 0, s, p);
+        else if (a.mask) hipLaunchKernelGGL((sdl::kernel<bf16, sdl::MASK_ROW>), grid, block, 0, s, p);
+        else hipLaunchKernelGGL((sdl::kernel<bf16, sdl::MASK_NONE>), grid, block, 0, s, p);
     }
     if (p.tail_parts) {
         const long n = (long)a.heads * tail_q * sdl::D;
