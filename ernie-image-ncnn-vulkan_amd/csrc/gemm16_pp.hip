@@ -296,6 +296,39 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
     }
 
     // Accumulator (32x32 f32): lane -> column lane%32; register r -> row 8(r/4) + 4(lane/32) + r%4.
+    if constexpr (EPI == EPI_GATE_RESID) {
+        // C = resid + gate * acc, C possibly aliasing resid. Each element is read and
+        // written by this lane only, so the gate pair and a 32-row block's residuals
+        // are loaded before any of the block's stores: 32 loads in flight per lane
+        // instead of one load-wait-store round trip per element.
+        float gv[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int n = n0 + wn * 64 + j * 32 + lrow;
+            gv[j] = n < p.N ? p.gate[n] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < MSUB; ++i) {
+            const int mb = m0 + wm * 32 * MSUB + i * 32 + 4 * lgrp;
+            float rv[16][2];
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int m = mb + 8 * (r >> 2) + (r & 3), n = n0 + wn * 64 + j * 32 + lrow;
+                    rv[r][j] = m < p.M && n < p.N ? p.resid[(size_t)m * p.ld_resid + n] : 0.f;
+                }
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int m = mb + 8 * (r >> 2) + (r & 3), n = n0 + wn * 64 + j * 32 + lrow;
+                    if (m < p.M && n < p.N)
+                        static_cast<float*>(p.C)[(size_t)m * p.ldc + n] = __builtin_fmaf(gv[j], acc[i][j][r], rv[r][j]);
+                }
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < MSUB; ++i) {
 #pragma unroll
