@@ -107,6 +107,67 @@ __global__ void __launch_bounds__(256) rmsnorm_rows_kernel(const TIn* __restrict
     }
 }
 
+// Same operation for widths of PER x 1024 (the block width 4096 has PER = 4):
+// persistent 256-thread workgroups striding over the rows. Thread t owns the
+// four-column groups t + 256 i, so its factors gamma (1 + scale) and shift stay
+// in registers for every row it touches, and the next row's load is in flight
+// while this row is reduced (wave sums, then the four wave partials through a
+// double-buffered LDS slot: one barrier per row) and stored.
+template <typename TIn, typename TOut, int PER>
+__global__ void __launch_bounds__(256) rmsnorm_persist_kernel(const TIn* __restrict__ x,
+                                                              const float* __restrict__ gamma,
+                                                              const float* __restrict__ shift,
+                                                              const float* __restrict__ scale, int rows, float eps,
+                                                              TOut* __restrict__ out)
+{
+    constexpr int width = PER * 1024;
+    __shared__ float red[2][4];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    f32x4 m[PER], a[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int c = 4 * (tid + 256 * i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float g = gamma ? gamma[c + e] : 1.0f;
+            m[i][e] = scale ? g * (scale[c + e] + 1.0f) : g;
+            a[i][e] = shift ? shift[c + e] : 0.0f;
+        }
+    }
+    int r = blockIdx.x;
+    f32x4 v[PER];
+    if (r < rows) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) v[i] = Vec4<TIn>::load(x + (size_t)r * width + 4 * (tid + 256 * i));
+    }
+    for (int it = 0; r < rows; r += gridDim.x, ++it) {
+        const int rn = r + gridDim.x;
+        f32x4 vn[PER];
+        if (rn < rows) {
+#pragma unroll
+            for (int i = 0; i < PER; ++i) vn[i] = Vec4<TIn>::load(x + (size_t)rn * width + 4 * (tid + 256 * i));
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) ss += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
+        ss = wave_sum(ss);
+        if (lane == 0) red[it & 1][wave] = ss;
+        __syncthreads();
+        const float tot = (red[it & 1][0] + red[it & 1][1]) + (red[it & 1][2] + red[it & 1][3]);
+        const float inv = 1.0f / sqrtf(tot / float(width) + eps);
+        TOut* orow = out + (size_t)r * width;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            f32x4 y;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[e] = (v[i][e] * inv) * m[i][e] + a[i][e];
+            Vec4<TOut>::store(orow + 4 * (tid + 256 * i), y);
+        }
+#pragma unroll
+        for (int i = 0; i < PER; ++i) v[i] = vn[i];
+    }
+}
+
 template <typename TOut>
 __global__ void __launch_bounds__(256) layernorm_mod_kernel(const float* __restrict__ x,
                                                             const float* __restrict__ shift,
@@ -322,8 +383,32 @@ template <typename TIn>
 int rms_dispatch_out(const TIn* x, const float* gamma, const float* shift, const float* scale, int rows, int width,
                      float eps, void* out, int odt, hipStream_t s)
 {
-    // Rows per workgroup: enough workgroups to cover the CUs several times over,
-    // with the per-column vectors staged once per workgroup.
+    if (width % 1024 == 0) {
+        // Four persistent workgroups per CU of an MI355X (256 CUs), never more than the rows.
+        const dim3 grid((unsigned)std::min(rows, 1024)), block(256);
+#define EHIP_RMS_PERSIST(PER)                                                                                    \
+        do {                                                                                                     \
+            if (odt == DT_F32)                                                                                   \
+                hipLaunchKernelGGL((rmsnorm_persist_kernel<TIn, float, PER>), grid, block, 0, s, x, gamma, shift, \
+                                   scale, rows, eps, static_cast<float*>(out));                                  \
+            else if (odt == DT_F16)                                                                              \
+                hipLaunchKernelGGL((rmsnorm_persist_kernel<TIn, f16, PER>), grid, block, 0, s, x, gamma, shift,   \
+                                   scale, rows, eps, static_cast<f16*>(out));                                    \
+            else                                                                                                 \
+                hipLaunchKernelGGL((rmsnorm_persist_kernel<TIn, bf16, PER>), grid, block, 0, s, x, gamma, shift,  \
+                                   scale, rows, eps, static_cast<bf16*>(out));                                   \
+        } while (0)
+        switch (width / 1024) {
+        case 1: EHIP_RMS_PERSIST(1); break;
+        case 2: EHIP_RMS_PERSIST(2); break;
+        case 3: EHIP_RMS_PERSIST(3); break;
+        default: EHIP_RMS_PERSIST(4); break;
+        }
+#undef EHIP_RMS_PERSIST
+        return launch_status();
+    }
+    // Other widths. Rows per workgroup: enough workgroups to cover the CUs several
+    // times over, with the per-column vectors staged once per workgroup.
     const int rpb = rows >= 2048 ? 8 : (rows >= 512 ? 4 : 1);
     const dim3 grid((rows + rpb - 1) / rpb), block(64 * kRowWaves);
     if (odt == DT_F32)
