@@ -34,6 +34,9 @@ struct BlockWeights {
     DeviceBuffer wo;                            // [dim][dim]
     DeviceBuffer w_ug;                          // [2*ffn][dim], 32-row up/gate interleave
     DeviceBuffer w_down;                        // [dim][ffn]
+    // 16-bit projections whose output count is a multiple of 256 are stored K-tiled,
+    // [K/32][N][32] (GemmArgs::w_k32); flags for wqkv, wo, w_ug, w_down.
+    bool k32[4] = {false, false, false, false};
 };
 
 struct HeadWeights {
@@ -244,6 +247,30 @@ int alloc_block(ernie_hip_ctx* ctx, BlockWeights& w, int dim, int ffn, int dtype
     return ERNIE_OK;
 }
 
+// Rewrites the 16-bit projection matrices of a freshly written block K-tiled,
+// through the staging buffer, and records which ones were.
+int tile_block_weights(ernie_hip_ctx* ctx, BlockWeights& w)
+{
+    if (w.dtype == ERNIE_DTYPE_FP32) return ERNIE_OK;
+    const int D = w.dim, F = w.ffn;
+    struct Mat { DeviceBuffer* b; int rows, cols; };
+    const Mat mats[4] = {{&w.wqkv, 3 * D, D}, {&w.wo, D, D}, {&w.w_ug, 2 * F, D}, {&w.w_down, D, F}};
+    size_t most = 0;
+    for (const Mat& m : mats) most = std::max(most, (size_t)m.rows * m.cols * 2);
+    int rc = dev_alloc(ctx, ctx->staging, most, "staging buffer");
+    for (int i = 0; i < 4 && !rc; ++i) {
+        const Mat& m = mats[i];
+        const size_t bytes = (size_t)m.rows * m.cols * 2;
+        if (m.rows % 256 || m.cols % 32 || bytes >= (1ull << 31)) continue;
+        rc = hip_status(ctx, hipMemcpyAsync(ctx->staging.ptr, m.b->ptr, bytes, hipMemcpyDeviceToDevice, ctx->stream),
+                        "tile weights");
+        if (!rc) rc = kernel_status(ctx, tile_k32(ctx->staging.ptr, m.b->ptr, m.rows, m.cols, ctx->stream), "tile weights");
+        if (!rc) w.k32[i] = true;
+    }
+    if (!rc) rc = hip_status(ctx, hipStreamSynchronize(ctx->stream), "tile weights");
+    return rc;
+}
+
 int check_block_dims(ernie_hip_ctx* ctx, int dim, int ffn, int dtype)
 {
     if (!valid_dtype(dtype)) return fail(ctx, ERNIE_ERROR, "invalid dtype");
@@ -332,6 +359,7 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
     {
         GemmArgs g;
         g.A = ws.h; g.lda = D; g.W = w.wqkv.ptr; g.ldw = D; g.M = S; g.N = 3 * D; g.K = D; g.dtype = dt;
+        g.w_k32 = w.k32[0];
         g.epilogue = EPI_STORE; g.C = ws.qkv; g.ldc = 3 * D; g.c_dtype = dt;
         rc = split_workspace(ctx, S, H, &g.split_ws, &g.split_ws_bytes);
         if (rc) return rc;
@@ -366,6 +394,7 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
     {
         GemmArgs g;
         g.A = ws.attn; g.lda = D; g.W = w.wo.ptr; g.ldw = D; g.M = S; g.N = D; g.K = D; g.dtype = dt;
+        g.w_k32 = w.k32[1];
         g.epilogue = EPI_GATE_RESID; g.C = ws.x1; g.ldc = D; g.c_dtype = ERNIE_DTYPE_FP32; g.resid = x; g.ld_resid = D;
         g.gate = gate_sa;
         rc = split_workspace(ctx, S, H, &g.split_ws, &g.split_ws_bytes);
@@ -385,6 +414,7 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
     {
         GemmArgs g;
         g.A = ws.h; g.lda = D; g.W = w.w_ug.ptr; g.ldw = D; g.M = S; g.N = 2 * F; g.K = D; g.dtype = dt;
+        g.w_k32 = w.k32[2];
         g.epilogue = EPI_GEGLU; g.C = ws.p; g.ldc = F; g.c_dtype = dt;
         rc = split_workspace(ctx, S, H, &g.split_ws, &g.split_ws_bytes);
         if (rc) return rc;
@@ -396,6 +426,7 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
     {
         GemmArgs g;
         g.A = ws.p; g.lda = F; g.W = w.w_down.ptr; g.ldw = F; g.M = S; g.N = D; g.K = F; g.dtype = dt;
+        g.w_k32 = w.k32[3];
         g.epilogue = EPI_GATE_RESID; g.C = out; g.ldc = D; g.c_dtype = ERNIE_DTYPE_FP32; g.resid = ws.x1; g.ld_resid = D;
         g.gate = gate_mlp;
         rc = split_workspace(ctx, S, H, &g.split_ws, &g.split_ws_bytes);
@@ -728,6 +759,7 @@ int ernie_hip_block_upload_tensors(ernie_hip_ctx* ctx, int index, const ernie_bl
     }
     // Host memory may be released once this returns: every copy out of it has finished.
     if (!rc) rc = hip_status(ctx, hipStreamSynchronize(ctx->stream), "block upload");
+    if (!rc) rc = tile_block_weights(ctx, bw);
     if (rc) {
         free_block(bw);
         return rc;
@@ -774,6 +806,7 @@ int ernie_hip_block_init_random(ernie_hip_ctx* ctx, int index, int dim, int ffn,
         if (rc) break;
     }
     if (!rc) rc = hip_status(ctx, hipStreamSynchronize(s), "init");
+    if (!rc) rc = tile_block_weights(ctx, bw);
     if (rc) {
         free_block(bw);
         return rc;

@@ -18,6 +18,10 @@
 //   * Each wave owns a 128 x 64 sub-tile (4 x 2 accumulators of 32 x 32). Rows past
 //     M and columns past N read as zero through the buffer range checks; tail tiles
 //     (M % 256) compute only their 64-row multiples.
+//   * W may be stored K-tiled, [K/32][N][32] (GemmArgs::w_k32): then every
+//     1-KiB load of a W stage reads 1 KiB of contiguous memory instead of 16
+//     half cache lines, which lowers the power the loads draw and lets the
+//     clock run higher (the block weights are stored this way).
 //   * Workgroup b runs on XCD b % 8: each XCD gets a contiguous range of tiles
 //     (4 M tiles per N sweep, sharing its own L2), and the tail row of tiles last.
 #include "common.hpp"
@@ -48,6 +52,8 @@ struct Params {
     const float* resid; long ld_resid;
     const float* gate;
     uint32_t a_bytes, w_bytes;
+    int w_row_bytes;  // byte distance of consecutive W rows within a K step: ldw * 2, or 64 if K-tiled
+    int w_kstep;      // byte distance of consecutive K steps of one W row: 64, or N * 64 if K-tiled
     int split;        // K parts per tail tile (1 = no split)
     float* part;      // [n_tiles][split][64 * tail_sub][BN] FP32 partial sums of split tail tiles
 };
@@ -186,7 +192,7 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
         const int row = wave * 32 + q * 16 + (lane >> 2);
         const int c = (lane & 3) ^ fsw(row);
         a_src[q] = (uint32_t)(((long)(m0 + row) * p.lda + c * 8) * 2);
-        w_src[q] = (uint32_t)(((long)(n0 + row) * p.ldw + c * 8) * 2);
+        w_src[q] = (uint32_t)((long)(n0 + row) * p.w_row_bytes + c * 16);
     }
     // K steps of this item: all of them, or part `part` of `split` for a tail tile.
     const int nk_all = p.K / BK;
@@ -195,13 +201,13 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
     const int nk = (int)((long)nk_all * (part + 1) / parts) - kt0;
     auto issue = [&](int kt) {
         uint8_t* st = smem + (kt & (NS - 1)) * STAGE;
-        const int koff = (kt0 + kt) * ROWB;
+        const int koff = (kt0 + kt) * ROWB, koff_w = (kt0 + kt) * p.w_kstep;
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(st + (wave * 32 + q * 16) * ROWB), 16, a_src[q],
                                                      koff, 0, 0);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(st + A_BYTES + (wave * 32 + q * 16) * ROWB), 16,
-                                                     w_src[q], koff, 0, 0);
+                                                     w_src[q], koff_w, 0, 0);
         }
     };
 
@@ -380,12 +386,16 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     // Buffer offsets are 32-bit: every staged row of every tile (rounded up to 256)
     // must lie below 2^31 bytes; larger operands take the register-staged kernel.
     const double ab = ((a.M + 255) / 256 * 256.0) * a.lda * 2, wb = ((a.N + 255) / 256 * 256.0) * a.ldw * 2;
-    if (ab >= 2147483647.0 || wb >= 2147483647.0) return 1;
+    if (ab >= 2147483647.0 || wb >= 2147483647.0) return a.w_k32 ? -1 : 1;  // no other kernel reads K-tiled W
+    // K-tiled W: a stage's rows past N would alias the next K step, so N is whole tiles.
+    if (a.w_k32 && (a.N % pingpong::BN || a.ldw != a.K)) return -1;
     pingpong::Params p{};
     p.A = a.A; p.lda = a.lda; p.W = a.W; p.ldw = a.ldw; p.M = a.M; p.N = a.N; p.K = a.K;
     p.C = a.C; p.ldc = a.ldc; p.bias = a.bias; p.resid = a.resid; p.ld_resid = a.ld_resid; p.gate = a.gate;
     p.a_bytes = (uint32_t)((long)a.M * a.lda * 2);
     p.w_bytes = (uint32_t)((long)a.N * a.ldw * 2);
+    p.w_row_bytes = a.w_k32 ? pingpong::ROWB : (int)(a.ldw * 2);
+    p.w_kstep = a.w_k32 ? a.N * pingpong::ROWB : pingpong::ROWB;
     p.m_full = a.M / pingpong::BM;
     p.tail_sub = (a.M % pingpong::BM + 63) / 64;
     p.n_tiles = (a.N + pingpong::BN - 1) / pingpong::BN;

@@ -31,6 +31,9 @@ struct GemmArgs {
     const float* resid = nullptr;  // [M][ld_resid] f32 (EPI_GATE_RESID; may alias C)
     long ld_resid = 0;
     const float* gate = nullptr;   // [N]
+    // W stored K-tiled as [K/32][N][32] (16-bit operands, N a multiple of 256,
+    // ldw = K): the layout tile_k32 writes. Row-major [N][ldw] otherwise.
+    bool w_k32 = false;
     // Optional split-K scratch for the tail row of tiles (M % 256 rows): FP32 partial
     // sums, summed by a second launch on the same stream. Calls on one stream may
     // share it; calls that run concurrently must not.
@@ -92,6 +95,10 @@ int gemv(const void* W, int w_dtype, const float* b, const float* x, int N, int 
 int transpose_to_tokens(const float* latent, int ch, int hw, void* out, int dtype, hipStream_t s);
 // proj [hw][ch] (f32, bias applied) -> pred [ch][hw] f32.
 int tokens_to_latent(const float* proj, int hw, int ch, float* pred, hipStream_t s);
+
+// Row-major [rows][cols] 16-bit matrix -> K-tiled [cols/32][rows][32] (the
+// layout GemmArgs::w_k32 reads); in and out must not overlap.
+int tile_k32(const void* in, void* out, int rows, int cols, hipStream_t s);
 
 // Up or gate matrix [rows][cols] (dtype in_dt) -> its rows of the interleaved W_ug (parity 0 = up).
 int interleave_up_gate(const void* in, int in_dt, void* out, int dt, int rows, int cols, int parity, hipStream_t s);

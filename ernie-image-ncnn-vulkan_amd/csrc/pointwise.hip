@@ -365,6 +365,18 @@ __global__ void interleave_kernel(const void* __restrict__ in, int idt, void* __
     }
 }
 
+// Row-major [rows][cols] -> K-tiled [cols/32][rows][32], 16 bytes (8 values) per
+// thread: chunk q = (r, c8) of the source lands at ((c8/4)*rows + r)*32 + (c8%4)*8.
+__global__ void tile_k32_kernel(const uint4* __restrict__ in, uint4* __restrict__ out, int rows, int cols)
+{
+    const int c8n = cols / 8;
+    const size_t n = (size_t)rows * c8n;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const int r = (int)(i / c8n), c8 = (int)(i % c8n);
+        out[((size_t)(c8 / 4) * rows + r) * 4 + (c8 % 4)] = in[i];
+    }
+}
+
 inline int launch_status()
 {
     const hipError_t e = hipGetLastError();
@@ -574,6 +586,16 @@ int interleave_up_gate(const void* in, int idt, void* out, int dt, int rows, int
         return -1;
     const size_t n = (size_t)rows * cols;
     hipLaunchKernelGGL(interleave_kernel, dim3(grid_for(n)), dim3(256), 0, s, in, idt, out, dt, rows, cols, parity);
+    return launch_status();
+}
+
+int tile_k32(const void* in, void* out, int rows, int cols, hipStream_t s)
+{
+    if (!in || !out || rows < 1 || cols < 32 || cols % 32) return -1;
+    if ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) return -1;
+    const size_t n = (size_t)rows * (cols / 8);
+    hipLaunchKernelGGL(tile_k32_kernel, dim3(grid_for(n)), dim3(256), 0, s, static_cast<const uint4*>(in),
+                       static_cast<uint4*>(out), rows, cols);
     return launch_status();
 }
 
