@@ -287,20 +287,26 @@ BlockWeights* block_slot(ernie_hip_ctx* ctx, int index)
 }
 
 // ---- workspace -------------------------------------------------------------------------
+// The GEMM operands h, attn and p are K-tiled, [cols/32][rows][32] with rows = S
+// rounded up to 256, at 16-bit storage (rows past S are read by a tail tile but never
+// stored); row-major [S][cols] at FP32.
 struct BlockWs {
-    void* h;      // [S][dim] dtype
+    void* h;      // dim columns, dtype
     void* qkv;    // [S][3dim] dtype
-    void* attn;   // [S][dim] dtype
+    void* attn;   // dim columns, dtype
     float* x1;    // [S][dim] f32
-    void* p;      // [S][ffn] dtype
+    void* p;      // ffn columns, dtype
+    int rows;     // K-tiled row count (0: row-major)
 };
 
 int block_workspace(ernie_hip_ctx* ctx, int S, int dim, int ffn, int dtype, BlockWs& ws)
 {
     const size_t e = esize(dtype);
+    ws.rows = dtype == ERNIE_DTYPE_FP32 ? 0 : (S + 255) / 256 * 256;
+    const size_t R = ws.rows ? ws.rows : S;
     auto up = [](size_t b) { return (b + 255) / 256 * 256; };
-    const size_t h = up((size_t)S * dim * e), qkv = up(3 * (size_t)S * dim * e), x1 = up((size_t)S * dim * 4),
-                 p = up((size_t)S * ffn * e);
+    const size_t h = up(R * dim * e), qkv = up(3 * (size_t)S * dim * e), x1 = up((size_t)S * dim * 4),
+                 p = up(R * ffn * e);
     const int rc = dev_alloc(ctx, ctx->ws, h + qkv + h + x1 + p, "block workspace");
     if (rc) return rc;
     char* b = static_cast<char*>(ctx->ws.ptr);
@@ -352,7 +358,7 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
     {
         Timed t(ctx, P_NORM, 0, dS * D * (4 + e));
         rc = kernel_status(ctx, rmsnorm_modulate(x, ERNIE_DTYPE_FP32, static_cast<const float*>(w.norm1.ptr), shift_sa, scale_sa,
-                                                 S, D, 1e-6f, ws.h, dt, s), "rmsnorm_modulate");
+                                                 S, D, 1e-6f, ws.h, dt, s, ws.rows), "rmsnorm_modulate");
         if (rc) return rc;
     }
     // gemm_0/1/2 as one [3D][D] projection
@@ -360,6 +366,7 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
         GemmArgs g;
         g.A = ws.h; g.lda = D; g.W = w.wqkv.ptr; g.ldw = D; g.M = S; g.N = 3 * D; g.K = D; g.dtype = dt;
         g.w_k32 = w.k32[0];
+        g.a_k32_rows = ws.rows;
         g.epilogue = EPI_STORE; g.C = ws.qkv; g.ldc = 3 * D; g.c_dtype = dt;
         rc = split_workspace(ctx, S, H, &g.split_ws, &g.split_ws_bytes);
         if (rc) return rc;
@@ -382,7 +389,11 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
         a.q = ws.qkv; a.k = static_cast<char*>(ws.qkv) + (size_t)D * eb; a.v = static_cast<char*>(ws.qkv) + 2 * (size_t)D * eb;
         a.o = ws.attn; a.dtype = dt; a.heads = H; a.kv_heads = H; a.sq = S; a.sk = S; a.d = kHeadDim;
         a.q_hs = a.k_hs = a.v_hs = kHeadDim; a.q_rs = a.k_rs = a.v_rs = 3L * D;
-        a.o_hs = kHeadDim; a.o_rs = D;
+        if (ws.rows) {
+            a.o_rs = 32; a.o_ds = 32L * ws.rows; a.o_hs = 4 * a.o_ds;  // K-tiled for the out projection
+        } else {
+            a.o_hs = kHeadDim; a.o_rs = D;
+        }
         a.mask = mask; a.mask_heads = 1; a.mask_rows = 1; a.valid_keys = valid_keys;
         rc = split_workspace(ctx, S, H, &a.split_ws, &a.split_ws_bytes);
         if (rc) return rc;
@@ -395,6 +406,7 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
         GemmArgs g;
         g.A = ws.attn; g.lda = D; g.W = w.wo.ptr; g.ldw = D; g.M = S; g.N = D; g.K = D; g.dtype = dt;
         g.w_k32 = w.k32[1];
+        g.a_k32_rows = ws.rows;
         g.epilogue = EPI_GATE_RESID; g.C = ws.x1; g.ldc = D; g.c_dtype = ERNIE_DTYPE_FP32; g.resid = x; g.ld_resid = D;
         g.gate = gate_sa;
         rc = split_workspace(ctx, S, H, &g.split_ws, &g.split_ws_bytes);
@@ -407,7 +419,7 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
     {
         Timed t(ctx, P_NORM, 0, dS * D * (4 + e));
         rc = kernel_status(ctx, rmsnorm_modulate(ws.x1, ERNIE_DTYPE_FP32, static_cast<const float*>(w.norm2.ptr), shift_mlp,
-                                                 scale_mlp, S, D, 1e-6f, ws.h, dt, s), "rmsnorm_modulate 2");
+                                                 scale_mlp, S, D, 1e-6f, ws.h, dt, s, ws.rows), "rmsnorm_modulate 2");
         if (rc) return rc;
     }
     // gemm_4 (up) + gemm_5 (gate) + ErnieGELU + mul_20 in one GEMM epilogue
@@ -415,6 +427,8 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
         GemmArgs g;
         g.A = ws.h; g.lda = D; g.W = w.w_ug.ptr; g.ldw = D; g.M = S; g.N = 2 * F; g.K = D; g.dtype = dt;
         g.w_k32 = w.k32[2];
+        g.a_k32_rows = ws.rows;
+        g.c_k32_rows = ws.rows;
         g.epilogue = EPI_GEGLU; g.C = ws.p; g.ldc = F; g.c_dtype = dt;
         rc = split_workspace(ctx, S, H, &g.split_ws, &g.split_ws_bytes);
         if (rc) return rc;
@@ -427,6 +441,7 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
         GemmArgs g;
         g.A = ws.p; g.lda = F; g.W = w.w_down.ptr; g.ldw = F; g.M = S; g.N = D; g.K = F; g.dtype = dt;
         g.w_k32 = w.k32[3];
+        g.a_k32_rows = ws.rows;
         g.epilogue = EPI_GATE_RESID; g.C = out; g.ldc = D; g.c_dtype = ERNIE_DTYPE_FP32; g.resid = ws.x1; g.ld_resid = D;
         g.gate = gate_mlp;
         rc = split_workspace(ctx, S, H, &g.split_ws, &g.split_ws_bytes);

@@ -358,7 +358,8 @@ int gemm(const GemmArgs& a, hipStream_t s)
     if (a.epilogue == EPI_GEGLU && (a.N % 64 || a.ldc < a.N / 2)) return -1;
     if (a.epilogue != EPI_GEGLU && a.ldc < a.N) return -1;
     if (a.epilogue > EPI_GEGLU || a.epilogue < 0) return -1;
-    if (a.w_k32 && a.dtype == DT_F32) return -1;  // only the 16-bit kernel reads K-tiled W
+    // Only the 16-bit kernel reads or writes K-tiled operands.
+    if ((a.w_k32 || a.a_k32_rows || a.c_k32_rows) && a.dtype == DT_F32) return -1;
     GemmParams p{};
     p.A = a.A; p.lda = a.lda; p.W = a.W; p.ldw = a.ldw;
     p.M = a.M; p.N = a.N; p.K = a.K;

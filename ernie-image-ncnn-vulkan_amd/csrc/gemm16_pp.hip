@@ -21,10 +21,11 @@
 //     the clock it holds gave 5-7% more throughput on every projection shape.
 //     Rows past M and columns past N read as zero through the buffer range checks;
 //     tail tiles (M % 256) compute only their 64-row multiples.
-//   * W may be stored K-tiled, [K/32][N][32] (GemmArgs::w_k32): then every
-//     1-KiB load of a W stage reads 1 KiB of contiguous memory instead of 16
-//     half cache lines, which lowers the power the loads draw and lets the
-//     clock run higher (the block weights are stored this way).
+//   * W and A may be stored K-tiled, [K/32][rows][32] (GemmArgs::w_k32,
+//     a_k32_rows): then every 1-KiB load of a stage reads 1 KiB of contiguous
+//     memory instead of 16 half cache lines, which lowers the power the loads draw
+//     and lets the clock run higher. The block weights and the activations the
+//     block's GEMMs read (RMSNorm, attention and GEGLU outputs) are stored this way.
 //   * Workgroup b runs on XCD b % 8: each XCD gets a contiguous range of tiles
 //     (4 M tiles per N sweep, sharing its own L2), and the tail row of tiles last.
 #include "common.hpp"
@@ -57,6 +58,9 @@ struct Params {
     uint32_t a_bytes, w_bytes;
     int w_row_bytes;  // byte distance of consecutive W rows within a K step: ldw * 2, or 64 if K-tiled
     int w_kstep;      // byte distance of consecutive K steps of one W row: 64, or N * 64 if K-tiled
+    int a_row_bytes;  // the same for A: lda * 2 or 64
+    int a_kstep;      // 64, or a_k32_rows * 64
+    long c_rs, c_ss;  // EPI_GEGLU output: element distance of rows and of 32-column groups
     int split;        // K parts per tail tile (1 = no split)
     float* part;      // [n_tiles][split][64 * tail_sub][BN] FP32 partial sums of split tail tiles
 };
@@ -84,7 +88,7 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(Params p)
         if (EPI == EPI_GEGLU) g += base[(size_t)q * rows * BN + 32];
     }
     if (EPI == EPI_GEGLU) {
-        static_cast<OutT*>(p.C)[(size_t)m * p.ldc + c] = OutT(v * gelu_erf(g));
+        static_cast<OutT*>(p.C)[(size_t)m * p.c_rs + (size_t)(c >> 5) * p.c_ss + (c & 31)] = OutT(v * gelu_erf(g));
     } else if (EPI == EPI_STORE) {
         if (p.bias) v += p.bias[n];
         static_cast<OutT*>(p.C)[(size_t)m * p.ldc + n] = OutT(v);
@@ -196,7 +200,7 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
     for (int q = 0; q < 2; ++q) {
         const int row = wave * 32 + q * 16 + (lane >> 2);
         const int c = (lane & 3) ^ fsw(row);
-        a_src[q] = (uint32_t)(((long)(m0 + row) * p.lda + c * 8) * 2);
+        a_src[q] = (uint32_t)((long)(m0 + row) * p.a_row_bytes + c * 16);
         w_src[q] = (uint32_t)((long)(n0 + row) * p.w_row_bytes + c * 16);
     }
     // K steps of this item: all of them, or part `part` of `split` for a tail tile.
@@ -206,7 +210,7 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
     const int nk = (int)((long)nk_all * (part + 1) / parts) - kt0;
     auto issue = [&](int kt) {
         uint8_t* st = smem + (kt & (NS - 1)) * STAGE;
-        const int koff = (kt0 + kt) * ROWB, koff_w = (kt0 + kt) * p.w_kstep;
+        const int koff = (kt0 + kt) * p.a_kstep, koff_w = (kt0 + kt) * p.w_kstep;
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(st + (wave * 32 + q * 16) * ROWB), 16, a_src[q],
@@ -349,12 +353,13 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
             const int m = row_w + 16 * i + r;
             if (m >= p.M) continue;
             if (EPI == EPI_GEGLU) {
-                // This wave's 64 W rows are 32 up rows then the 32 matching gate rows.
+                // This wave's 64 W rows are 32 up rows then the 32 matching gate rows:
+                // output columns 32 g .. 32 g + 31, g = (n0 + 64 wn) / 64.
+                const size_t cg = (size_t)((n0 + wn * 64) >> 6) * p.c_ss;
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    const int nout = (n0 + wn * 64) / 2 + 16 * j + r16;
-                    if (2 * nout < p.N)
-                        static_cast<OutT*>(p.C)[(size_t)m * p.ldc + nout] =
+                    if (n0 + wn * 64 < p.N)
+                        static_cast<OutT*>(p.C)[(size_t)m * p.c_rs + cg + 16 * j + r16] =
                             OutT(acc[i][j][r] * gelu_erf(acc[i][j + 2][r]));
                 }
             } else {
@@ -392,19 +397,30 @@ __global__ void __launch_bounds__(512, 1) kernel(Params p)
 
 int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
 {
-    if (a.dtype == DT_F32 || a.K % pingpong::BK) return 1;
+    // No other kernel takes K-tiled operands: shapes this one rejects are errors then.
+    const int other = a.w_k32 || a.a_k32_rows || a.c_k32_rows ? -1 : 1;
+    if (a.dtype == DT_F32 || a.K % pingpong::BK) return other;
     if (a.epilogue == EPI_STORE && a.c_dtype != DT_F32 && a.c_dtype != a.dtype) return -1;
     if (a.epilogue == EPI_GEGLU && a.c_dtype != a.dtype) return -1;
     // Buffer offsets are 32-bit: every staged row of every tile (rounded up to 256)
     // must lie below 2^31 bytes; larger operands take the register-staged kernel.
     const double ab = ((a.M + 255) / 256 * 256.0) * a.lda * 2, wb = ((a.N + 255) / 256 * 256.0) * a.ldw * 2;
-    if (ab >= 2147483647.0 || wb >= 2147483647.0) return a.w_k32 ? -1 : 1;  // no other kernel reads K-tiled W
+    if (ab >= 2147483647.0 || wb >= 2147483647.0) return other;
     // K-tiled W: a stage's rows past N would alias the next K step, so N is whole tiles.
     if (a.w_k32 && (a.N % pingpong::BN || a.ldw != a.K)) return -1;
+    // K-tiled A: every tile row, the tail's included, inside each 32-column slab.
+    if (a.a_k32_rows && (a.a_k32_rows < (a.M + pingpong::BM - 1) / pingpong::BM * pingpong::BM || a.lda != a.K ||
+                         (double)a.a_k32_rows * a.K * 2 >= 2147483647.0))
+        return -1;
+    if (a.c_k32_rows && (a.epilogue != EPI_GEGLU || a.c_k32_rows < a.M)) return -1;
     pingpong::Params p{};
     p.A = a.A; p.lda = a.lda; p.W = a.W; p.ldw = a.ldw; p.M = a.M; p.N = a.N; p.K = a.K;
     p.C = a.C; p.ldc = a.ldc; p.bias = a.bias; p.resid = a.resid; p.ld_resid = a.ld_resid; p.gate = a.gate;
-    p.a_bytes = (uint32_t)((long)a.M * a.lda * 2);
+    p.a_bytes = (uint32_t)(a.a_k32_rows ? (long)a.a_k32_rows * a.K * 2 : (long)a.M * a.lda * 2);
+    p.a_row_bytes = a.a_k32_rows ? pingpong::ROWB : (int)(a.lda * 2);
+    p.a_kstep = a.a_k32_rows ? a.a_k32_rows * pingpong::ROWB : pingpong::ROWB;
+    p.c_rs = a.c_k32_rows ? 32 : a.ldc;
+    p.c_ss = a.c_k32_rows ? 32L * a.c_k32_rows : 32;
     p.w_bytes = (uint32_t)((long)a.N * a.ldw * 2);
     p.w_row_bytes = a.w_k32 ? pingpong::ROWB : (int)(a.ldw * 2);
     p.w_kstep = a.w_k32 ? a.N * pingpong::ROWB : pingpong::ROWB;

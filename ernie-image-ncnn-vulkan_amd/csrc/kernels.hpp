@@ -34,6 +34,13 @@ struct GemmArgs {
     // W stored K-tiled as [K/32][N][32] (16-bit operands, N a multiple of 256,
     // ldw = K): the layout tile_k32 writes. Row-major [N][ldw] otherwise.
     bool w_k32 = false;
+    // A stored K-tiled as [K/32][a_k32_rows][32] (16-bit operands, lda = K), with
+    // a_k32_rows >= M rounded up to 256 so a tail tile's rows stay inside each
+    // 32-column slab (rows past M are read but never stored). 0 = row-major [M][lda].
+    int a_k32_rows = 0;
+    // EPI_GEGLU only: C stored K-tiled as [(N/2)/32][c_k32_rows][32], c_k32_rows >= M,
+    // i.e. in the layout a following GEMM reads through a_k32_rows. 0 = row-major.
+    int c_k32_rows = 0;
     // Optional split-K scratch for the tail row of tiles (M % 256 rows): FP32 partial
     // sums, summed by a second launch on the same stream. Calls on one stream may
     // share it; calls that run concurrently must not.
@@ -51,6 +58,10 @@ struct SdpaArgs {
     int dtype = 0;
     int heads = 0, kv_heads = 0, sq = 0, sk = 0, d = 0;
     long q_hs = 0, q_rs = 0, k_hs = 0, k_rs = 0, v_hs = 0, v_rs = 0, o_hs = 0, o_rs = 0;  // strides (elements)
+    // Element distance between consecutive 32-value groups of one output row of a
+    // head (0 = 32: contiguous). With o_rs = 32, o_ds = rows * 32 and o_hs = 4 * o_ds
+    // the output is K-tiled for the next GEMM (head_dim 128, 16-bit kernel only).
+    long o_ds = 0;
     const float* mask = nullptr;  // additive [mask_heads][mask_rows][sk]; mask_rows 1 or sq
     int mask_heads = 1, mask_rows = 1;
     int valid_keys = 0;           // keys >= valid_keys are excluded (0 = sk)
@@ -68,8 +79,10 @@ int sdpa16_d128(const SdpaArgs& a, hipStream_t stream);
 
 // ---- bandwidth-bound kernels ------------------------------------------------------
 // out = RMSNorm(x) * gamma [* (1 + scale) + shift]; FP32 statistics.
+// out_k32_rows > 0 (16-bit out, width a multiple of 32): out is K-tiled as
+// [width/32][out_k32_rows][32] for a GEMM that reads A through a_k32_rows.
 int rmsnorm_modulate(const void* x, int x_dtype, const float* gamma, const float* shift, const float* scale,
-                     int rows, int width, float eps, void* out, int out_dtype, hipStream_t s);
+                     int rows, int width, float eps, void* out, int out_dtype, hipStream_t s, int out_k32_rows = 0);
 // out = LayerNorm(x) (non-affine) * (1 + scale) + shift.
 int layernorm_modulate(const float* x, const float* shift, const float* scale, int rows, int width, float eps,
                        void* out, int out_dtype, hipStream_t s);

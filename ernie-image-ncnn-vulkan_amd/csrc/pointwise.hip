@@ -56,11 +56,19 @@ constexpr int kMaxPer = 4;  // float4 groups per thread -> width up to 4096
 // per workgroup instead of once per row); no workgroup barrier inside the row
 // loop, the statistics are a single wave reduction.
 constexpr int kRowWaves = 4, kRowMaxWidth = 4096;
+// Element (r, c) of a [rows][width] output: row-major, or K-tiled as
+// [width/32][out_rows][32] when out_rows > 0 (four-value groups never straddle a
+// 32-column slab).
+__device__ __forceinline__ size_t out_index(int r, int c, int width, int out_rows)
+{
+    return out_rows ? ((size_t)(c >> 5) * out_rows + r) * 32 + (c & 31) : (size_t)r * width + c;
+}
 template <typename TIn, typename TOut>
 __global__ void __launch_bounds__(256) rmsnorm_rows_kernel(const TIn* __restrict__ x, const float* __restrict__ gamma,
                                                            const float* __restrict__ shift,
                                                            const float* __restrict__ scale, int rows, int width,
-                                                           int rows_per_block, float eps, TOut* __restrict__ out)
+                                                           int rows_per_block, float eps, TOut* __restrict__ out,
+                                                           int out_rows)
 {
     __shared__ f32x4 mul4[kRowMaxWidth / 4], add4[kRowMaxWidth / 4];
     const int w4 = width >> 2;
@@ -92,7 +100,6 @@ __global__ void __launch_bounds__(256) rmsnorm_rows_kernel(const TIn* __restrict
             }
         }
         const float inv = 1.0f / sqrtf(wave_sum(ss) / float(width) + eps);
-        TOut* orow = out + (size_t)r * width;
 #pragma unroll
         for (int i = 0; i < kRowMaxWidth / 256; ++i) {
             const int c4 = lane + 64 * i;
@@ -101,7 +108,7 @@ __global__ void __launch_bounds__(256) rmsnorm_rows_kernel(const TIn* __restrict
                 f32x4 y;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) y[e] = (v[i][e] * inv) * m[e] + a[e];
-                Vec4<TOut>::store(orow + 4 * c4, y);
+                Vec4<TOut>::store(out + out_index(r, 4 * c4, width, out_rows), y);
             }
         }
     }
@@ -118,7 +125,7 @@ __global__ void __launch_bounds__(256) rmsnorm_persist_kernel(const TIn* __restr
                                                               const float* __restrict__ gamma,
                                                               const float* __restrict__ shift,
                                                               const float* __restrict__ scale, int rows, float eps,
-                                                              TOut* __restrict__ out)
+                                                              TOut* __restrict__ out, int out_rows)
 {
     constexpr int width = PER * 1024;
     __shared__ float red[2][4];
@@ -155,16 +162,84 @@ __global__ void __launch_bounds__(256) rmsnorm_persist_kernel(const TIn* __restr
         __syncthreads();
         const float tot = (red[it & 1][0] + red[it & 1][1]) + (red[it & 1][2] + red[it & 1][3]);
         const float inv = 1.0f / sqrtf(tot / float(width) + eps);
-        TOut* orow = out + (size_t)r * width;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             f32x4 y;
 #pragma unroll
             for (int e = 0; e < 4; ++e) y[e] = (v[i][e] * inv) * m[i][e] + a[i][e];
-            Vec4<TOut>::store(orow + 4 * (tid + 256 * i), y);
+            Vec4<TOut>::store(out + out_index(r, 4 * (tid + 256 * i), width, out_rows), y);
         }
 #pragma unroll
         for (int i = 0; i < PER; ++i) v[i] = vn[i];
+    }
+}
+
+// The same operation writing K-tiled output ([width/32][out_rows][32]) for widths
+// of NI x 512: persistent workgroups take rows in pairs (r0 even, r0 + 1), so each
+// store instruction covers, per 32-column slab, both rows' 64 bytes, which are
+// adjacent in the tiled layout: four whole 128-byte lines per instruction. Lane l of
+// wave w holds row r0 + (l / 8 % 2) and columns 32 s + 4 (l % 8) .. + 3 of slabs
+// s = 4 (w + 4 i) + l / 16, i < NI.
+template <typename TIn, typename TOut, int NI>
+__global__ void __launch_bounds__(256) rmsnorm_pair_k32_kernel(const TIn* __restrict__ x,
+                                                               const float* __restrict__ gamma,
+                                                               const float* __restrict__ shift,
+                                                               const float* __restrict__ scale, int rows, float eps,
+                                                               TOut* __restrict__ out, int out_rows)
+{
+    constexpr int width = NI * 512;
+    __shared__ float red[2][4][2];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, b = (lane >> 3) & 1;
+    int col[NI];
+    f32x4 m[NI], a[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        col[i] = 32 * (4 * (wave + 4 * i) + (lane >> 4)) + 4 * (lane & 7);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float g = gamma ? gamma[col[i] + e] : 1.0f;
+            m[i][e] = scale ? g * (scale[col[i] + e] + 1.0f) : g;
+            a[i][e] = shift ? shift[col[i] + e] : 0.0f;
+        }
+    }
+    const int pairs = (rows + 1) >> 1;
+    int pr = blockIdx.x;
+    f32x4 v[NI];
+    auto load = [&](int pair, f32x4 (&dst)[NI]) {
+        const int r = 2 * pair + b;
+#pragma unroll
+        for (int i = 0; i < NI; ++i)
+            dst[i] = r < rows ? Vec4<TIn>::load(x + (size_t)r * width + col[i]) : f32x4{0.f, 0.f, 0.f, 0.f};
+    };
+    if (pr < pairs) load(pr, v);
+    for (int it = 0; pr < pairs; pr += gridDim.x, ++it) {
+        f32x4 vn[NI];
+        if (pr + (int)gridDim.x < pairs) load(pr + gridDim.x, vn);
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) ss += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
+        // Sum over the 32 lanes of this wave that hold the same row (lane bit 3 fixed).
+        ss += __shfl_xor(ss, 1, 64);
+        ss += __shfl_xor(ss, 2, 64);
+        ss += __shfl_xor(ss, 4, 64);
+        ss += __shfl_xor(ss, 16, 64);
+        ss += __shfl_xor(ss, 32, 64);
+        if ((lane & ~8) == 0) red[it & 1][wave][b] = ss;
+        __syncthreads();
+        const float tot = (red[it & 1][0][b] + red[it & 1][1][b]) + (red[it & 1][2][b] + red[it & 1][3][b]);
+        const float inv = 1.0f / sqrtf(tot / float(width) + eps);
+        const int r = 2 * pr + b;
+        if (r < rows) {
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                f32x4 y;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) y[e] = (v[i][e] * inv) * m[i][e] + a[i][e];
+                Vec4<TOut>::store(out + ((size_t)(col[i] >> 5) * out_rows + r) * 32 + (col[i] & 31), y);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NI; ++i) v[i] = vn[i];
     }
 }
 
@@ -393,8 +468,33 @@ bool valid_dt(int dt) { return dt == DT_F32 || dt == DT_F16 || dt == DT_BF16; }
 
 template <typename TIn>
 int rms_dispatch_out(const TIn* x, const float* gamma, const float* shift, const float* scale, int rows, int width,
-                     float eps, void* out, int odt, hipStream_t s)
+                     float eps, void* out, int odt, hipStream_t s, int out_rows)
 {
+    if (out_rows && width % 512 == 0 && width <= 4096 && odt != DT_F32) {
+        // Four persistent workgroups per CU of an MI355X, never more than the row pairs.
+        const dim3 grid((unsigned)std::min((rows + 1) / 2, 1024)), block(256);
+#define EHIP_RMS_PAIR(NI)                                                                                        \
+        do {                                                                                                     \
+            if (odt == DT_F16)                                                                                   \
+                hipLaunchKernelGGL((rmsnorm_pair_k32_kernel<TIn, f16, NI>), grid, block, 0, s, x, gamma, shift,   \
+                                   scale, rows, eps, static_cast<f16*>(out), out_rows);                          \
+            else                                                                                                 \
+                hipLaunchKernelGGL((rmsnorm_pair_k32_kernel<TIn, bf16, NI>), grid, block, 0, s, x, gamma, shift,  \
+                                   scale, rows, eps, static_cast<bf16*>(out), out_rows);                         \
+        } while (0)
+        switch (width / 512) {
+        case 1: EHIP_RMS_PAIR(1); break;
+        case 2: EHIP_RMS_PAIR(2); break;
+        case 3: EHIP_RMS_PAIR(3); break;
+        case 4: EHIP_RMS_PAIR(4); break;
+        case 5: EHIP_RMS_PAIR(5); break;
+        case 6: EHIP_RMS_PAIR(6); break;
+        case 7: EHIP_RMS_PAIR(7); break;
+        default: EHIP_RMS_PAIR(8); break;
+        }
+#undef EHIP_RMS_PAIR
+        return launch_status();
+    }
     if (width % 1024 == 0) {
         // Four persistent workgroups per CU of an MI355X (256 CUs), never more than the rows.
         const dim3 grid((unsigned)std::min(rows, 1024)), block(256);
@@ -402,13 +502,13 @@ int rms_dispatch_out(const TIn* x, const float* gamma, const float* shift, const
         do {                                                                                                     \
             if (odt == DT_F32)                                                                                   \
                 hipLaunchKernelGGL((rmsnorm_persist_kernel<TIn, float, PER>), grid, block, 0, s, x, gamma, shift, \
-                                   scale, rows, eps, static_cast<float*>(out));                                  \
+                                   scale, rows, eps, static_cast<float*>(out), out_rows);                                  \
             else if (odt == DT_F16)                                                                              \
                 hipLaunchKernelGGL((rmsnorm_persist_kernel<TIn, f16, PER>), grid, block, 0, s, x, gamma, shift,   \
-                                   scale, rows, eps, static_cast<f16*>(out));                                    \
+                                   scale, rows, eps, static_cast<f16*>(out), out_rows);                                    \
             else                                                                                                 \
                 hipLaunchKernelGGL((rmsnorm_persist_kernel<TIn, bf16, PER>), grid, block, 0, s, x, gamma, shift,  \
-                                   scale, rows, eps, static_cast<bf16*>(out));                                   \
+                                   scale, rows, eps, static_cast<bf16*>(out), out_rows);                                   \
         } while (0)
         switch (width / 1024) {
         case 1: EHIP_RMS_PERSIST(1); break;
@@ -425,26 +525,29 @@ int rms_dispatch_out(const TIn* x, const float* gamma, const float* shift, const
     const dim3 grid((rows + rpb - 1) / rpb), block(64 * kRowWaves);
     if (odt == DT_F32)
         hipLaunchKernelGGL((rmsnorm_rows_kernel<TIn, float>), grid, block, 0, s, x, gamma, shift, scale, rows, width,
-                           rpb, eps, static_cast<float*>(out));
+                           rpb, eps, static_cast<float*>(out), out_rows);
     else if (odt == DT_F16)
         hipLaunchKernelGGL((rmsnorm_rows_kernel<TIn, f16>), grid, block, 0, s, x, gamma, shift, scale, rows, width,
-                           rpb, eps, static_cast<f16*>(out));
+                           rpb, eps, static_cast<f16*>(out), out_rows);
     else
         hipLaunchKernelGGL((rmsnorm_rows_kernel<TIn, bf16>), grid, block, 0, s, x, gamma, shift, scale, rows, width,
-                           rpb, eps, static_cast<bf16*>(out));
+                           rpb, eps, static_cast<bf16*>(out), out_rows);
     return launch_status();
 }
 
 }  // namespace
 
 int rmsnorm_modulate(const void* x, int xdt, const float* gamma, const float* shift, const float* scale, int rows,
-                     int width, float eps, void* out, int odt, hipStream_t s)
+                     int width, float eps, void* out, int odt, hipStream_t s, int out_rows)
 {
     if (!x || !out || rows < 1 || width < 4 || width % 4 || width > kRowMaxWidth) return -1;
     if (!valid_dt(xdt) || !valid_dt(odt) || (!shift) != (!scale)) return -1;
-    if (xdt == DT_F32) return rms_dispatch_out(static_cast<const float*>(x), gamma, shift, scale, rows, width, eps, out, odt, s);
-    if (xdt == DT_F16) return rms_dispatch_out(static_cast<const f16*>(x), gamma, shift, scale, rows, width, eps, out, odt, s);
-    return rms_dispatch_out(static_cast<const bf16*>(x), gamma, shift, scale, rows, width, eps, out, odt, s);
+    if (out_rows && (out_rows < rows || width % 32 || odt == DT_F32)) return -1;
+    if (xdt == DT_F32)
+        return rms_dispatch_out(static_cast<const float*>(x), gamma, shift, scale, rows, width, eps, out, odt, s, out_rows);
+    if (xdt == DT_F16)
+        return rms_dispatch_out(static_cast<const f16*>(x), gamma, shift, scale, rows, width, eps, out, odt, s, out_rows);
+    return rms_dispatch_out(static_cast<const bf16*>(x), gamma, shift, scale, rows, width, eps, out, odt, s, out_rows);
 }
 
 int layernorm_modulate(const float* x, const float* shift, const float* scale, int rows, int width, float eps,

@@ -454,6 +454,7 @@ int sdpa(const SdpaArgs& a, hipStream_t s)
     if (a.mask && a.mask_heads != 1 && a.mask_heads != a.heads) return -1;
     const int kv_end = a.valid_keys > 0 ? a.valid_keys : a.sk;
     if (kv_end > a.sk) return -1;
+    if (a.o_ds != 0 && a.o_ds != 32 && (a.dtype == DT_F32 || a.d != 128 || a.o_ds % 8)) return -1;
     SdpaParams p{};
     p.q = a.q; p.k = a.k; p.v = a.v; p.o = a.o;
     p.heads = a.heads; p.group = a.heads / a.kv_heads; p.sq = a.sq; p.sk = a.sk; p.d = a.d; p.kv_end = kv_end;
@@ -475,6 +476,8 @@ int sdpa(const SdpaArgs& a, hipStream_t s)
         hipLaunchKernelGGL(sdpa32_kernel, dim3((a.sq + BQ - 1) / BQ, a.heads), block, 0, s, p);
     } else if (const int rc = sdpa16_d128(a, s); rc != 1) {
         return rc;
+    } else if (a.o_ds != 0 && a.o_ds != 32) {
+        return -1;  // only the head_dim-128 kernel writes grouped (K-tiled) output rows
     } else {
         const bool fast = p.vec_ok && a.d == 128;
         const int mm = !a.mask ? MASK_NONE : (a.mask_rows > 1 ? MASK_PER_QUERY : MASK_ROW);

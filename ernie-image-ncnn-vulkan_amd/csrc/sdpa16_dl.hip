@@ -57,6 +57,7 @@ struct Params {
     const void* q; const void* k; const void* v; void* o;
     int heads, group, sq, sk, kv_end;
     long q_hs, q_rs, k_hs, k_rs, v_hs, v_rs, o_hs, o_rs;
+    long o_ds;  // element distance between the four 32-value groups of an output row
     const float* mask; long mask_hs;  // additive FP32 mask: one row [sk] or per query [sq][sk] per head
     float scale_log2;
     // Split of the last, partial query tile (sq % 128 queries) along the keys:
@@ -90,7 +91,7 @@ __global__ void __launch_bounds__(256) combine_kernel(Params p, int tail_q)
         O += po[(size_t)q * BQ * D] * w;
     }
     const int qi = p.full_qt * BQ + ql;
-    static_cast<T*>(p.o)[(size_t)h * p.o_hs + (size_t)qi * p.o_rs + d] = T(O / L);
+    static_cast<T*>(p.o)[(size_t)h * p.o_hs + (size_t)qi * p.o_rs + (size_t)(d >> 5) * p.o_ds + (d & 31)] = T(O / L);
 }
 
 template <typename T> struct Mfma;
@@ -479,11 +480,11 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
         for (int rq = 0; rq < 4; ++rq) {
-            const int d0 = 32 * dt + 8 * rq + 4 * g;
+            // Values 32 dt + 8 rq + 4 g .. + 3: offset 8 rq + 4 g in the dt-th group of 32.
             union { u32x2 u; T e[4]; } pk;
 #pragma unroll
             for (int e = 0; e < 4; ++e) pk.e[e] = T(oacc[dt][4 * rq + e] * inv);
-            *reinterpret_cast<u32x2*>(orow + d0) = pk.u;
+            *reinterpret_cast<u32x2*>(orow + (size_t)dt * p.o_ds + 8 * rq + 4 * g) = pk.u;
         }
 }
 
@@ -499,8 +500,8 @@ int sdpa16_d128(const SdpaArgs& a, hipStream_t s)
     const uintptr_t bases = reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.k) |
                             reinterpret_cast<uintptr_t>(a.v) | reinterpret_cast<uintptr_t>(a.o);
     if (bases % 16 || a.q_hs % vec || a.q_rs % vec || a.k_hs % vec || a.k_rs % vec || a.v_hs % vec || a.v_rs % vec ||
-        a.o_hs % vec || a.o_rs % vec)
-        return 1;
+        a.o_hs % vec || a.o_rs % vec || a.o_ds % vec)
+        return a.o_ds != 0 && a.o_ds != 32 ? -1 : 1;
     const int kv_end = a.valid_keys > 0 ? a.valid_keys : a.sk;
     const int ntiles = (kv_end + sdl::BKV - 1) / sdl::BKV;
     if ((double)ntiles * sdl::BKV * (double)std::max(a.k_rs, a.v_rs) * 2 >= 2147483647.0) return 1;
@@ -509,6 +510,7 @@ int sdpa16_d128(const SdpaArgs& a, hipStream_t s)
     p.heads = a.heads; p.group = a.heads / a.kv_heads; p.sq = a.sq; p.sk = a.sk; p.kv_end = kv_end;
     p.q_hs = a.q_hs; p.q_rs = a.q_rs; p.k_hs = a.k_hs; p.k_rs = a.k_rs;
     p.v_hs = a.v_hs; p.v_rs = a.v_rs; p.o_hs = a.o_hs; p.o_rs = a.o_rs;
+    p.o_ds = a.o_ds ? a.o_ds : 32;
     p.mask = a.mask;
     const bool dense = a.mask && a.mask_rows > 1;
     p.mask_hs = a.mask && a.mask_heads > 1 ? (long)a.sk * (dense ? a.sq : 1) : 0;
