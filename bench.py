@@ -28,8 +28,8 @@ HBM_PEAK = 8.0e12
 # launch, from two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) scaled by the same
 # counters' reading for a plain 512 MiB FP32 copy (x2.000 fetch, x1.000 write); the
 # runs and the per-dispatch table are in profiles/denoise_1024_fp16_hbm_traffic.md.
-MEASURED_TRAFFIC = {"fp16": {"gemm_up_gate": 1.527e9 + 1.42e7, "gemm_qkv": 8.293e8 + 1.733e7,
-                             "sdpa": 2.313e8 + 1.944e7}}
+MEASURED_TRAFFIC = {"fp16": {"gemm_up_gate": 1.540e9 + 1.42e7, "gemm_qkv": 8.390e8 + 1.734e7,
+                             "sdpa": 2.335e8 + 1.945e7}}
 DIM, FFN, LATENT_CH, TEXT_DIM = 4096, 12288, 128, 3072
 
 
