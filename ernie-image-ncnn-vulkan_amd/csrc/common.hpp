@@ -75,4 +75,14 @@ __device__ __forceinline__ float gelu_erf(float x)
     return x * (x >= 0.f ? __builtin_fmaf(-0.5f, tail, 1.0f) : 0.5f * tail);
 }
 
+// x * sigmoid(x) = x / (1 + exp(-x)) (ncnn Swish, the text MLP's silu_7), with bare
+// v_exp_f32 / v_rcp_f32: exp(-x) overflows to +inf for x < -88, giving -0.
+__device__ __forceinline__ float silu(float x)
+{
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.4426950408889634f * x));
+}
+
+// Activation on the gate half of a gated-MLP epilogue: SiLU or erf GELU.
+template <bool kSilu> __device__ __forceinline__ float glu_act(float g) { return kSilu ? silu(g) : gelu_erf(g); }
+
 }  // namespace ehip

@@ -39,6 +39,18 @@ struct BlockWeights {
     bool k32[4] = {false, false, false, false};
 };
 
+// One Mistral text decoder block (tests/fixtures/text-s64.ncnn.param), head_dim 128.
+struct TextBlockWeights {
+    bool loaded = false;
+    int hidden = 0, heads = 0, kv_heads = 0, ffn = 0, dtype = 0;
+    DeviceBuffer norm1, norm2;  // FP32 [hidden]
+    DeviceBuffer wqkv;          // [(heads + 2 kv_heads) * 128][hidden]: q, k, v rows (gemm_0/1/2)
+    DeviceBuffer wo;            // [hidden][heads * 128]
+    DeviceBuffer w_ug;          // [2 ffn][hidden]: up / gate rows interleaved in 32-row groups
+    DeviceBuffer w_down;        // [hidden][ffn]
+    bool k32[4] = {false, false, false, false};  // K-tiled wqkv, wo, w_ug, w_down (16-bit)
+};
+
 struct HeadWeights {
     bool loaded = false;
     int dim = 0, latent_ch = 0, text_dim = 0, dtype = 0;
@@ -60,6 +72,7 @@ struct ernie_hip_ctx {
     std::string error;
     int query_rows = 128;
     std::vector<BlockWeights> blocks;
+    std::vector<TextBlockWeights> text_blocks;
     HeadWeights heads;
     // Activation workspace, grown on demand.
     DeviceBuffer ws;
@@ -67,6 +80,8 @@ struct ernie_hip_ctx {
     DeviceBuffer head_ws;  // head intermediates
     DeviceBuffer dit_act;  // run_dit activations: x [S][dim], c, mods
     DeviceBuffer split_ws;   // GEMM tail-row split-K partial sums
+    DeviceBuffer text_ws;    // text block activations
+    DeviceBuffer ones;       // FP32 ones: unit gates of the text block's residual epilogues
     // Event timing.
     bool profiling = false;
     unsigned profile_mask = ~0u;  // classes that record events while profiling
@@ -135,6 +150,12 @@ void free_block(BlockWeights& w)
 {
     for (DeviceBuffer* b : {&w.norm1, &w.norm_q, &w.norm_k, &w.norm2, &w.wqkv, &w.wo, &w.w_ug, &w.w_down}) dev_free(*b);
     w = BlockWeights{};
+}
+
+void free_text_block(TextBlockWeights& w)
+{
+    for (DeviceBuffer* b : {&w.norm1, &w.norm2, &w.wqkv, &w.wo, &w.w_ug, &w.w_down}) dev_free(*b);
+    w = TextBlockWeights{};
 }
 
 void free_heads(HeadWeights& h)
@@ -249,26 +270,39 @@ int alloc_block(ernie_hip_ctx* ctx, BlockWeights& w, int dim, int ffn, int dtype
 
 // Rewrites the 16-bit projection matrices of a freshly written block K-tiled,
 // through the staging buffer, and records which ones were.
-int tile_block_weights(ernie_hip_ctx* ctx, BlockWeights& w)
+struct TiledMat { DeviceBuffer* b; int rows, cols; };
+
+int tile_matrices(ernie_hip_ctx* ctx, int dtype, const TiledMat (&mats)[4], bool (&k32)[4])
 {
-    if (w.dtype == ERNIE_DTYPE_FP32) return ERNIE_OK;
-    const int D = w.dim, F = w.ffn;
-    struct Mat { DeviceBuffer* b; int rows, cols; };
-    const Mat mats[4] = {{&w.wqkv, 3 * D, D}, {&w.wo, D, D}, {&w.w_ug, 2 * F, D}, {&w.w_down, D, F}};
+    if (dtype == ERNIE_DTYPE_FP32) return ERNIE_OK;
     size_t most = 0;
-    for (const Mat& m : mats) most = std::max(most, (size_t)m.rows * m.cols * 2);
+    for (const TiledMat& m : mats) most = std::max(most, (size_t)m.rows * m.cols * 2);
     int rc = dev_alloc(ctx, ctx->staging, most, "staging buffer");
     for (int i = 0; i < 4 && !rc; ++i) {
-        const Mat& m = mats[i];
+        const TiledMat& m = mats[i];
         const size_t bytes = (size_t)m.rows * m.cols * 2;
         if (m.rows % 256 || m.cols % 32 || bytes >= (1ull << 31)) continue;
         rc = hip_status(ctx, hipMemcpyAsync(ctx->staging.ptr, m.b->ptr, bytes, hipMemcpyDeviceToDevice, ctx->stream),
                         "tile weights");
         if (!rc) rc = kernel_status(ctx, tile_k32(ctx->staging.ptr, m.b->ptr, m.rows, m.cols, ctx->stream), "tile weights");
-        if (!rc) w.k32[i] = true;
+        if (!rc) k32[i] = true;
     }
     if (!rc) rc = hip_status(ctx, hipStreamSynchronize(ctx->stream), "tile weights");
     return rc;
+}
+
+int tile_block_weights(ernie_hip_ctx* ctx, BlockWeights& w)
+{
+    const int D = w.dim, F = w.ffn;
+    const TiledMat mats[4] = {{&w.wqkv, 3 * D, D}, {&w.wo, D, D}, {&w.w_ug, 2 * F, D}, {&w.w_down, D, F}};
+    return tile_matrices(ctx, w.dtype, mats, w.k32);
+}
+
+int tile_text_weights(ernie_hip_ctx* ctx, TextBlockWeights& w)
+{
+    const int H = w.hidden, F = w.ffn, QD = w.heads * 128, QKV = (w.heads + 2 * w.kv_heads) * 128;
+    const TiledMat mats[4] = {{&w.wqkv, QKV, H}, {&w.wo, H, QD}, {&w.w_ug, 2 * F, H}, {&w.w_down, H, F}};
+    return tile_matrices(ctx, w.dtype, mats, w.k32);
 }
 
 int check_block_dims(ernie_hip_ctx* ctx, int dim, int ffn, int dtype)
@@ -453,6 +487,168 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
     return ERNIE_OK;
 }
 
+// ---- Mistral text block (tests/fixtures/text-s64.ncnn.param) ------------------------------
+int ones_buffer(ernie_hip_ctx* ctx, int n, const float** out)
+{
+    const size_t bytes = (size_t)n * 4;
+    if (ctx->ones.bytes < bytes) {
+        int rc = dev_alloc(ctx, ctx->ones, bytes, "ones");
+        if (rc) return rc;
+        rc = hip_status(ctx, hipMemsetD32Async(static_cast<hipDeviceptr_t>(ctx->ones.ptr), 0x3f800000u, n, ctx->stream),
+                        "ones");
+        if (rc) return rc;
+    }
+    *out = static_cast<const float*>(ctx->ones.ptr);
+    return ERNIE_OK;
+}
+
+// rmsn_8 -> gemm_0/1/2 -> rotary (lines 18-44) -> sdpa_20 (GQA, additive mask in3) ->
+// gemm_3 + add_12 -> rmsn_9 -> gemm_4 (gate) silu_7, gemm_5 (up), mul_13 -> gemm_6 + add_14.
+// The residual adds are the GEMM epilogues with a unit gate; the gated MLP is one GEMM
+// over the interleaved up/gate rows with a SiLU epilogue. out may alias x.
+int text_block_forward(ernie_hip_ctx* ctx, const TextBlockWeights& w, const float* x, float* out, const float* cos_t,
+                       const float* sin_t, const float* mask, int S)
+{
+    const int H = w.hidden, F = w.ffn, nq = w.heads, nk = w.kv_heads, dt = w.dtype;
+    const int QD = nq * 128, KVD = nk * 128, QKV = QD + 2 * KVD;
+    const size_t e = esize(dt);
+    const double dS = S;
+    auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+    const size_t bh = up((size_t)S * H * e), bqkv = up((size_t)S * QKV * e), battn = up((size_t)S * QD * e),
+                 bx1 = up((size_t)S * H * 4), bp = up((size_t)S * F * e);
+    int rc = dev_alloc(ctx, ctx->text_ws, bh + bqkv + battn + bx1 + bp, "text workspace");
+    if (rc) return rc;
+    char* base = static_cast<char*>(ctx->text_ws.ptr);
+    void *h = base, *qkv = base + bh, *attn = base + bh + bqkv, *p = base + bh + bqkv + battn + bx1;
+    float* x1 = reinterpret_cast<float*>(base + bh + bqkv + battn);
+    const float* ones = nullptr;
+    rc = ones_buffer(ctx, H, &ones);
+    if (rc) return rc;
+    hipStream_t s = ctx->stream;
+    void* split_ws = nullptr;
+    size_t split_ws_bytes = 0;
+    rc = split_workspace(ctx, S, nq, &split_ws, &split_ws_bytes);
+    if (rc) return rc;
+    {
+        Timed t(ctx, P_NORM, 0, dS * H * (4 + e));
+        rc = kernel_status(ctx, rmsnorm_modulate(x, ERNIE_DTYPE_FP32, static_cast<const float*>(w.norm1.ptr), nullptr,
+                                                 nullptr, S, H, 1e-5f, h, dt, s), "text rmsnorm");
+        if (rc) return rc;
+    }
+    {
+        GemmArgs g;
+        g.A = h; g.lda = H; g.W = w.wqkv.ptr; g.ldw = H; g.M = S; g.N = QKV; g.K = H; g.dtype = dt;
+        g.w_k32 = w.k32[0];
+        g.epilogue = EPI_STORE; g.C = qkv; g.ldc = QKV; g.c_dtype = dt;
+        g.split_ws = split_ws; g.split_ws_bytes = split_ws_bytes;
+        Timed t(ctx, P_QKV, 2.0 * dS * QKV * H, gemm_bytes(dS, QKV, H, e, e));
+        rc = kernel_status(ctx, gemm(g, s), "text gemm qkv");
+        if (rc) return rc;
+    }
+    {
+        Timed t(ctx, P_ROPE, 0, dS * (QD + KVD) * e * 2 + dS * 128 * 8);
+        rc = kernel_status(ctx, qk_norm_rope_qk(qkv, dt, S, nq, nk, QKV, QD, nullptr, nullptr, cos_t, sin_t, s),
+                           "text rotary");
+        if (rc) return rc;
+    }
+    {
+        SdpaArgs a;
+        a.q = qkv; a.k = static_cast<char*>(qkv) + (size_t)QD * e; a.v = static_cast<char*>(qkv) + (size_t)(QD + KVD) * e;
+        a.o = attn; a.dtype = dt; a.heads = nq; a.kv_heads = nk; a.sq = S; a.sk = S; a.d = kHeadDim;
+        a.q_hs = a.k_hs = a.v_hs = kHeadDim; a.q_rs = a.k_rs = a.v_rs = QKV;
+        a.o_hs = kHeadDim; a.o_rs = QD;
+        a.mask = mask; a.mask_heads = 1; a.mask_rows = mask ? S : 1;
+        a.split_ws = split_ws; a.split_ws_bytes = split_ws_bytes;
+        Timed t(ctx, P_SDPA, 4.0 * dS * dS * kHeadDim * nq, dS * (2 * QD + 2 * KVD) * e);
+        rc = kernel_status(ctx, sdpa(a, s), "text sdpa");
+        if (rc) return rc;
+    }
+    {
+        GemmArgs g;
+        g.A = attn; g.lda = QD; g.W = w.wo.ptr; g.ldw = QD; g.M = S; g.N = H; g.K = QD; g.dtype = dt;
+        g.w_k32 = w.k32[1];
+        g.epilogue = EPI_GATE_RESID; g.C = x1; g.ldc = H; g.c_dtype = ERNIE_DTYPE_FP32; g.resid = x; g.ld_resid = H;
+        g.gate = ones;
+        g.split_ws = split_ws; g.split_ws_bytes = split_ws_bytes;
+        Timed t(ctx, P_OUT, 2.0 * dS * H * QD, gemm_bytes(dS, H, QD, e, 8));
+        rc = kernel_status(ctx, gemm(g, s), "text gemm o");
+        if (rc) return rc;
+    }
+    {
+        Timed t(ctx, P_NORM, 0, dS * H * (4 + e));
+        rc = kernel_status(ctx, rmsnorm_modulate(x1, ERNIE_DTYPE_FP32, static_cast<const float*>(w.norm2.ptr), nullptr,
+                                                 nullptr, S, H, 1e-5f, h, dt, s), "text rmsnorm 2");
+        if (rc) return rc;
+    }
+    {
+        GemmArgs g;
+        g.A = h; g.lda = H; g.W = w.w_ug.ptr; g.ldw = H; g.M = S; g.N = 2 * F; g.K = H; g.dtype = dt;
+        g.w_k32 = w.k32[2];
+        g.epilogue = EPI_SWIGLU; g.C = p; g.ldc = F; g.c_dtype = dt;
+        g.split_ws = split_ws; g.split_ws_bytes = split_ws_bytes;
+        Timed t(ctx, P_UG, 2.0 * dS * 2 * F * H, gemm_bytes(dS, 2.0 * F, H, e, 0) + dS * F * e);
+        rc = kernel_status(ctx, gemm(g, s), "text gemm gate/up");
+        if (rc) return rc;
+    }
+    {
+        GemmArgs g;
+        g.A = p; g.lda = F; g.W = w.w_down.ptr; g.ldw = F; g.M = S; g.N = H; g.K = F; g.dtype = dt;
+        g.w_k32 = w.k32[3];
+        g.epilogue = EPI_GATE_RESID; g.C = out; g.ldc = H; g.c_dtype = ERNIE_DTYPE_FP32; g.resid = x1; g.ld_resid = H;
+        g.gate = ones;
+        g.split_ws = split_ws; g.split_ws_bytes = split_ws_bytes;
+        Timed t(ctx, P_DOWN, 2.0 * dS * H * F, gemm_bytes(dS, H, F, e, 8));
+        rc = kernel_status(ctx, gemm(g, s), "text gemm down");
+        if (rc) return rc;
+    }
+    return ERNIE_OK;
+}
+
+int check_text_dims(ernie_hip_ctx* ctx, int hidden, int heads, int kv_heads, int ffn, int dtype)
+{
+    if (!valid_dtype(dtype)) return fail(ctx, ERNIE_ERROR, "invalid dtype");
+    if (hidden < 128 || hidden % 128 || hidden > 4096) return fail(ctx, ERNIE_ERROR, "hidden must be a multiple of 128 in [128,4096]");
+    if (heads < 1 || kv_heads < 1 || heads % kv_heads || heads * 128 > 8192)
+        return fail(ctx, ERNIE_ERROR, "heads must be a positive multiple of kv_heads, at most 64");
+    if (ffn < 32 || ffn % 32) return fail(ctx, ERNIE_ERROR, "ffn must be a positive multiple of 32");
+    return ERNIE_OK;
+}
+
+int alloc_text_block(ernie_hip_ctx* ctx, TextBlockWeights& w, int hidden, int heads, int kv_heads, int ffn, int dtype)
+{
+    const size_t e = esize(dtype), QKV = (size_t)(heads + 2 * kv_heads) * 128;
+    int rc = 0;
+    rc = rc ? rc : dev_alloc(ctx, w.norm1, (size_t)hidden * 4, "text block weights");
+    rc = rc ? rc : dev_alloc(ctx, w.norm2, (size_t)hidden * 4, "text block weights");
+    rc = rc ? rc : dev_alloc(ctx, w.wqkv, QKV * hidden * e, "text block weights");
+    rc = rc ? rc : dev_alloc(ctx, w.wo, (size_t)hidden * heads * 128 * e, "text block weights");
+    rc = rc ? rc : dev_alloc(ctx, w.w_ug, 2 * (size_t)ffn * hidden * e, "text block weights");
+    rc = rc ? rc : dev_alloc(ctx, w.w_down, (size_t)hidden * ffn * e, "text block weights");
+    if (rc) {
+        free_text_block(w);
+        return rc;
+    }
+    w.hidden = hidden; w.heads = heads; w.kv_heads = kv_heads; w.ffn = ffn; w.dtype = dtype;
+    return ERNIE_OK;
+}
+
+TextBlockWeights* text_slot(ernie_hip_ctx* ctx, int index)
+{
+    if (index < 0 || index > 4096) return nullptr;
+    if ((size_t)index >= ctx->text_blocks.size()) ctx->text_blocks.resize(index + 1);
+    return &ctx->text_blocks[index];
+}
+
+int check_text_call(ernie_hip_ctx* ctx, int index, int S, const void* x, const void* out, const void* cos_t,
+                    const void* sin_t)
+{
+    if (index < 0 || (size_t)index >= ctx->text_blocks.size() || !ctx->text_blocks[index].loaded)
+        return fail(ctx, ERNIE_ERROR, "text block " + std::to_string(index) + " is not loaded");
+    if (S < 1 || S > 65536) return fail(ctx, ERNIE_ERROR, "token count out of range");
+    if (!x || !out || !cos_t || !sin_t) return fail(ctx, ERNIE_ERROR, "null text block tensor");
+    return ERNIE_OK;
+}
+
 // ---- heads ------------------------------------------------------------------------
 int head_gemm(ernie_hip_ctx* ctx, const void* a, const void* w, const float* bias, float* c, int M, int N, int K, int dt)
 {
@@ -565,7 +761,10 @@ void ernie_hip_destroy(ernie_hip_ctx* ctx)
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     for (auto& b : ctx->blocks) free_block(b);
+    for (auto& b : ctx->text_blocks) free_text_block(b);
     free_heads(ctx->heads);
+    dev_free(ctx->text_ws);
+    dev_free(ctx->ones);
     dev_free(ctx->ws);
     dev_free(ctx->staging);
     dev_free(ctx->head_ws);
@@ -888,6 +1087,151 @@ int ernie_hip_block_sequence(ernie_hip_ctx* ctx, const int* blocks, int count, c
         if (!rc) {
             (void)hipEventRecord(ev[count], ctx->stream);
             rc = hip_status(ctx, hipEventSynchronize(ev[count]), "block timing");
+        }
+        for (int i = 0; i < count && !rc; ++i) {
+            float ms = 0.f;
+            (void)hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
+            seconds[i] = ms * 1e-3;
+        }
+        for (auto& e : ev) (void)hipEventDestroy(e);
+    }
+    return rc;
+}
+
+// ---- Mistral text blocks -----------------------------------------------------------------
+int ernie_hip_text_block_upload_tensors(ernie_hip_ctx* ctx, int index, const ernie_text_block_host_tensors* w,
+                                        int hidden, int heads, int kv_heads, int ffn, int dtype)
+{
+    if (!ctx || !w) return ERNIE_ERROR;
+    int rc = check_text_dims(ctx, hidden, heads, kv_heads, ffn, dtype);
+    if (rc) return rc;
+    const ernie_host_tensor* parts[] = {&w->norm1, &w->wq, &w->wk, &w->wv, &w->wo,
+                                        &w->norm2, &w->w_gate, &w->w_up, &w->w_down};
+    for (const ernie_host_tensor* t : parts) {
+        if (!t->data) return fail(ctx, ERNIE_ERROR, "null text block weight");
+        if (!valid_dtype(t->dtype)) return fail(ctx, ERNIE_ERROR, "invalid text block weight dtype");
+    }
+    TextBlockWeights* slot = text_slot(ctx, index);
+    if (!slot) return fail(ctx, ERNIE_ERROR, "text block index out of range");
+    free_text_block(*slot);
+    TextBlockWeights tw;
+    rc = alloc_text_block(ctx, tw, hidden, heads, kv_heads, ffn, dtype);
+    if (rc) return rc;
+    const size_t QD = (size_t)heads * 128 * hidden, KVD = (size_t)kv_heads * 128 * hidden;
+    constexpr int F32 = ERNIE_DTYPE_FP32;
+    rc = rc ? rc : upload_tensor(ctx, tw.norm1.ptr, 0, F32, w->norm1.data, w->norm1.dtype, hidden, "norm1");
+    rc = rc ? rc : upload_tensor(ctx, tw.norm2.ptr, 0, F32, w->norm2.data, w->norm2.dtype, hidden, "norm2");
+    rc = rc ? rc : upload_tensor(ctx, tw.wqkv.ptr, 0, dtype, w->wq.data, w->wq.dtype, QD, "wq");
+    rc = rc ? rc : upload_tensor(ctx, tw.wqkv.ptr, QD, dtype, w->wk.data, w->wk.dtype, KVD, "wk");
+    rc = rc ? rc : upload_tensor(ctx, tw.wqkv.ptr, QD + KVD, dtype, w->wv.data, w->wv.dtype, KVD, "wv");
+    rc = rc ? rc : upload_tensor(ctx, tw.wo.ptr, 0, dtype, w->wo.data, w->wo.dtype, QD, "wo");
+    rc = rc ? rc : upload_tensor(ctx, tw.w_down.ptr, 0, dtype, w->w_down.data, w->w_down.dtype,
+                                 (size_t)hidden * ffn, "w_down");
+    for (int parity = 0; parity < 2 && !rc; ++parity) {
+        const ernie_host_tensor& src = parity ? w->w_gate : w->w_up;
+        const size_t bytes = (size_t)ffn * hidden * esize(src.dtype);
+        rc = dev_alloc(ctx, ctx->staging, bytes, "staging buffer");
+        if (!rc) rc = hip_status(ctx, hipMemcpyAsync(ctx->staging.ptr, src.data, bytes, hipMemcpyHostToDevice, ctx->stream), "w_ug");
+        if (!rc) rc = kernel_status(ctx, interleave_up_gate(ctx->staging.ptr, src.dtype, tw.w_ug.ptr, dtype, ffn, hidden,
+                                                            parity, ctx->stream), "w_ug");
+        if (!rc) rc = hip_status(ctx, hipStreamSynchronize(ctx->stream), "w_ug");
+    }
+    if (!rc) rc = hip_status(ctx, hipStreamSynchronize(ctx->stream), "text block upload");
+    if (!rc) rc = tile_text_weights(ctx, tw);
+    if (rc) {
+        free_text_block(tw);
+        return rc;
+    }
+    tw.loaded = true;
+    *slot = tw;
+    return ERNIE_OK;
+}
+
+int ernie_hip_text_block_init_random(ernie_hip_ctx* ctx, int index, int hidden, int heads, int kv_heads, int ffn,
+                                     int dtype, uint64_t seed, float std_dev)
+{
+    if (!ctx) return ERNIE_ERROR;
+    int rc = check_text_dims(ctx, hidden, heads, kv_heads, ffn, dtype);
+    if (rc) return rc;
+    TextBlockWeights* slot = text_slot(ctx, index);
+    if (!slot) return fail(ctx, ERNIE_ERROR, "text block index out of range");
+    free_text_block(*slot);
+    TextBlockWeights tw;
+    rc = alloc_text_block(ctx, tw, hidden, heads, kv_heads, ffn, dtype);
+    if (rc) return rc;
+    const uint64_t stride = 1ull << 40;
+    struct Item { void* p; int dt; size_t n; float mean; };
+    const size_t QKV = (size_t)(heads + 2 * kv_heads) * 128;
+    const Item items[] = {{tw.norm1.ptr, ERNIE_DTYPE_FP32, (size_t)hidden, 1.f},
+                          {tw.wqkv.ptr, dtype, QKV * hidden, 0.f},
+                          {tw.wo.ptr, dtype, (size_t)hidden * heads * 128, 0.f},
+                          {tw.norm2.ptr, ERNIE_DTYPE_FP32, (size_t)hidden, 1.f},
+                          {tw.w_ug.ptr, dtype, 2 * (size_t)ffn * hidden, 0.f},
+                          {tw.w_down.ptr, dtype, (size_t)hidden * ffn, 0.f}};
+    uint64_t k = 0;
+    for (const Item& it : items) {
+        rc = kernel_status(ctx, fill_normal(it.p, it.dt, it.n, seed, (k++) * stride, it.mean, std_dev, ctx->stream),
+                           "text init");
+        if (rc) break;
+    }
+    if (!rc) rc = hip_status(ctx, hipStreamSynchronize(ctx->stream), "text init");
+    if (!rc) rc = tile_text_weights(ctx, tw);
+    if (rc) {
+        free_text_block(tw);
+        return rc;
+    }
+    tw.loaded = true;
+    *slot = tw;
+    return ERNIE_OK;
+}
+
+int ernie_hip_text_block_release(ernie_hip_ctx* ctx, int index)
+{
+    if (!ctx || index < 0 || (size_t)index >= ctx->text_blocks.size()) return ERNIE_ERROR;
+    (void)hipStreamSynchronize(ctx->stream);
+    free_text_block(ctx->text_blocks[index]);
+    return ERNIE_OK;
+}
+
+int ernie_hip_text_block_forward(ernie_hip_ctx* ctx, int index, const float* x, float* out, const float* cos_t,
+                                 const float* sin_t, const float* mask, int S)
+{
+    if (!ctx) return ERNIE_ERROR;
+    const int rc = check_text_call(ctx, index, S, x, out, cos_t, sin_t);
+    if (rc) return rc;
+    return text_block_forward(ctx, ctx->text_blocks[index], x, out, cos_t, sin_t, mask, S);
+}
+
+int ernie_hip_text_block_sequence(ernie_hip_ctx* ctx, const int* blocks, int count, const float* x, float* out,
+                                  const float* cos_t, const float* sin_t, const float* mask, int S, double* seconds)
+{
+    if (!ctx || !blocks) return ERNIE_ERROR;
+    if (count < 1 || count > 25) return fail(ctx, ERNIE_ERROR, "Text path requires 1..25 blocks");
+    for (int i = 0; i < count; ++i) {
+        const int rc = check_text_call(ctx, blocks[i], S, x, out, cos_t, sin_t);
+        if (rc) return rc;
+        if (ctx->text_blocks[blocks[i]].hidden != ctx->text_blocks[blocks[0]].hidden)
+            return fail(ctx, ERNIE_ERROR, "text blocks differ in width");
+    }
+    std::vector<hipEvent_t> ev;
+    if (seconds) {
+        ev.resize(count + 1, nullptr);
+        for (auto& e : ev)
+            if (hipEventCreate(&e) != hipSuccess) {
+                for (auto& f : ev)
+                    if (f) (void)hipEventDestroy(f);
+                return fail(ctx, ERNIE_ERROR, "event create");
+            }
+    }
+    int rc = ERNIE_OK;
+    for (int i = 0; i < count && !rc; ++i) {
+        if (seconds) (void)hipEventRecord(ev[i], ctx->stream);
+        rc = text_block_forward(ctx, ctx->text_blocks[blocks[i]], i == 0 ? x : out, out, cos_t, sin_t, mask, S);
+    }
+    if (seconds) {
+        if (!rc) {
+            (void)hipEventRecord(ev[count], ctx->stream);
+            rc = hip_status(ctx, hipEventSynchronize(ev[count]), "text block timing");
         }
         for (int i = 0; i < count && !rc; ++i) {
             float ms = 0.f;

@@ -190,11 +190,11 @@ __global__ void __launch_bounds__(512) gemm16_kernel(GemmParams p)
         for (int r = 0; r < 16; ++r) {
             const int m = row0 + sub * 32 + 8 * (r >> 2) + 4 * lgrp + (r & 3);
             if (m >= p.M) continue;
-            if (EPI == EPI_GEGLU) {
+            if (epi_glu(EPI)) {
                 const int nout = (n0 + wn * 64) / 2 + lrow;
                 if (2 * nout < p.N) {
                     const float up = acc[i][0][r], g = acc[i][1][r];
-                    static_cast<OutT*>(p.C)[(size_t)m * p.ldc + nout] = OutT(up * gelu_erf(g));
+                    static_cast<OutT*>(p.C)[(size_t)m * p.ldc + nout] = OutT(up * glu_act<EPI == EPI_SWIGLU>(g));
                 }
             } else {
 #pragma unroll
@@ -290,10 +290,11 @@ __global__ void __launch_bounds__(256) gemm32_kernel(GemmParams p)
         for (int r = 0; r < 16; ++r) {
             const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lgrp + (r & 3);
             if (m >= p.M) continue;
-            if (EPI == EPI_GEGLU) {
+            if (epi_glu(EPI)) {
                 const int nout = (n0 + wn * 64) / 2 + lrow;
                 if (2 * nout < p.N)
-                    static_cast<float*>(p.C)[(size_t)m * p.ldc + nout] = acc[i][0][r] * gelu_erf(acc[i][1][r]);
+                    static_cast<float*>(p.C)[(size_t)m * p.ldc + nout] =
+                        acc[i][0][r] * glu_act<EPI == EPI_SWIGLU>(acc[i][1][r]);
             } else {
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
@@ -336,9 +337,14 @@ int launch16(const GemmArgs& a, GemmParams& p, hipStream_t s)
         else return -1;
     } else if (a.epilogue == EPI_GATE_RESID) {
         hipLaunchKernelGGL((gemm16_kernel<T, float, EPI_GATE_RESID>), grid, block, 0, s, p);
-    } else {
+    } else if (a.epilogue == EPI_SWIGLU) {
+        if (a.c_dtype != a.dtype) return -1;
+        hipLaunchKernelGGL((gemm16_kernel<T, T, EPI_SWIGLU>), grid, block, 0, s, p);
+    } else if (a.epilogue == EPI_GEGLU) {
         if (a.c_dtype != a.dtype) return -1;
         hipLaunchKernelGGL((gemm16_kernel<T, T, EPI_GEGLU>), grid, block, 0, s, p);
+    } else {
+        return -1;
     }
     return 0;
 }
@@ -355,9 +361,9 @@ int gemm(const GemmArgs& a, hipStream_t s)
     if (a.lda < a.K || a.ldw < a.K || a.lda % align || a.ldw % align) return -1;
     if ((reinterpret_cast<uintptr_t>(a.A) | reinterpret_cast<uintptr_t>(a.W)) & 15) return -1;
     if (a.epilogue == EPI_GATE_RESID && (!a.resid || !a.gate || a.c_dtype != DT_F32)) return -1;
-    if (a.epilogue == EPI_GEGLU && (a.N % 64 || a.ldc < a.N / 2)) return -1;
-    if (a.epilogue != EPI_GEGLU && a.ldc < a.N) return -1;
-    if (a.epilogue > EPI_GEGLU || a.epilogue < 0) return -1;
+    if (epi_glu(a.epilogue) && (a.N % 64 || a.ldc < a.N / 2)) return -1;
+    if (!epi_glu(a.epilogue) && a.ldc < a.N) return -1;
+    if (a.epilogue < 0 || (a.epilogue > EPI_GEGLU && a.epilogue != EPI_SWIGLU)) return -1;
     // Only the 16-bit kernel reads or writes K-tiled operands.
     if ((a.w_k32 || a.a_k32_rows || a.c_k32_rows) && a.dtype == DT_F32) return -1;
     GemmParams p{};
@@ -373,7 +379,9 @@ int gemm(const GemmArgs& a, hipStream_t s)
         const dim3 grid(p.m_tiles * p.n_tiles), block(256);
         if (a.epilogue == EPI_STORE) hipLaunchKernelGGL((gemm32_kernel<EPI_STORE>), grid, block, 0, s, p);
         else if (a.epilogue == EPI_GATE_RESID) hipLaunchKernelGGL((gemm32_kernel<EPI_GATE_RESID>), grid, block, 0, s, p);
-        else hipLaunchKernelGGL((gemm32_kernel<EPI_GEGLU>), grid, block, 0, s, p);
+        else if (a.epilogue == EPI_SWIGLU) hipLaunchKernelGGL((gemm32_kernel<EPI_SWIGLU>), grid, block, 0, s, p);
+        else if (a.epilogue == EPI_GEGLU) hipLaunchKernelGGL((gemm32_kernel<EPI_GEGLU>), grid, block, 0, s, p);
+        else return -1;
     } else if ((rc = gemm16_pingpong(a, s)) != 1) {
         return rc;
     } else if (a.dtype == DT_F16) {

@@ -71,7 +71,7 @@ template <typename OutT, int EPI>
 __global__ void __launch_bounds__(256) split_reduce_kernel(Params p)
 {
     const int rows = 64 * p.tail_sub;
-    const int cols = EPI == EPI_GEGLU ? p.N / 2 : p.N;
+    const int cols = epi_glu(EPI) ? p.N / 2 : p.N;
     const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (long)rows * cols) return;
     const int rl = (int)(idx / cols), c = (int)(idx - (long)rl * cols);
@@ -79,16 +79,17 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(Params p)
     if (m >= p.M) return;
     // Column n of the tile grid; GEGLU output column c holds up column (c / 32) * 64 + c % 32
     // and gate column + 32 of the interleaved W rows.
-    const int n = EPI == EPI_GEGLU ? (c / 32) * 64 + (c % 32) : c;
+    const int n = epi_glu(EPI) ? (c / 32) * 64 + (c % 32) : c;
     const int nt = n / BN, cl = n - nt * BN;
     const float* base = p.part + (size_t)nt * p.split * rows * BN + (size_t)rl * BN + cl;
     float v = 0.f, g = 0.f;
     for (int q = 0; q < p.split; ++q) {
         v += base[(size_t)q * rows * BN];
-        if (EPI == EPI_GEGLU) g += base[(size_t)q * rows * BN + 32];
+        if (epi_glu(EPI)) g += base[(size_t)q * rows * BN + 32];
     }
-    if (EPI == EPI_GEGLU) {
-        static_cast<OutT*>(p.C)[(size_t)m * p.c_rs + (size_t)(c >> 5) * p.c_ss + (c & 31)] = OutT(v * gelu_erf(g));
+    if (epi_glu(EPI)) {
+        static_cast<OutT*>(p.C)[(size_t)m * p.c_rs + (size_t)(c >> 5) * p.c_ss + (c & 31)] =
+            OutT(v * glu_act<EPI == EPI_SWIGLU>(g));
     } else if (EPI == EPI_STORE) {
         if (p.bias) v += p.bias[n];
         static_cast<OutT*>(p.C)[(size_t)m * p.ldc + n] = OutT(v);
@@ -352,7 +353,7 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
         for (int r = 0; r < 4; ++r) {
             const int m = row_w + 16 * i + r;
             if (m >= p.M) continue;
-            if (EPI == EPI_GEGLU) {
+            if (epi_glu(EPI)) {
                 // This wave's 64 W rows are 32 up rows then the 32 matching gate rows:
                 // output columns 32 g .. 32 g + 31, g = (n0 + 64 wn) / 64.
                 const size_t cg = (size_t)((n0 + wn * 64) >> 6) * p.c_ss;
@@ -360,7 +361,7 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
                 for (int j = 0; j < 2; ++j) {
                     if (n0 + wn * 64 < p.N)
                         static_cast<OutT*>(p.C)[(size_t)m * p.c_rs + cg + 16 * j + r16] =
-                            OutT(acc[i][j][r] * gelu_erf(acc[i][j + 2][r]));
+                            OutT(acc[i][j][r] * glu_act<EPI == EPI_SWIGLU>(acc[i][j + 2][r]));
                 }
             } else {
 #pragma unroll
@@ -401,7 +402,7 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     const int other = a.w_k32 || a.a_k32_rows || a.c_k32_rows ? -1 : 1;
     if (a.dtype == DT_F32 || a.K % pingpong::BK) return other;
     if (a.epilogue == EPI_STORE && a.c_dtype != DT_F32 && a.c_dtype != a.dtype) return -1;
-    if (a.epilogue == EPI_GEGLU && a.c_dtype != a.dtype) return -1;
+    if (epi_glu(a.epilogue) && a.c_dtype != a.dtype) return -1;
     // Buffer offsets are 32-bit: every staged row of every tile (rounded up to 256)
     // must lie below 2^31 bytes; larger operands take the register-staged kernel.
     const double ab = ((a.M + 255) / 256 * 256.0) * a.lda * 2, wb = ((a.N + 255) / 256 * 256.0) * a.ldw * 2;
@@ -412,7 +413,7 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     if (a.a_k32_rows && (a.a_k32_rows < (a.M + pingpong::BM - 1) / pingpong::BM * pingpong::BM || a.lda != a.K ||
                          (double)a.a_k32_rows * a.K * 2 >= 2147483647.0))
         return -1;
-    if (a.c_k32_rows && (a.epilogue != EPI_GEGLU || a.c_k32_rows < a.M)) return -1;
+    if (a.c_k32_rows && (!epi_glu(a.epilogue) || a.c_k32_rows < a.M)) return -1;
     pingpong::Params p{};
     p.A = a.A; p.lda = a.lda; p.W = a.W; p.ldw = a.ldw; p.M = a.M; p.N = a.N; p.K = a.K;
     p.C = a.C; p.ldc = a.ldc; p.bias = a.bias; p.resid = a.resid; p.ld_resid = a.ld_resid; p.gate = a.gate;
@@ -447,6 +448,8 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
             else hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_STORE>), grid, block, 0, s, p);                     \
         } else if (a.epilogue == EPI_GATE_RESID) {                                                            \
             hipLaunchKernelGGL((pingpong::kernel<T, float, EPI_GATE_RESID>), grid, block, 0, s, p);                 \
+        } else if (a.epilogue == EPI_SWIGLU) {                                                                \
+            hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_SWIGLU>), grid, block, 0, s, p);                         \
         } else {                                                                                              \
             hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_GEGLU>), grid, block, 0, s, p);                          \
         }                                                                                                     \
@@ -455,7 +458,7 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     else EHIP_PINGPONG(bf16);
 #undef EHIP_PINGPONG
     if (p.split > 1) {
-        const long items = (long)64 * p.tail_sub * (a.epilogue == EPI_GEGLU ? a.N / 2 : a.N);
+        const long items = (long)64 * p.tail_sub * (epi_glu(a.epilogue) ? a.N / 2 : a.N);
         const dim3 rgrid((unsigned)((items + 255) / 256)), rblock(256);
 #define EHIP_REDUCE(OUT, EPI) hipLaunchKernelGGL((pingpong::split_reduce_kernel<OUT, EPI>), rgrid, rblock, 0, s, p)
         if (a.epilogue == EPI_STORE) {
@@ -464,6 +467,9 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
             else EHIP_REDUCE(bf16, EPI_STORE);
         } else if (a.epilogue == EPI_GATE_RESID) {
             EHIP_REDUCE(float, EPI_GATE_RESID);
+        } else if (a.epilogue == EPI_SWIGLU) {
+            if (a.dtype == DT_F16) EHIP_REDUCE(f16, EPI_SWIGLU);
+            else EHIP_REDUCE(bf16, EPI_SWIGLU);
         } else {
             if (a.dtype == DT_F16) EHIP_REDUCE(f16, EPI_GEGLU);
             else EHIP_REDUCE(bf16, EPI_GEGLU);

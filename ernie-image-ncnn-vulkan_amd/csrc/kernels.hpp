@@ -14,7 +14,10 @@ enum Epilogue : int {
     EPI_STORE = 0,       // C = acc (+ bias[n]), C dtype = c_dtype
     EPI_GATE_RESID = 1,  // C(f32) = resid(f32) + gate[n] * acc
     EPI_GEGLU = 2,       // W rows interleaved in 32-row [up | gate] pairs; C[m][n/2] = up * gelu(gate)
+    EPI_SWIGLU = 4,      // as EPI_GEGLU with SiLU on the gate: C[m][n/2] = up * silu(gate) (the text MLP)
 };
+// Gated epilogues: W rows interleaved in 32-row [up | gate] pairs, N/2 outputs.
+constexpr bool epi_glu(int e) { return e == EPI_GEGLU || e == EPI_SWIGLU; }
 
 struct GemmArgs {
     const void* A = nullptr;  // [M][lda], dtype

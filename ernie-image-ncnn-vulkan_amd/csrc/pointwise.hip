@@ -288,7 +288,8 @@ __global__ void __launch_bounds__(256) layernorm_mod_kernel(const float* __restr
 // per workgroup: the q heads (gamma gq, at the row start) and then the k heads
 // (gamma gk, at k_offset). A head is handled by 16 lanes, lane l owning values
 // [4l, 4l+4) and [64+4l, 64+4l+4), the rotary pairs (d, d+64); the token's cos /
-// sin and the two gammas are loaded once per lane and reused for every head.
+// sin and the two gammas are loaded once per lane and reused for every head. A NULL
+// gamma skips the norm of its heads: rotary only (the text block has no Q/K norm).
 template <typename T>
 __global__ void __launch_bounds__(256) qk_norm_rope_kernel(T* __restrict__ x, int nq, int nk, long row_stride,
                                                            long k_offset, const float* __restrict__ gq,
@@ -308,13 +309,18 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(T* __restrict__ x, in
         T* v = row + (is_k ? k_offset + (long)(h - nq) * 128 : (long)h * 128);
         const float* g = is_k ? gk : gq;
         const f32x4 a = Vec4<T>::load(v + d), b = Vec4<T>::load(v + 64 + d);
-        float ss = 0.f;
+        float inv = 1.0f;
+        f32x4 ga = {1.f, 1.f, 1.f, 1.f}, gb = {1.f, 1.f, 1.f, 1.f};
+        if (g) {  // NULL gamma: rotary only (the text block has no Q/K norm)
+            float ss = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) ss += a[e] * a[e] + b[e] * b[e];
+            for (int e = 0; e < 4; ++e) ss += a[e] * a[e] + b[e] * b[e];
 #pragma unroll
-        for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 16);
-        const float inv = 1.0f / sqrtf(ss / 128.f + 1e-6f);
-        const f32x4 ga = Vec4<float>::load(g + d), gb = Vec4<float>::load(g + 64 + d);
+            for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 16);
+            inv = 1.0f / sqrtf(ss / 128.f + 1e-6f);
+            ga = Vec4<float>::load(g + d);
+            gb = Vec4<float>::load(g + 64 + d);
+        }
         f32x4 lo, hi;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -570,7 +576,7 @@ int layernorm_modulate(const float* x, const float* shift, const float* scale, i
 int qk_norm_rope_qk(void* x, int dt, int rows, int nq, int nk, long row_stride, long k_offset, const float* gq,
                     const float* gk, const float* cos_t, const float* sin_t, hipStream_t s)
 {
-    if (!x || !gq || (nk && !gk) || !cos_t || !sin_t || rows < 1 || nq < 0 || nk < 0 || nq + nk < 1) return -1;
+    if (!x || !cos_t || !sin_t || rows < 1 || nq < 0 || nk < 0 || nq + nk < 1) return -1;
     if (row_stride < (long)nq * 128 || (nk && (k_offset < (long)nq * 128 || row_stride < k_offset + (long)nk * 128)))
         return -1;
     // Four-value vector accesses: 16-byte (FP32) or 8-byte (16-bit) alignment of every head.

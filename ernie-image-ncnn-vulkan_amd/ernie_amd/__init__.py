@@ -102,6 +102,12 @@ def hip():
             "ernie_hip_block_forward": (c_int, [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int]),
             "ernie_hip_block_sequence": (c_int, [c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int,
                                                  c_vp]),
+            "ernie_hip_text_block_upload_tensors": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_int]),
+            "ernie_hip_text_block_init_random": (c_int, [c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_u64,
+                                                         c_float]),
+            "ernie_hip_text_block_release": (c_int, [c_vp, c_int]),
+            "ernie_hip_text_block_forward": (c_int, [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int]),
+            "ernie_hip_text_block_sequence": (c_int, [c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_vp]),
             "ernie_hip_heads_upload": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int]),
             "ernie_hip_heads_init_random": (c_int, [c_vp, c_int, c_int, c_int, c_int, c_u64, c_float]),
             "ernie_hip_input_head": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_vp]),
@@ -172,6 +178,10 @@ def facade():
                                                  c_int, c_vp, c_vp, cp, c_size_t]),
             "ernie_denoise": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_int,
                                       c_int, c_int, c_int, c_vp, c_vp, cp, c_size_t]),
+            "ernie_text_constants": (c_int, [c_vp, c_int, c_vp, c_vp, c_vp, cp, c_size_t]),
+            "ernie_text_embeddings": (c_int, [c_vp, c_size_t, c_int, c_vp, c_int, c_int, c_vp, cp, c_size_t]),
+            "ernie_run_text_blocks": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_int, c_vp, c_vp, c_vp, c_int, c_vp,
+                                              c_vp, cp, c_size_t]),
             "ernie_sha256_hex": (c_int, [c_vp, c_size_t, cp]),
             "ernie_block_file_inspect": (c_int, [cp, cp, c_int, cp, ctypes.POINTER(BlockFileInfo), cp, c_size_t]),
             "ernie_block_load": (c_int, [c_vp, c_int, cp, cp, c_int, c_int, cp, ctypes.POINTER(BlockFileInfo), cp,
@@ -251,6 +261,38 @@ def dit_constants(freqs, w, h, valid, text):
     if rc < 0:
         _raise(rc, e.value)
     return cos, sin, mask, rc
+
+
+def text_constants(freqs, bucket):
+    """Facade text_constants: 64 YaRN inverse frequencies -> cos, sin [bucket][128], mask [bucket][bucket]."""
+    import numpy as np
+    freqs = np.ascontiguousarray(freqs, np.float32)
+    if freqs.size != 64:
+        raise ValueError("expected 64 inverse frequencies")
+    n = max(bucket, 1)
+    cos = np.empty((n, 128), np.float32)
+    sin = np.empty((n, 128), np.float32)
+    mask = np.empty((n, n), np.float32)
+    e = _err()
+    rc = facade().ernie_text_constants(freqs.ctypes.data, bucket, cos.ctypes.data, sin.ctypes.data, mask.ctypes.data,
+                                       e, 512)
+    if rc < 0:
+        _raise(rc, e.value)
+    return cos, sin, mask
+
+
+def text_embeddings(table_bf16, ids, bucket):
+    """Facade text_embeddings over an in-memory BF16 table (uint16 [vocabulary][width])."""
+    import numpy as np
+    table = np.ascontiguousarray(table_bf16, np.uint16)
+    ids = np.ascontiguousarray(ids, np.uint32)
+    out = np.empty((max(bucket, 1), table.shape[1]), np.float32)
+    e = _err()
+    rc = facade().ernie_text_embeddings(table.ctypes.data, table.shape[0], table.shape[1], ids.ctypes.data, ids.size,
+                                        bucket, out.ctypes.data, e, 512)
+    if rc < 0:
+        _raise(rc, e.value)
+    return out
 
 
 def sha256_hex(data):
@@ -382,6 +424,38 @@ class Context:
                   ptr(sin), ptr(mask), valid_keys, S, secs.ctypes.data if timing else None)
         return secs
 
+    # ---- Mistral text blocks --------------------------------------------------
+    TEXT_FIELDS = ("norm1", "wq", "wk", "wv", "wo", "norm2", "w_gate", "w_up", "w_down")
+
+    def text_block_upload(self, index, weights, hidden, heads, kv_heads, ffn, dtype):
+        """weights: dict of FP32 numpy arrays keyed like TEXT_FIELDS ([out][in] matrices)."""
+        import numpy as np
+        return self.text_block_upload_tensors(
+            index, {f: (np.ascontiguousarray(weights[f], np.float32), FP32) for f in self.TEXT_FIELDS}, hidden,
+            heads, kv_heads, ffn, dtype)
+
+    def text_block_upload_tensors(self, index, tensors, hidden, heads, kv_heads, ffn, dtype):
+        """tensors: dict field -> (numpy array, element dtype); FP16/BF16 arrays hold raw uint16 bits."""
+        import numpy as np
+        keep = [np.ascontiguousarray(tensors[f][0]) for f in self.TEXT_FIELDS]
+        arr = (HostTensor * len(keep))(*[HostTensor(a.ctypes.data, tensors[f][1])
+                                         for a, f in zip(keep, self.TEXT_FIELDS)])
+        self.call("text_block_upload_tensors", index, ctypes.cast(arr, c_vp), hidden, heads, kv_heads, ffn, dtype)
+
+    def text_block_init_random(self, index, hidden, heads, kv_heads, ffn, dtype, seed, std=0.02):
+        self.call("text_block_init_random", index, hidden, heads, kv_heads, ffn, dtype, seed, std)
+
+    def text_block_forward(self, index, x, out, cos, sin, S, mask=None):
+        self.call("text_block_forward", index, ptr(x), ptr(out), ptr(cos), ptr(sin), ptr(mask), S)
+
+    def text_block_sequence(self, blocks, x, out, cos, sin, S, mask=None, timing=False):
+        import numpy as np
+        ids = (c_int * len(blocks))(*blocks)
+        secs = np.zeros(len(blocks), np.float64) if timing else None
+        self.call("text_block_sequence", ctypes.cast(ids, c_vp), len(blocks), ptr(x), ptr(out), ptr(cos), ptr(sin),
+                  ptr(mask), S, secs.ctypes.data if timing else None)
+        return secs
+
     def heads_upload(self, weights, dim, latent_ch, text_dim, dtype):
         import numpy as np
         fields = ("x_w", "x_b", "text_w", "t1_w", "t1_b", "t2_w", "t2_b", "mod_w", "mod_b", "out_mod_w",
@@ -476,6 +550,17 @@ class Facade:
         if rc:
             _raise(rc, e.value)
         return info.as_dict()
+
+    def run_text_blocks(self, blocks, x, S, width, cos, sin, mask, out, dtype=FP32):
+        import numpy as np
+        ids = (c_int * len(blocks))(*blocks)
+        secs = np.zeros(len(blocks), np.float64)
+        e = _err()
+        rc = self.L.ernie_run_text_blocks(self.dev, ctypes.cast(ids, c_vp), len(blocks), ptr(x), S, width, ptr(cos),
+                                          ptr(sin), ptr(mask), dtype, ptr(out), secs.ctypes.data, e, 512)
+        if rc < 0:
+            _raise(rc, e.value)
+        return secs
 
     def denoise(self, blocks, latent, height, width, text, text_tokens, cos, sin, mask, valid_prefix, steps,
                 start_step=0, dtype=FP16):

@@ -10,6 +10,7 @@
 #include "ernie/conditioning.h"
 #include "ernie/denoiser.h"
 #include "ernie/sha256.h"
+#include "ernie/text_encoder.h"
 
 struct ernie_device {
     ernie::Device device;
@@ -166,6 +167,55 @@ int ernie_run_block_sequence(ernie_device* device, const int* blocks, int count,
         ernie::check_status(ernie_hip_convert(d.ctx(), result.data, ERNIE_DTYPE_FP32, out, ERNIE_DTYPE_FP32,
                                               result.total()),
                             d.ctx(), "copy block output");
+        d.synchronize();
+        if (compute_seconds)
+            for (size_t i = 0; i < stats.compute_seconds.size(); ++i) compute_seconds[i] = stats.compute_seconds[i];
+        return ERNIE_OK;
+    });
+}
+
+int ernie_text_constants(const float* inverse_frequencies, int bucket, float* cos_out, float* sin_out,
+                         float* mask_out, char* err, size_t errlen)
+{
+    return guarded(err, errlen, [&] {
+        if (!inverse_frequencies || !cos_out || !sin_out || !mask_out) throw std::invalid_argument("null text constant");
+        const auto k = ernie::text_constants(std::vector<float>(inverse_frequencies, inverse_frequencies + 64), bucket);
+        std::memcpy(cos_out, k.cos.data(), k.cos.size() * sizeof(float));
+        std::memcpy(sin_out, k.sin.data(), k.sin.size() * sizeof(float));
+        std::memcpy(mask_out, k.mask.data(), k.mask.size() * sizeof(float));
+        return ERNIE_OK;
+    });
+}
+
+int ernie_text_embeddings(const uint16_t* table, size_t vocabulary, int width, const uint32_t* ids, int count,
+                          int bucket, float* out, char* err, size_t errlen)
+{
+    return guarded(err, errlen, [&] {
+        if (!ids || !out || count < 0) throw std::invalid_argument("null text embedding argument");
+        const auto rows = ernie::text_embeddings(table, vocabulary, width, std::vector<uint32_t>(ids, ids + count),
+                                                 bucket);
+        std::memcpy(out, rows.data(), rows.size() * sizeof(float));
+        return ERNIE_OK;
+    });
+}
+
+int ernie_run_text_blocks(ernie_device* device, const int* blocks, int count, const float* x, int S, int width,
+                          const float* cos_t, const float* sin_t, const float* mask, int storage_dtype, float* out,
+                          double* compute_seconds, char* err, size_t errlen)
+{
+    return guarded(err, errlen, [&]() -> int {
+        if (!device || !blocks || count < 0) throw std::invalid_argument("null text block argument");
+        std::vector<ernie::BlockModel> models;
+        for (int i = 0; i < count; ++i) models.push_back({blocks[i]});
+        std::vector<ernie::DeviceMat> constants = {wrap(cos_t, 128, S), wrap(sin_t, 128, S),
+                                                   mask ? wrap(mask, S, S) : ernie::DeviceMat{}};
+        ernie::BlockSequenceStats stats;
+        const auto& d = device->device;
+        const auto result =
+            ernie::run_text_blocks(models, wrap(x, width, S, 1, 2), constants, option_for(d, storage_dtype), stats);
+        ernie::check_status(ernie_hip_convert(d.ctx(), result.data, ERNIE_DTYPE_FP32, out, ERNIE_DTYPE_FP32,
+                                              result.total()),
+                            d.ctx(), "copy text block output");
         d.synchronize();
         if (compute_seconds)
             for (size_t i = 0; i < stats.compute_seconds.size(); ++i) compute_seconds[i] = stats.compute_seconds[i];

@@ -61,6 +61,22 @@ int ernie_denoise(ernie_device* device, const int* blocks, int count, float* lat
                   int valid_prefix, int steps, int start_step, int storage_dtype, double* step_seconds,
                   float* step_timesteps, char* err, size_t errlen);
 
+/* ---- Mistral text path (src/text_encoder.h) ------------------------------------ */
+/* text_constants (src/text_encoder.cpp:92-118) on the host from the 64 YaRN inverse
+ * frequencies: cos/sin [bucket][128], causal mask [bucket][bucket]. */
+int ernie_text_constants(const float* inverse_frequencies, int bucket, float* cos_out, float* sin_out,
+                         float* mask_out, char* err, size_t errlen);
+/* text_embeddings (src/text_encoder.cpp:68-90) from an in-memory BF16 table
+ * [vocabulary][width] -> out [bucket][width] FP32 (rows past `count` zero). */
+int ernie_text_embeddings(const uint16_t* table, size_t vocabulary, int width, const uint32_t* ids, int count,
+                          int bucket, float* out, char* err, size_t errlen);
+/* run_text_blocks (src/text_encoder.h:17-19): x [S][width] device FP32, cos/sin
+ * [S][128], mask [S][S] (device; NULL = none), blocks = resident text block slots.
+ * out [S][width] device FP32. compute_seconds (nullable) gets per-block time. */
+int ernie_run_text_blocks(ernie_device* device, const int* blocks, int count, const float* x, int S, int width,
+                          const float* cos_t, const float* sin_t, const float* mask, int storage_dtype, float* out,
+                          double* compute_seconds, char* err, size_t errlen);
+
 /* ---- on-disk blocks (block.ncnn.param + block.ncnn.bin) ----------------------- */
 typedef struct {
     int tokens, dim, ffn;         /* static token count of the graph, block widths */

@@ -95,7 +95,8 @@ int ernie_hip_set_attention_query_rows(ernie_hip_ctx* ctx, int rows);
 /* attention_internal_submissions (src/ernie_attention.cpp:256-265): always 0 here. */
 uint64_t ernie_hip_attention_internal_submissions(const ernie_hip_ctx* ctx);
 /* rmsn_9/rmsn_10 + rotary (block.ncnn.param lines 28-57) in place on `heads`
- * heads of 128 values per token at x + t*row_stride + h*128; cos/sin [rows][128]. */
+ * heads of 128 values per token at x + t*row_stride + h*128; cos/sin [rows][128].
+ * gamma NULL: rotary only (the text block's q/k path, text-s64.ncnn.param lines 18-44). */
 int ernie_hip_qk_norm_rope(ernie_hip_ctx* ctx, void* x, int dtype, int rows, int heads, long row_stride,
                            const float* gamma, const float* cos_t, const float* sin_t);
 
@@ -167,6 +168,40 @@ int ernie_hip_block_forward(ernie_hip_ctx* ctx, int index, const float* x, float
 int ernie_hip_block_sequence(ernie_hip_ctx* ctx, const int* blocks, int count, const float* x, float* out,
                              const float* mods, const float* cos_t, const float* sin_t, const float* mask,
                              int valid_keys, int S, double* seconds);
+
+/* ---- Mistral text blocks (src/text_encoder.h:14-33, tests/fixtures/text-s64.ncnn.param) ----
+ * One decoder block: RMSNorm (eps 1e-5) -> q/k/v projections -> rotary on q and k ->
+ * SDPA with grouped K/V heads and an additive mask -> o_proj + residual -> RMSNorm ->
+ * down(silu(gate) * up) + residual, head_dim 128, FP32 residual stream. */
+/* Host tensors in the .bin order of tools/build_text_weights.py:15-25 (matrices [out][in]). */
+typedef struct {
+    ernie_host_tensor norm1;   /* input_layernorm.weight [hidden] */
+    ernie_host_tensor wq;      /* self_attn.q_proj [heads*128][hidden] */
+    ernie_host_tensor wk;      /* self_attn.k_proj [kv_heads*128][hidden] */
+    ernie_host_tensor wv;      /* self_attn.v_proj [kv_heads*128][hidden] */
+    ernie_host_tensor wo;      /* self_attn.o_proj [hidden][heads*128] */
+    ernie_host_tensor norm2;   /* post_attention_layernorm.weight [hidden] */
+    ernie_host_tensor w_gate;  /* mlp.gate_proj [ffn][hidden] */
+    ernie_host_tensor w_up;    /* mlp.up_proj [ffn][hidden] */
+    ernie_host_tensor w_down;  /* mlp.down_proj [hidden][ffn] */
+} ernie_text_block_host_tensors;
+/* Replaces load_component of one text block Net (src/text_encoder.cpp:30-40); the
+ * reference's path is hidden 3072, 32 heads, 8 K/V heads, ffn 9216. */
+int ernie_hip_text_block_upload_tensors(ernie_hip_ctx* ctx, int index, const ernie_text_block_host_tensors* w,
+                                        int hidden, int heads, int kv_heads, int ffn, int dtype);
+/* Synthetic text block: matrices N(0, std), norm gammas 1 + N(0, std), from `seed`. */
+int ernie_hip_text_block_init_random(ernie_hip_ctx* ctx, int index, int hidden, int heads, int kv_heads, int ffn,
+                                     int dtype, uint64_t seed, float std_dev);
+int ernie_hip_text_block_release(ernie_hip_ctx* ctx, int index);
+/* in0 = x [S][hidden] FP32, in1/in2 = cos/sin [S][128] FP32 (text_constants),
+ * in3 = additive mask [S][S] FP32 (the causal mask; NULL = none). out0 [S][hidden]
+ * FP32; out may alias x. */
+int ernie_hip_text_block_forward(ernie_hip_ctx* ctx, int index, const float* x, float* out, const float* cos_t,
+                                 const float* sin_t, const float* mask, int S);
+/* run_text_blocks core (src/text_encoder.cpp:124-180): blocks[0..count), 1..25.
+ * seconds (nullable) receives per-block device time. */
+int ernie_hip_text_block_sequence(ernie_hip_ctx* ctx, const int* blocks, int count, const float* x, float* out,
+                                  const float* cos_t, const float* sin_t, const float* mask, int S, double* seconds);
 
 /* ---- DiT heads (heads/input, heads/output head.ncnn.param) ----------------------- */
 typedef struct {

@@ -20,6 +20,8 @@
 //   time features ...... src/denoiser.cpp:22-39
 //   schedule / Euler ... src/latent_ops.cpp:31-92
 //   DiT heads .......... artifacts/2026-09-05/components/heads/{input,output}/head.ncnn.param
+//   text block ......... tests/fixtures/text-s64.ncnn.param, tools/export_text_block.py:56-67
+//   text constants ..... src/text_encoder.cpp:92-118
 //
 // Every function is pinned by a check in tests/ (known-answer tests ported
 // from the reference probes, closed forms, invariants, or a brute-force FP64
@@ -125,6 +127,35 @@ int orc_input_head(const orc_input_head_weights* w, int dim, int latent_ch, int 
 // x [S][dim], c [dim] -> prediction [latent_ch][hw] (first hw tokens).
 int orc_output_head(const orc_output_head_weights* w, int dim, int latent_ch,
                     const float* x, int S, int hw, const float* c, float* pred, int threads);
+
+// ---- Mistral text block (tests/fixtures/text-s64.ncnn.param; tools/export_text_block.py:56-67) ----
+// x * sigmoid(x) in FP32 as x / (1 + exp(-x)) (the graph's Swish layer silu_7).
+// Pinned: FP64 closed form and torch.nn.functional.silu in tests.
+void orc_silu(const float* x, size_t n, float* out);
+// src/text_encoder.cpp:92-118: cos/sin [bucket][128] with c[j] = c[j+64] = cos(t * f_j)
+// from the 64 YaRN inverse frequencies, and the causal mask [bucket][bucket]
+// (-FLT_MAX above the diagonal, 0 elsewhere). Returns -1 for a bucket outside
+// [1,2048] or a non-finite / non-positive frequency.
+// Pinned: FP64 closed form and the mask's exact structure in tests.
+int orc_text_constants(const float* freqs64, int bucket, float* cos_out, float* sin_out, float* mask_out);
+// Weight layout of tools/build_text_weights.py:15-25 (.bin order); matrices [out][in].
+typedef struct {
+    const float* norm1;          // input_layernorm.weight [hidden]
+    const float* wq;             // q_proj [heads*128][hidden]
+    const float* wk, *wv;        // k_proj / v_proj [kv_heads*128][hidden]
+    const float* wo;             // o_proj [hidden][heads*128]
+    const float* norm2;          // post_attention_layernorm.weight [hidden]
+    const float* w_gate, *w_up;  // gate_proj / up_proj [ffn][hidden]
+    const float* w_down;         // down_proj [hidden][ffn]
+} orc_text_block_weights;
+// One decoder block: RMSNorm (eps 1e-5) -> q/k/v -> rotary on q and k -> SDPA with
+// GQA and the additive mask [S][S] (NULL = none) -> o_proj + residual -> RMSNorm ->
+// down(silu(gate) * up) + residual. out may alias x.
+// Pinned: composition of pinned operators + a PyTorch FP64 restatement of
+// tools/export_text_block.py:56-67 in tests.
+int orc_text_block_forward(const orc_text_block_weights* w, int hidden, int heads, int kv_heads, int ffn,
+                           const float* x, const float* cos_t, const float* sin_t, const float* mask, int S,
+                           float* out, int precise_attention, int threads);
 
 #ifdef __cplusplus
 }

@@ -51,8 +51,12 @@ def lib():
                                      _f32p, ctypes.c_int, _f32p, _f32p, _f32p, _f32p, ctypes.c_int]
         L.orc_output_head.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, _f32p, ctypes.c_int, ctypes.c_int,
                                       _f32p, _f32p, ctypes.c_int]
+        L.orc_silu.argtypes = [_f32p, ctypes.c_size_t, _f32p]
+        L.orc_text_constants.argtypes = [_f32p, ctypes.c_int, _f32p, _f32p, _f32p]
+        L.orc_text_block_forward.argtypes = [ctypes.c_void_p] + [ctypes.c_int] * 4 + [_f32p] * 4 + [
+            ctypes.c_int, _f32p, ctypes.c_int, ctypes.c_int]
         for name in ("orc_timestep_features", "orc_flow_schedule_turbo", "orc_dit_constants", "orc_block_forward",
-                     "orc_input_head", "orc_output_head"):
+                     "orc_input_head", "orc_output_head", "orc_text_constants", "orc_text_block_forward"):
             getattr(L, name).restype = ctypes.c_int
     return _lib
 
@@ -249,3 +253,43 @@ def output_head(weights, x, c, hw, threads=0):
     if rc:
         raise ValueError("output_head rejected its arguments")
     return pred
+
+
+def silu(x):
+    x = f32(x)
+    out = np.empty_like(x)
+    lib().orc_silu(_p(x), x.size, _p(out))
+    return out
+
+
+def text_constants(freqs, bucket):
+    """64 YaRN inverse frequencies -> cos, sin [bucket][128], causal mask [bucket][bucket]."""
+    cos = np.empty((bucket, 128), np.float32)
+    sin = np.empty((bucket, 128), np.float32)
+    mask = np.empty((bucket, bucket), np.float32)
+    if lib().orc_text_constants(_p(f32(freqs)), bucket, _p(cos), _p(sin), _p(mask)):
+        raise ValueError("text_constants rejected its arguments")
+    return cos, sin, mask
+
+
+TEXT_FIELDS = ("norm1", "wq", "wk", "wv", "wo", "norm2", "w_gate", "w_up", "w_down")
+
+
+class _TextWeights(ctypes.Structure):
+    _fields_ = [(n, _f32p) for n in TEXT_FIELDS]
+
+
+def text_block_forward(weights, x, cos, sin, mask, heads, kv_heads, precise=True, threads=0):
+    """weights: dict with TEXT_FIELDS (FP32, [out][in] for matrices); mask [S][S] or None."""
+    keep = {n: f32(weights[n]) for n in TEXT_FIELDS}
+    st = _TextWeights(*[_p(keep[n]) for n in TEXT_FIELDS])
+    x = f32(x)
+    S, hidden = x.shape
+    ffn = keep["w_up"].shape[0]
+    out = np.empty_like(x)
+    rc = lib().orc_text_block_forward(ctypes.byref(st), hidden, heads, kv_heads, ffn, _p(x), _p(f32(cos)),
+                                      _p(f32(sin)), None if mask is None else _p(f32(mask)), S, _p(out),
+                                      1 if precise else 0, threads)
+    if rc:
+        raise ValueError("text_block_forward rejected its arguments")
+    return out

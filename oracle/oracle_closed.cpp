@@ -6,6 +6,7 @@
 #include "oracle.h"
 
 #include <cmath>
+#include <limits>
 #include <cstdint>
 
 namespace {
@@ -127,4 +128,24 @@ extern "C" void orc_modulate(float* h, const float* shift, const float* scale, i
             row[i] = scaled + shift[i];
         }
     }
+}
+
+// src/text_encoder.cpp:92-118 (float phase = t * f_j; std::cos / std::sin in FP32).
+extern "C" int orc_text_constants(const float* freqs64, int bucket, float* cos_out, float* sin_out, float* mask_out)
+{
+    if (bucket < 1 || bucket > 2048) return -1;
+    for (int j = 0; j < 64; ++j)
+        if (!std::isfinite(freqs64[j]) || freqs64[j] <= 0.f) return -1;
+    for (int t = 0; t < bucket; ++t) {
+        float* c = cos_out + (size_t)t * 128;
+        float* s = sin_out + (size_t)t * 128;
+        for (int j = 0; j < 64; ++j) {
+            const float phase = float(t) * freqs64[j];
+            c[j] = c[j + 64] = std::cos(phase);
+            s[j] = s[j + 64] = std::sin(phase);
+        }
+        float* m = mask_out + (size_t)t * bucket;
+        for (int k = 0; k < bucket; ++k) m[k] = k > t ? -std::numeric_limits<float>::max() : 0.f;
+    }
+    return 0;
 }

@@ -365,3 +365,41 @@ extern "C" int orc_output_head(const orc_output_head_weights* w, int dim, int la
         for (int ch = 0; ch < latent_ch; ++ch) pred[(size_t)ch * hw + t] = proj[(size_t)t * latent_ch + ch];
     return 0;
 }
+
+extern "C" void orc_silu(const float* x, size_t n, float* out)
+{
+    for (size_t i = 0; i < n; ++i) out[i] = x[i] / (1.0f + std::exp(-x[i]));
+}
+
+// tests/fixtures/text-s64.ncnn.param: rmsn_8 -> gemm_0/1/2 -> rotary (Slice/BinaryOp
+// lines 18-44) -> sdpa_20 (GQA, mask in3) -> gemm_3 -> add_12 -> rmsn_9 -> gemm_4
+// (gate) -> silu_7, gemm_5 (up), mul_13 -> gemm_6 -> add_14.
+extern "C" int orc_text_block_forward(const orc_text_block_weights* w, int hidden, int heads, int kv_heads, int ffn,
+                                      const float* x, const float* cos_t, const float* sin_t, const float* mask,
+                                      int S, float* out, int precise_attention, int threads)
+{
+    if (!w || hidden <= 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads || ffn <= 0 || S < 1) return -1;
+    const int qd = heads * 128, kvd = kv_heads * 128;
+    const size_t SH = (size_t)S * hidden, SF = (size_t)S * ffn;
+    std::vector<float> h(SH), q((size_t)S * qd), k((size_t)S * kvd), v((size_t)S * kvd), attn((size_t)S * qd),
+        x1(SH);
+    orc_rmsnorm(x, w->norm1, S, hidden, 1e-5f, h.data());
+    orc_gemm_nt(h.data(), w->wq, nullptr, S, qd, hidden, q.data(), threads);
+    orc_gemm_nt(h.data(), w->wk, nullptr, S, kvd, hidden, k.data(), threads);
+    orc_gemm_nt(h.data(), w->wv, nullptr, S, kvd, hidden, v.data(), threads);
+    for (int hh = 0; hh < heads; ++hh) orc_rope_rows(q.data() + hh * 128, cos_t, sin_t, S, qd, 128);
+    for (int hh = 0; hh < kv_heads; ++hh) orc_rope_rows(k.data() + hh * 128, cos_t, sin_t, S, kvd, 128);
+    orc_sdpa(q.data(), k.data(), v.data(), attn.data(), heads, kv_heads, S, S, 128, 128, qd, 128, kvd, 128, qd, mask,
+             1, mask ? S : 1, 1.0f / std::sqrt(128.0f), 0, S, precise_attention, threads);
+    orc_gemm_nt(attn.data(), w->wo, nullptr, S, hidden, qd, h.data(), threads);
+    for (size_t i = 0; i < SH; ++i) x1[i] = x[i] + h[i];
+    orc_rmsnorm(x1.data(), w->norm2, S, hidden, 1e-5f, h.data());
+    std::vector<float> gate(SF), up(SF);
+    orc_gemm_nt(h.data(), w->w_gate, nullptr, S, ffn, hidden, gate.data(), threads);
+    orc_gemm_nt(h.data(), w->w_up, nullptr, S, ffn, hidden, up.data(), threads);
+    orc_silu(gate.data(), SF, gate.data());
+    for (size_t i = 0; i < SF; ++i) up[i] = gate[i] * up[i];
+    orc_gemm_nt(up.data(), w->w_down, nullptr, S, hidden, ffn, h.data(), threads);
+    for (size_t i = 0; i < SH; ++i) out[i] = x1[i] + h[i];
+    return 0;
+}

@@ -14,6 +14,8 @@ import numpy as np
 BLOCK_GATES = {"fp32": (2e-4, 2e-4, 2e-5), "fp16": (0.02, 0.02, 0.01), "bf16": (0.15, 0.08, 0.03)}
 SEQUENCE_GATES = {"fp32": (2e-4, 2e-4, 2e-4), "fp16": (0.03, 0.03, 0.03), "bf16": (0.2, 0.2, 0.12)}
 HEAD_GATES = {"fp32": (2e-4, 2e-4, 2e-5), "fp16": (0.03, 0.03, 0.02), "bf16": (0.2, 0.2, 0.1)}
+# tools/validate_text.py:53-54: text block / text stack gates as (atol, rtol, nrmse).
+TEXT_GATES = {"fp32": (2e-4, 2e-4, 2e-4), "fp16": (0.03, 0.03, 0.03), "bf16": (0.2, 0.2, 0.15)}
 # tools/validate_denoiser.py:53-55 as (nrmse, global_rtol, atol); the reference has no BF16 denoiser gate.
 DENOISER_GATES = {"fp32": (0.002, 0.002, 0.0002), "fp16": (0.1, 0.1, 0.03)}
 
@@ -181,3 +183,46 @@ def residual_case():
     a = (np.where(i % 2 == 1, -1.0, 1.0) * (70000.0 + y * 128.0)).astype(np.float32)
     b = ((i % 8) * 128.0 + 0 * y).astype(np.float32)
     return a, b
+
+
+# ---- probes/attention_probe.cpp:20-112: causal GQA attention ----------------------
+# 32 query heads over 8 key/value heads, head_dim 128; inputs are a hash of
+# (head, position, dim, seed) in [-1, 1); the mask is 0 for visible keys and
+# -1e30 past the query's position; the expectation is an FP64 softmax over
+# exactly the visible keys. Operator gates (max abs, nrmse) from suite(), lines 321-323.
+GQA_PROBE_LIMITS = {"fp32": (2e-5, 2e-5), "fp16": (0.002, 0.005), "bf16": (0.015, 0.03)}
+
+
+def gqa_sample(heads, length, start, seed, head_dim=128):
+    h = np.arange(heads, dtype=np.uint64)[:, None, None]
+    p = np.arange(start, start + length, dtype=np.uint64)[None, :, None]
+    d = np.arange(head_dim, dtype=np.uint64)[None, None, :]
+    m = np.uint64(0xFFFFFFFF)
+    x = (np.uint64(seed) ^ ((h + 1) * np.uint64(0x9E3779B9) & m) ^ ((p + 1) * np.uint64(0x85EBCA6B) & m)
+         ^ ((d + 1) * np.uint64(0xC2B2AE35) & m)) & m
+    x ^= x >> np.uint64(16)
+    x = (x * np.uint64(0x7FEB352D)) & m
+    x ^= x >> np.uint64(15)
+    return (((x & np.uint64(65535)).astype(np.int64) - 32768) / 32768.0).astype(np.float32)
+
+
+def gqa_causal_case(length, seed, q_heads=32, kv_heads=8):
+    q = gqa_sample(q_heads, length, 0, seed)
+    k = gqa_sample(kv_heads, length, 0, seed + 1)
+    v = gqa_sample(kv_heads, length, 0, seed + 2)
+    pos = np.arange(length)
+    mask = np.where(pos[None, :] <= pos[:, None], 0.0, -1e30).astype(np.float32)
+    return q, k, v, mask
+
+
+def gqa_causal_expected(q, k, v):
+    q_heads, length, width = q.shape
+    group = q_heads // k.shape[0]
+    out = np.empty(q.shape, np.float64)
+    for h in range(q_heads):
+        kh, vh = k[h // group].astype(np.float64), v[h // group].astype(np.float64)
+        for p in range(length):
+            s = kh[:p + 1] @ q[h, p].astype(np.float64) / math.sqrt(width)
+            w = np.exp(s - s.max())
+            out[h, p] = (w @ vh[:p + 1]) / w.sum()
+    return out
