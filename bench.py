@@ -48,6 +48,10 @@ def parse():
     ap.add_argument("--events", choices=("dominant", "all"), default="dominant",
                     help="HIP events in the timed steps: around the dominant kernel class only (its roofline), or "
                          "around every launch; the per-class table always comes from one extra profiled step")
+    ap.add_argument("--workload", choices=("denoise", "text"), default="denoise",
+                    help="denoise: the headline DiT denoise (default); text: one Mistral text prefill, 25 blocks "
+                         "(hidden 3072, 32 heads over 8 K/V heads, ffn 9216) at --text-bucket tokens, causal")
+    ap.add_argument("--text-bucket", type=int, default=2048)
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run a plain FP32 copy kernel of this many MiB three times (the reference "
                          "dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
@@ -80,12 +84,96 @@ def cpu_baseline(tokens):
             "block_seconds": block_s}
 
 
+def text_cpu_baseline(bucket, threads):
+    """One FP32 text block of the oracle at the bucket, extrapolated to 25 blocks."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import numpy as np
+    import oracle as O
+    shapes = {"norm1": (3072,), "wq": (4096, 3072), "wk": (1024, 3072), "wv": (1024, 3072), "wo": (3072, 4096),
+              "norm2": (3072,), "w_gate": (9216, 3072), "w_up": (9216, 3072), "w_down": (3072, 9216)}
+    w = {n: O.normal(shapes[n], 40, offset=i << 40, mean=1.0 if n.startswith("norm") else 0.0, std=0.02)
+         for i, n in enumerate(O.TEXT_FIELDS)}
+    freqs = (1.0 / (1e6 ** (np.arange(0, 128, 2) / 128.0))).astype(np.float32)
+    cos, sin, mask = O.text_constants(freqs, bucket)
+    x = O.normal((bucket, 3072), 41, std=0.2)
+    t0 = time.perf_counter()
+    O.text_block_forward(w, x, cos, sin, mask, 32, 8, precise=False, threads=threads)
+    block_s = time.perf_counter() - t0
+    return {"value": 1.0 / (25.0 * block_s), "unit": "prefills/s", "cores": threads, "kind": "port",
+            "sample": f"1 FP32 Mistral text block (hidden 3072, 32/8 heads, ffn 9216, S={bucket}) of the C++ "
+                      f"oracle, {block_s:.2f} s, extrapolated x25 blocks", "block_seconds": block_s}
+
+
+def text_main(args):
+    """Mistral text prefill: 25 resident text blocks on one bucket of tokens."""
+    import torch
+    import ernie_amd as E
+    dt = {"fp16": E.FP16, "bf16": E.BF16, "fp32": E.FP32}[args.precision]
+    S, H = args.text_bucket, 3072
+    ctx = E.Context(0)
+    blocks = list(range(25))
+    for b in blocks:
+        ctx.text_block_init_random(b, H, 32, 8, 9216, dt, seed=2000 + b, std=0.02)
+    freqs = (1.0 / (1e6 ** (__import__("numpy").arange(0, 128, 2) / 128.0))).astype("float32")
+    cos, sin, mask = E.text_constants(freqs, S)
+    cd, sd, md = (torch.from_numpy(a).cuda() for a in (cos, sin, mask))
+    x = torch.empty((S, H), dtype=torch.float32, device="cuda")
+    ctx.fill_normal(x, E.FP32, x.numel(), seed=41, std=0.2)
+    out = torch.empty_like(x)
+    # The causal mask text_constants builds is applied by position (the facade's path).
+    for _ in range(max(args.warmup, 1)):
+        ctx.text_block_sequence(blocks, x, out, cd, sd, S, causal=True)
+    torch.cuda.synchronize()
+    ctx.profile_reset()
+    ctx.profile(True)
+    ctx.text_block_sequence(blocks, x, out, cd, sd, S, causal=True)
+    ctx.profile(False)
+    table = ctx.profile_query()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ctx.text_block_sequence(blocks, x, out, cd, sd, S, causal=True)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    mfma_cls = ("gemm_qkv", "sdpa", "gemm_out", "gemm_up_gate", "gemm_down")
+    dom = max(mfma_cls, key=lambda c: table[c]["ms"])
+    d = table[dom]
+    avg_s = d["ms"] / max(d["launches"], 1) * 1e-3
+    flop = d["flop"] / max(d["launches"], 1)
+    peak = PEAK[args.precision]
+    result = {
+        "metric": f"Mistral text prefill/s (25 blocks, {S} tokens, causal)", "value": args.steps / elapsed,
+        "unit": "prefills/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": elapsed / args.steps * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": args.precision, "data": "synthetic",
+        "config": {"workload": f"Mistral text encoder prefill: 25 blocks, hidden 3072, 32 heads over 8 K/V heads, "
+                               f"ffn 9216 SiLU-gated, {S} tokens, causal mask, {args.precision} storage / fp32 "
+                               f"accumulate", "tokens": S, "blocks": 25},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": flop / avg_s / 1e12, "peak": peak / 1e12,
+                     "unit": "TFLOP/s", "frac": flop / avg_s / peak, "traffic": None, "flop_per_launch": flop,
+                     "avg_launch_us": avg_s * 1e6},
+        "kernels": {c: {"launches": table[c]["launches"],
+                        "avg_us": table[c]["ms"] * 1e3 / max(table[c]["launches"], 1),
+                        "tflops": (table[c]["flop"] / (table[c]["ms"] * 1e-3) / 1e12) if table[c]["ms"] and
+                        table[c]["flop"] else None} for c in E.PROFILE_CLASSES if table[c]["launches"]},
+    }
+    if args.cpu_baseline == "on":
+        print("bench: text cpu baseline ...", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = text_cpu_baseline(S, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    ctx.close()
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the DiT block path runs on a single device "
               "(multi-GPU sharding is a design note, not part of this build)", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "text":
+        return text_main(args)
     import numpy as np
     import torch
     import ernie_amd as E

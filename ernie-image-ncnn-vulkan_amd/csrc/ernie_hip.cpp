@@ -507,7 +507,7 @@ int ones_buffer(ernie_hip_ctx* ctx, int n, const float** out)
 // The residual adds are the GEMM epilogues with a unit gate; the gated MLP is one GEMM
 // over the interleaved up/gate rows with a SiLU epilogue. out may alias x.
 int text_block_forward(ernie_hip_ctx* ctx, const TextBlockWeights& w, const float* x, float* out, const float* cos_t,
-                       const float* sin_t, const float* mask, int S)
+                       const float* sin_t, const float* mask, int causal, int S)
 {
     const int H = w.hidden, F = w.ffn, nq = w.heads, nk = w.kv_heads, dt = w.dtype;
     const int QD = nq * 128, KVD = nk * 128, QKV = QD + 2 * KVD;
@@ -557,8 +557,9 @@ int text_block_forward(ernie_hip_ctx* ctx, const TextBlockWeights& w, const floa
         a.o = attn; a.dtype = dt; a.heads = nq; a.kv_heads = nk; a.sq = S; a.sk = S; a.d = kHeadDim;
         a.q_hs = a.k_hs = a.v_hs = kHeadDim; a.q_rs = a.k_rs = a.v_rs = QKV;
         a.o_hs = kHeadDim; a.o_rs = QD;
-        a.mask = mask; a.mask_heads = 1; a.mask_rows = mask ? S : 1;
+        a.mask = mask; a.mask_heads = 1; a.mask_rows = mask ? S : 1; a.causal = causal;
         a.split_ws = split_ws; a.split_ws_bytes = split_ws_bytes;
+        // All-key FLOP (the causal launch skips about half of them).
         Timed t(ctx, P_SDPA, 4.0 * dS * dS * kHeadDim * nq, dS * (2 * QD + 2 * KVD) * e);
         rc = kernel_status(ctx, sdpa(a, s), "text sdpa");
         if (rc) return rc;
@@ -873,6 +874,18 @@ int ernie_hip_sdpa(ernie_hip_ctx* ctx, const void* q, const void* k, const void*
     a.v_hs = v_hs; a.v_rs = v_rs; a.o_hs = o_hs; a.o_rs = o_rs; a.mask = mask; a.mask_heads = mask_heads;
     a.mask_rows = mask_rows; a.valid_keys = valid_keys; a.scale = scale;
     return kernel_status(ctx, sdpa(a, ctx->stream), "sdpa");
+}
+
+int ernie_hip_sdpa_causal(ernie_hip_ctx* ctx, const void* q, const void* k, const void* v, void* out, int dtype,
+                          int heads, int kv_heads, int sq, int sk, int d, long q_hs, long q_rs, long k_hs, long k_rs,
+                          long v_hs, long v_rs, long o_hs, long o_rs, float scale)
+{
+    if (!ctx) return ERNIE_ERROR;
+    SdpaArgs a;
+    a.q = q; a.k = k; a.v = v; a.o = out; a.dtype = dtype; a.heads = heads; a.kv_heads = kv_heads;
+    a.sq = sq; a.sk = sk; a.d = d; a.q_hs = q_hs; a.q_rs = q_rs; a.k_hs = k_hs; a.k_rs = k_rs;
+    a.v_hs = v_hs; a.v_rs = v_rs; a.o_hs = o_hs; a.o_rs = o_rs; a.causal = 1; a.scale = scale;
+    return kernel_status(ctx, sdpa(a, ctx->stream), "sdpa causal");
 }
 
 int ernie_hip_set_attention_query_rows(ernie_hip_ctx* ctx, int rows)
@@ -1194,16 +1207,17 @@ int ernie_hip_text_block_release(ernie_hip_ctx* ctx, int index)
 }
 
 int ernie_hip_text_block_forward(ernie_hip_ctx* ctx, int index, const float* x, float* out, const float* cos_t,
-                                 const float* sin_t, const float* mask, int S)
+                                 const float* sin_t, const float* mask, int causal, int S)
 {
     if (!ctx) return ERNIE_ERROR;
     const int rc = check_text_call(ctx, index, S, x, out, cos_t, sin_t);
     if (rc) return rc;
-    return text_block_forward(ctx, ctx->text_blocks[index], x, out, cos_t, sin_t, mask, S);
+    return text_block_forward(ctx, ctx->text_blocks[index], x, out, cos_t, sin_t, mask, causal, S);
 }
 
 int ernie_hip_text_block_sequence(ernie_hip_ctx* ctx, const int* blocks, int count, const float* x, float* out,
-                                  const float* cos_t, const float* sin_t, const float* mask, int S, double* seconds)
+                                  const float* cos_t, const float* sin_t, const float* mask, int causal, int S,
+                                  double* seconds)
 {
     if (!ctx || !blocks) return ERNIE_ERROR;
     if (count < 1 || count > 25) return fail(ctx, ERNIE_ERROR, "Text path requires 1..25 blocks");
@@ -1226,7 +1240,8 @@ int ernie_hip_text_block_sequence(ernie_hip_ctx* ctx, const int* blocks, int cou
     int rc = ERNIE_OK;
     for (int i = 0; i < count && !rc; ++i) {
         if (seconds) (void)hipEventRecord(ev[i], ctx->stream);
-        rc = text_block_forward(ctx, ctx->text_blocks[blocks[i]], i == 0 ? x : out, out, cos_t, sin_t, mask, S);
+        rc = text_block_forward(ctx, ctx->text_blocks[blocks[i]], i == 0 ? x : out, out, cos_t, sin_t, mask, causal,
+                                S);
     }
     if (seconds) {
         if (!rc) {

@@ -430,8 +430,9 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     p.n_tiles = (a.N + pingpong::BN - 1) / pingpong::BN;
     // Split the tail row of tiles along K so that its items cover the CUs once
     // (at most 16 parts, at least 4 K steps each), within the caller's workspace.
+    // With M < 256 the tail row is the whole GEMM (a short prompt's projections).
     p.split = 1;
-    if (p.tail_sub && p.m_full && a.split_ws) {
+    if (p.tail_sub && a.split_ws) {
         const size_t per_part = (size_t)p.n_tiles * 64 * p.tail_sub * pingpong::BN * sizeof(float);
         int sp = std::min(16, std::max(1, kSplitTargetItems / p.n_tiles));
         sp = std::min(sp, std::max(1, a.K / pingpong::BK / 4));

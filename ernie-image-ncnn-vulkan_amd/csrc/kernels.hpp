@@ -68,6 +68,10 @@ struct SdpaArgs {
     const float* mask = nullptr;  // additive [mask_heads][mask_rows][sk]; mask_rows 1 or sq
     int mask_heads = 1, mask_rows = 1;
     int valid_keys = 0;           // keys >= valid_keys are excluded (0 = sk)
+    // Causal: key k is visible to query q only if k <= q + (sk - sq) (the text encoder's
+    // prefill mask, src/text_encoder.cpp:115-116, without reading a mask tensor). Key
+    // tiles wholly above the diagonal are skipped by the head_dim-128 16-bit kernel.
+    int causal = 0;
     float scale = 0.f;
     // Optional FP32 scratch for splitting a partial last query tile along the keys
     // (merged by a second launch on the same stream); calls that run concurrently

@@ -33,6 +33,7 @@ constexpr int VT_STRIDE = BKV + 8;  // halves, transposed V row (one d)
 struct SdpaParams {
     const void* q; const void* k; const void* v; void* o;
     int heads, group, sq, sk, d, kv_end;
+    int causal, qk_off;  // causal: keys > query + qk_off (= sk - sq) excluded
     long q_hs, q_rs, k_hs, k_rs, v_hs, v_rs, o_hs, o_rs;
     const float* mask; long mask_hs; long mask_rs;
     float scale_log2;
@@ -173,6 +174,8 @@ __global__ void __launch_bounds__(256, 2) sdpa16_kernel(SdpaParams p)
                              ? p.mask + (size_t)h * p.mask_hs + (size_t)min(my_q, p.sq - 1) * p.mask_rs
                              : nullptr;
     constexpr bool MASK = MM != MASK_NONE;
+    // Keys at or past lim are excluded: the valid-key bound, and the diagonal when causal.
+    const int lim = p.causal ? min(p.kv_end, my_q + 1 + p.qk_off) : p.kv_end;
 
     const int ntiles = (p.kv_end + BKV - 1) / BKV;
     load_global(0);
@@ -197,7 +200,7 @@ __global__ void __launch_bounds__(256, 2) sdpa16_kernel(SdpaParams p)
             }
         }
         // Scores in log2 units: s * c (+ mask * log2 e); keys >= kv_end excluded.
-        const bool partial = kv0 + BKV > p.kv_end;
+        const bool partial = kv0 + BKV > p.kv_end || p.causal;
         if (MASK || partial) {
 #pragma unroll
             for (int t = 0; t < 2; ++t)
@@ -207,7 +210,7 @@ __global__ void __launch_bounds__(256, 2) sdpa16_kernel(SdpaParams p)
                     float v = sacc[t][r] * c;
                     if constexpr (MM == MASK_ROW) v += Ms[buf][kk];
                     if constexpr (MM == MASK_PER_QUERY) v += (kv0 + kk < p.sk ? qmask[kv0 + kk] : 0.f) * kLog2e;
-                    sacc[t][r] = kv0 + kk < p.kv_end ? v : -INFINITY;
+                    sacc[t][r] = kv0 + kk < lim ? v : -INFINITY;
                 }
         }
         float tmax = -INFINITY;
@@ -359,6 +362,7 @@ __global__ void __launch_bounds__(256) sdpa32_kernel(SdpaParams p)
     float m_run = -INFINITY;
     double l_run = 0.0;
     const float* mrow = p.mask ? p.mask + (size_t)h * p.mask_hs + (size_t)min(my_q, p.sq - 1) * p.mask_rs : nullptr;
+    const int lim = p.causal ? min(p.kv_end, my_q + 1 + p.qk_off) : p.kv_end;
 
     const int ntiles = (p.kv_end + BKV - 1) / BKV;
     load_global(0);
@@ -390,7 +394,7 @@ __global__ void __launch_bounds__(256) sdpa32_kernel(SdpaParams p)
                 const int key = kv0 + 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
                 float s = sacc[t][r] * p.scale_log2;
                 if (mrow) s += (key < p.sk ? mrow[key] : 0.f) * kLog2e;
-                s = key < p.kv_end ? s : -INFINITY;
+                s = key < lim ? s : -INFINITY;
                 sacc[t][r] = s;
                 tmax = fmaxf(tmax, s);
             }
@@ -454,10 +458,12 @@ int sdpa(const SdpaArgs& a, hipStream_t s)
     if (a.mask && a.mask_heads != 1 && a.mask_heads != a.heads) return -1;
     const int kv_end = a.valid_keys > 0 ? a.valid_keys : a.sk;
     if (kv_end > a.sk) return -1;
+    if (a.causal && a.sq > a.sk) return -1;  // every query must see at least key 0
     if (a.o_ds != 0 && a.o_ds != 32 && (a.dtype == DT_F32 || a.d != 128 || a.o_ds % 8)) return -1;
     SdpaParams p{};
     p.q = a.q; p.k = a.k; p.v = a.v; p.o = a.o;
     p.heads = a.heads; p.group = a.heads / a.kv_heads; p.sq = a.sq; p.sk = a.sk; p.d = a.d; p.kv_end = kv_end;
+    p.causal = a.causal ? 1 : 0; p.qk_off = a.sk - a.sq;
     p.q_hs = a.q_hs; p.q_rs = a.q_rs; p.k_hs = a.k_hs; p.k_rs = a.k_rs;
     p.v_hs = a.v_hs; p.v_rs = a.v_rs; p.o_hs = a.o_hs; p.o_rs = a.o_rs;
     p.mask = a.mask;

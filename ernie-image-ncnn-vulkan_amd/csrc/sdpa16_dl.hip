@@ -30,6 +30,9 @@
 //   * K rows are chunk-swizzled by (key & 15), V rows by 2 (key & 7) (32-byte
 //     pairs kept together for the transposing reads): both measured conflict-free
 //     for these read patterns.
+//   * Causal mode (key k visible to query q iff k <= q + sk - sq): a workgroup's
+//     key loop ends at the tile holding its last query's diagonal, and only tiles
+//     that cross a wave's diagonal are masked, per lane, without a mask tensor.
 //   * Online softmax in the log2 domain; the running offset is raised only when a
 //     tile's maximum exceeds it by more than 8, so the O / l rescale is almost
 //     always skipped (exact: O and l share the offset).
@@ -60,6 +63,7 @@ struct Params {
     long o_ds;  // element distance between the four 32-value groups of an output row
     const float* mask; long mask_hs;  // additive FP32 mask: one row [sk] or per query [sq][sk] per head
     float scale_log2;
+    int causal, qk_off;  // causal: keys > query + qk_off (= sk - sq) excluded
     // Split of the last, partial query tile (sq % 128 queries) along the keys:
     // tail_parts > 0 parts per head write unnormalised FP32 O and their (m, l) to
     // part_o [heads * tail_parts][128][128] / part_ml [heads * tail_parts][128][2].
@@ -205,8 +209,13 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
             h = u / p.tail_parts;
             part = u - h * p.tail_parts;
             q_base = p.full_qt * BQ;
-            it0 = (int)((long)ntiles * part / p.tail_parts);
-            it1 = (int)((long)ntiles * (part + 1) / p.tail_parts);
+        }
+        // Causal: no key tile past the one holding the last query's diagonal.
+        const int nt = p.causal ? min(ntiles, (min(q_base + BQ, p.sq) - 1 + p.qk_off) / BKV + 1) : ntiles;
+        it1 = nt;
+        if (part >= 0) {
+            it0 = (int)((long)nt * part / p.tail_parts);
+            it1 = (int)((long)nt * (part + 1) / p.tail_parts);
         }
     }
     const int kvh = h / p.group;
@@ -214,6 +223,8 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lrow = lane & 31, g = lane >> 5;
     const int my_q = q_base + wave * 32 + lrow;
+    // Keys at or past key_lim are excluded: the valid-key bound, and the diagonal when causal.
+    const int key_lim = p.causal ? min(p.kv_end, my_q + 1 + p.qk_off) : p.kv_end;
 
     const T* Q = static_cast<const T*>(p.q) + (size_t)h * p.q_hs;
     vec8 qf[8];
@@ -338,14 +349,16 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
     // the softmax applies to the scores: 1 when they were scaled here, else c.
     auto prep = [&](f32x16 (&sacc)[2], int it) -> float {
         const int kv0 = it * BKV;
-        const bool scaled = MM != MASK_NONE || kv0 + BKV > p.kv_end;
+        // Masked per lane: past the valid keys, or (causal) across this wave's diagonal.
+        const bool scaled = MM != MASK_NONE || kv0 + BKV > p.kv_end ||
+                            (p.causal && kv0 + BKV - 1 > q_base + wave * 32 + p.qk_off);
         if (scaled) {
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int kk = 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
-                    sacc[t][r] = kv0 + kk < p.kv_end ? sacc[t][r] * c : -INFINITY;
+                    sacc[t][r] = kv0 + kk < key_lim ? sacc[t][r] * c : -INFINITY;
                 }
         }
         float tmax = max3(sacc[0][0], sacc[0][1], sacc[0][2]);
@@ -510,6 +523,7 @@ int sdpa16_d128(const SdpaArgs& a, hipStream_t s)
     p.heads = a.heads; p.group = a.heads / a.kv_heads; p.sq = a.sq; p.sk = a.sk; p.kv_end = kv_end;
     p.q_hs = a.q_hs; p.q_rs = a.q_rs; p.k_hs = a.k_hs; p.k_rs = a.k_rs;
     p.v_hs = a.v_hs; p.v_rs = a.v_rs; p.o_hs = a.o_hs; p.o_rs = a.o_rs;
+    p.causal = a.causal ? 1 : 0; p.qk_off = a.sk - a.sq;
     p.o_ds = a.o_ds ? a.o_ds : 32;
     p.mask = a.mask;
     const bool dense = a.mask && a.mask_rows > 1;

@@ -106,8 +106,11 @@ def hip():
             "ernie_hip_text_block_init_random": (c_int, [c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_u64,
                                                          c_float]),
             "ernie_hip_text_block_release": (c_int, [c_vp, c_int]),
-            "ernie_hip_text_block_forward": (c_int, [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int]),
-            "ernie_hip_text_block_sequence": (c_int, [c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_vp]),
+            "ernie_hip_text_block_forward": (c_int, [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int]),
+            "ernie_hip_text_block_sequence": (c_int, [c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int,
+                                                      c_vp]),
+            "ernie_hip_sdpa_causal": (c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int] +
+                                      [c_long] * 8 + [c_float]),
             "ernie_hip_heads_upload": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int]),
             "ernie_hip_heads_init_random": (c_int, [c_vp, c_int, c_int, c_int, c_int, c_u64, c_float]),
             "ernie_hip_input_head": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_vp]),
@@ -180,8 +183,8 @@ def facade():
                                       c_int, c_int, c_int, c_vp, c_vp, cp, c_size_t]),
             "ernie_text_constants": (c_int, [c_vp, c_int, c_vp, c_vp, c_vp, cp, c_size_t]),
             "ernie_text_embeddings": (c_int, [c_vp, c_size_t, c_int, c_vp, c_int, c_int, c_vp, cp, c_size_t]),
-            "ernie_run_text_blocks": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_int, c_vp, c_vp, c_vp, c_int, c_vp,
-                                              c_vp, cp, c_size_t]),
+            "ernie_run_text_blocks": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_int, c_vp, c_vp, c_vp, c_int, c_int,
+                                              c_vp, c_vp, cp, c_size_t]),
             "ernie_sha256_hex": (c_int, [c_vp, c_size_t, cp]),
             "ernie_block_file_inspect": (c_int, [cp, cp, c_int, cp, ctypes.POINTER(BlockFileInfo), cp, c_size_t]),
             "ernie_block_load": (c_int, [c_vp, c_int, cp, cp, c_int, c_int, cp, ctypes.POINTER(BlockFileInfo), cp,
@@ -445,16 +448,19 @@ class Context:
     def text_block_init_random(self, index, hidden, heads, kv_heads, ffn, dtype, seed, std=0.02):
         self.call("text_block_init_random", index, hidden, heads, kv_heads, ffn, dtype, seed, std)
 
-    def text_block_forward(self, index, x, out, cos, sin, S, mask=None):
-        self.call("text_block_forward", index, ptr(x), ptr(out), ptr(cos), ptr(sin), ptr(mask), S)
+    def text_block_forward(self, index, x, out, cos, sin, S, mask=None, causal=False):
+        self.call("text_block_forward", index, ptr(x), ptr(out), ptr(cos), ptr(sin), ptr(mask), 1 if causal else 0, S)
 
-    def text_block_sequence(self, blocks, x, out, cos, sin, S, mask=None, timing=False):
+    def text_block_sequence(self, blocks, x, out, cos, sin, S, mask=None, causal=False, timing=False):
         import numpy as np
         ids = (c_int * len(blocks))(*blocks)
         secs = np.zeros(len(blocks), np.float64) if timing else None
         self.call("text_block_sequence", ctypes.cast(ids, c_vp), len(blocks), ptr(x), ptr(out), ptr(cos), ptr(sin),
-                  ptr(mask), S, secs.ctypes.data if timing else None)
+                  ptr(mask), 1 if causal else 0, S, secs.ctypes.data if timing else None)
         return secs
+
+    def sdpa_causal(self, q, k, v, out, dtype, heads, kv_heads, sq, sk, d, strides, scale=0.0):
+        self.call("sdpa_causal", ptr(q), ptr(k), ptr(v), ptr(out), dtype, heads, kv_heads, sq, sk, d, *strides, scale)
 
     def heads_upload(self, weights, dim, latent_ch, text_dim, dtype):
         import numpy as np
@@ -551,13 +557,14 @@ class Facade:
             _raise(rc, e.value)
         return info.as_dict()
 
-    def run_text_blocks(self, blocks, x, S, width, cos, sin, mask, out, dtype=FP32):
+    def run_text_blocks(self, blocks, x, S, width, cos, sin, mask, out, dtype=FP32, causal=False):
         import numpy as np
         ids = (c_int * len(blocks))(*blocks)
         secs = np.zeros(len(blocks), np.float64)
         e = _err()
         rc = self.L.ernie_run_text_blocks(self.dev, ctypes.cast(ids, c_vp), len(blocks), ptr(x), S, width, ptr(cos),
-                                          ptr(sin), ptr(mask), dtype, ptr(out), secs.ctypes.data, e, 512)
+                                          ptr(sin), ptr(mask), 1 if causal else 0, dtype, ptr(out), secs.ctypes.data,
+                                          e, 512)
         if rc < 0:
             _raise(rc, e.value)
         return secs

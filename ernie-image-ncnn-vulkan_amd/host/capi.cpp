@@ -200,8 +200,8 @@ int ernie_text_embeddings(const uint16_t* table, size_t vocabulary, int width, c
 }
 
 int ernie_run_text_blocks(ernie_device* device, const int* blocks, int count, const float* x, int S, int width,
-                          const float* cos_t, const float* sin_t, const float* mask, int storage_dtype, float* out,
-                          double* compute_seconds, char* err, size_t errlen)
+                          const float* cos_t, const float* sin_t, const float* mask, int causal, int storage_dtype,
+                          float* out, double* compute_seconds, char* err, size_t errlen)
 {
     return guarded(err, errlen, [&]() -> int {
         if (!device || !blocks || count < 0) throw std::invalid_argument("null text block argument");
@@ -209,6 +209,8 @@ int ernie_run_text_blocks(ernie_device* device, const int* blocks, int count, co
         for (int i = 0; i < count; ++i) models.push_back({blocks[i]});
         std::vector<ernie::DeviceMat> constants = {wrap(cos_t, 128, S), wrap(sin_t, 128, S),
                                                    mask ? wrap(mask, S, S) : ernie::DeviceMat{}};
+        constants[2].causal = causal != 0;
+        if (causal && !mask) throw std::invalid_argument("A causal text mask needs its [S][S] tensor");
         ernie::BlockSequenceStats stats;
         const auto& d = device->device;
         const auto result =

@@ -45,6 +45,8 @@ struct DeviceMat {
     float* data = nullptr;
     int dims = 0, w = 0, h = 1, c = 1;
     int valid_prefix = 0;
+    // Set by upload_text_constants on its causal mask: applied by position, not read.
+    bool causal = false;
     size_t total() const { return size_t(w) * h * c; }
     bool empty() const { return data == nullptr || total() == 0; }
     // Allocate on the device.

@@ -34,7 +34,7 @@ struct TextConstantsHost {
 TextConstantsHost text_constants(const std::vector<float>& inverse_frequencies, int bucket);
 // The file form: 64 FP32 values (256 bytes).
 TextConstantsHost text_constants(const std::string& inverse_frequency_path, int bucket);
-// Uploads: cosine, sine, causal mask.
+// Uploads: cosine, sine, causal mask (marked causal: the device applies it by position).
 std::vector<DeviceMat> upload_text_constants(const Device& device, const TextConstantsHost& constants);
 
 // src/text_encoder.cpp:119-180: blocks in order on input [S][hidden] FP32 with the

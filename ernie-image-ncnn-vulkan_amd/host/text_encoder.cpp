@@ -105,6 +105,7 @@ std::vector<DeviceMat> upload_text_constants(const Device& device, const TextCon
     cos.upload(device, k.cos.data(), k.cos.size());
     sin.upload(device, k.sin.data(), k.sin.size());
     mask.upload(device, k.mask.data(), k.mask.size());
+    mask.causal = true;
     return {cos, sin, mask};
 }
 
@@ -135,8 +136,9 @@ DeviceMat run_text_blocks(const std::vector<BlockModel>& models, const DeviceMat
     for (std::size_t i = 0; i < models.size(); ++i) {
         double seconds = 0;
         const int index = models[i].index;
-        check_status(ernie_hip_text_block_sequence(ctx, &index, 1, in, current.data, cos.data, sin.data,
-                                                   mask.empty() ? nullptr : mask.data, S, &seconds),
+        const float* m = mask.empty() || mask.causal ? nullptr : mask.data;
+        check_status(ernie_hip_text_block_sequence(ctx, &index, 1, in, current.data, cos.data, sin.data, m,
+                                                   mask.causal ? 1 : 0, S, &seconds),
                      ctx, "text block");
         in = current.data;
         stats.load_seconds.push_back(0.0);

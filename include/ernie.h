@@ -72,10 +72,12 @@ int ernie_text_embeddings(const uint16_t* table, size_t vocabulary, int width, c
                           int bucket, float* out, char* err, size_t errlen);
 /* run_text_blocks (src/text_encoder.h:17-19): x [S][width] device FP32, cos/sin
  * [S][128], mask [S][S] (device; NULL = none), blocks = resident text block slots.
- * out [S][width] device FP32. compute_seconds (nullable) gets per-block time. */
+ * causal = 1 declares the mask the causal one text_constants builds: it is then
+ * applied by position and not read. out [S][width] device FP32. compute_seconds
+ * (nullable) gets per-block time. */
 int ernie_run_text_blocks(ernie_device* device, const int* blocks, int count, const float* x, int S, int width,
-                          const float* cos_t, const float* sin_t, const float* mask, int storage_dtype, float* out,
-                          double* compute_seconds, char* err, size_t errlen);
+                          const float* cos_t, const float* sin_t, const float* mask, int causal, int storage_dtype,
+                          float* out, double* compute_seconds, char* err, size_t errlen);
 
 /* ---- on-disk blocks (block.ncnn.param + block.ncnn.bin) ----------------------- */
 typedef struct {

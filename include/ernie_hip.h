@@ -89,6 +89,13 @@ int ernie_hip_sdpa(ernie_hip_ctx* ctx, const void* q, const void* k, const void*
                    long k_head_stride, long k_row_stride, long v_head_stride, long v_row_stride,
                    long o_head_stride, long o_row_stride, const float* mask, int mask_heads, int mask_rows,
                    int valid_keys, float scale);
+/* Causal prefill attention (the text encoder's mask, src/text_encoder.cpp:115-116,
+ * applied without a mask tensor): key k is visible to query q iff k <= q + (sk - sq);
+ * sq <= sk. Otherwise as ernie_hip_sdpa. */
+int ernie_hip_sdpa_causal(ernie_hip_ctx* ctx, const void* q, const void* k, const void* v, void* out, int dtype,
+                          int heads, int kv_heads, int sq, int sk, int d, long q_head_stride, long q_row_stride,
+                          long k_head_stride, long k_row_stride, long v_head_stride, long v_row_stride,
+                          long o_head_stride, long o_row_stride, float scale);
 /* set_attention_query_rows (src/ernie_attention.cpp:245-255): accepted for
  * compatibility (rows in {128,64,32,16}, else -1); flash attention needs no chunks. */
 int ernie_hip_set_attention_query_rows(ernie_hip_ctx* ctx, int rows);
@@ -194,14 +201,16 @@ int ernie_hip_text_block_init_random(ernie_hip_ctx* ctx, int index, int hidden, 
                                      int dtype, uint64_t seed, float std_dev);
 int ernie_hip_text_block_release(ernie_hip_ctx* ctx, int index);
 /* in0 = x [S][hidden] FP32, in1/in2 = cos/sin [S][128] FP32 (text_constants),
- * in3 = additive mask [S][S] FP32 (the causal mask; NULL = none). out0 [S][hidden]
- * FP32; out may alias x. */
+ * in3 = additive mask [S][S] FP32 (NULL = none); causal = 1 applies the causal mask
+ * text_constants builds without reading a tensor (pass mask = NULL then). out0
+ * [S][hidden] FP32; out may alias x. */
 int ernie_hip_text_block_forward(ernie_hip_ctx* ctx, int index, const float* x, float* out, const float* cos_t,
-                                 const float* sin_t, const float* mask, int S);
+                                 const float* sin_t, const float* mask, int causal, int S);
 /* run_text_blocks core (src/text_encoder.cpp:124-180): blocks[0..count), 1..25.
  * seconds (nullable) receives per-block device time. */
 int ernie_hip_text_block_sequence(ernie_hip_ctx* ctx, const int* blocks, int count, const float* x, float* out,
-                                  const float* cos_t, const float* sin_t, const float* mask, int S, double* seconds);
+                                  const float* cos_t, const float* sin_t, const float* mask, int causal, int S,
+                                  double* seconds);
 
 /* ---- DiT heads (heads/input, heads/output head.ncnn.param) ----------------------- */
 typedef struct {

@@ -30,6 +30,27 @@ def test_gqa_causal_attention_probe(ctx, dt, length):
     m = kat.metrics(got, ref)
     atol, nrmse = kat.GQA_PROBE_LIMITS[NAMES[dt]]
     assert m["finite"] and m["max_abs_error"] <= atol and m["nrmse"] <= nrmse, m
+    # The same attention applied by position (no mask tensor; tiles above the diagonal skipped).
+    o2 = empty(q.shape, dt)
+    ctx.sdpa_causal(dev(q, dt), dev(k, dt), dev(v, dt), o2, dt, 32, 8, length, length, d, strides)
+    m2 = kat.metrics(host(o2), ref)
+    assert m2["finite"] and m2["max_abs_error"] <= atol and m2["nrmse"] <= nrmse, m2
+
+
+@pytest.mark.parametrize("dt", ALL_DT, ids=lambda d: NAMES[d])
+def test_gqa_causal_queries_after_a_prefix(ctx, dt):
+    # The probe's growth case (probes/attention_probe.cpp:326): queries at positions
+    # 34..64 over all 65 keys, key k visible iff k <= q + (sk - sq).
+    sk, sq, d = 65, 31, 128
+    q, k, v, _ = kat.gqa_causal_case(sk, 83)
+    ref = kat.gqa_causal_expected(stored(q, dt), stored(k, dt), stored(v, dt))[:, sk - sq:]
+    qt = np.ascontiguousarray(q[:, sk - sq:])
+    o = empty(qt.shape, dt)
+    strides = (sq * d, d, sk * d, d, sk * d, d, sq * d, d)
+    ctx.sdpa_causal(dev(qt, dt), dev(k, dt), dev(v, dt), o, dt, 32, 8, sq, sk, d, strides)
+    m = kat.metrics(host(o), ref)
+    atol, nrmse = kat.GQA_PROBE_LIMITS[NAMES[dt]]
+    assert m["finite"] and m["max_abs_error"] <= atol and m["nrmse"] <= nrmse, m
 
 
 @pytest.mark.parametrize("dt", ALL_DT, ids=lambda d: NAMES[d])
@@ -47,10 +68,11 @@ def test_rotary_only_matches_oracle(ctx, dt):
     assert np.max(np.abs(got - ref)) <= limit * max(1.0, np.max(np.abs(ref)))
 
 
-def run_text_block(ctx, index, x, cos, sin, mask):
+def run_text_block(ctx, index, x, cos, sin, mask, causal=False):
     S, hidden = x.shape
     out = empty((S, hidden))
-    ctx.text_block_forward(index, dev(x), out, dev(cos), dev(sin), S, mask=None if mask is None else dev(mask))
+    ctx.text_block_forward(index, dev(x), out, dev(cos), dev(sin), S, mask=None if mask is None else dev(mask),
+                           causal=causal)
     return host(out)
 
 
@@ -78,6 +100,9 @@ def test_text_block_full_width_against_oracle(ctx, full_text_block, dt, S):
         m = kat.north_star_fp32(got, ref)
         assert m["passed"], m
     np.testing.assert_array_equal(run_text_block(ctx, 3, x, cos, sin, mask), got)  # repeat-deterministic
+    # Causal by position instead of the mask tensor.
+    gc = kat.gate(run_text_block(ctx, 3, x, cos, sin, None, causal=True), ref, *kat.TEXT_GATES[NAMES[dt]])
+    assert gc["passed"], gc
     ctx.call("text_block_release", 3)
 
 
@@ -90,7 +115,7 @@ def test_text_block_ragged_tiles_against_oracle(ctx, dt):
     ctx.text_block_upload(4, w, hidden, heads, kv, ffn, dt)
     cos, sin, mask = O.text_constants(yarn_like_frequencies(), S)
     x = O.normal((S, hidden), 45, std=0.2)
-    got = run_text_block(ctx, 4, x, cos, sin, mask)
+    got = run_text_block(ctx, 4, x, cos, sin, None, causal=True)
     ref = O.text_block_forward(w, x, cos, sin, mask, heads, kv)
     g = kat.gate(got, ref, *kat.TEXT_GATES[NAMES[dt]])
     assert g["passed"], g
@@ -121,6 +146,12 @@ def test_text_sequence_and_facade_against_oracle(ctx):
         out2 = empty((S, hidden))
         fac.run_text_blocks([10, 11, 12], xd, S, hidden, cd, sd, md, out2, dtype=E.FP16)
         np.testing.assert_array_equal(host(out2), got)
+        # The facade's causal mask (as upload_text_constants marks it) runs by position.
+        fac.hip.text_block_sequence([10, 11, 12], xd, out, cd, sd, S, causal=True)
+        fac.run_text_blocks([10, 11, 12], xd, S, hidden, cd, sd, md, out2, dtype=E.FP16, causal=True)
+        np.testing.assert_array_equal(host(out2), host(out))
+        gc = kat.gate(host(out), ref, *kat.TEXT_GATES["fp16"])
+        assert gc["passed"], gc
         # src/text_encoder.cpp:41-45: 1..25 blocks and exactly the three constants.
         with pytest.raises(E.ErnieInvalidRequest):
             fac.run_text_blocks([], xd, S, hidden, cd, sd, md, out2, dtype=E.FP16)
