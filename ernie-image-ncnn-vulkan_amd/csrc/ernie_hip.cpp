@@ -352,16 +352,16 @@ int block_workspace(ernie_hip_ctx* ctx, int S, int dim, int ffn, int dtype, Bloc
     return ERNIE_OK;
 }
 
-// Split-K scratch of the block GEMMs' tail row of tiles (S % 256 rows): at most 256
-// items of (64 * tail_sub) x 256 FP32 partials.
+// Split-K scratch of the block GEMMs: the tail row of tiles (S % 256 rows) or, for a
+// GEMM with too few tiles for the CUs, every tile: at most 256 items of up to 256 x 256
+// FP32 partials.
 constexpr int kSplitItems = 256;
 
 // The same buffer also holds the attention key-range parts of a partial last query
 // tile: up to 16 parts per head of 128 queries x (128 values + m, l) FP32.
 size_t split_bytes(int S, int heads)
 {
-    const int tail_sub = (S % 256 + 63) / 64;
-    const size_t gemm = (size_t)kSplitItems * 64 * tail_sub * 256 * sizeof(float);
+    const size_t gemm = (size_t)kSplitItems * 256 * 256 * sizeof(float);
     const size_t attn = S % 128 ? (size_t)heads * 16 * 128 * (128 + 2) * sizeof(float) : 0;
     return std::max(gemm, attn);
 }

@@ -62,7 +62,11 @@ struct Params {
     int a_kstep;      // 64, or a_k32_rows * 64
     long c_rs, c_ss;  // EPI_GEGLU output: element distance of rows and of 32-column groups
     int split;        // K parts per tail tile (1 = no split)
-    float* part;      // [n_tiles][split][64 * tail_sub][BN] FP32 partial sums of split tail tiles
+    // split_all: every tile (not only the tail row) is split into `split` K parts; used
+    // when the GEMM has too few tiles to fill the CUs. Partial layout then
+    // [m_tiles][n_tiles][split][BM][BN]; else [n_tiles][split][64 * tail_sub][BN].
+    int split_all;
+    float* part;
 };
 
 // Sums the K parts of the split tail tiles and applies the epilogue: one thread per
@@ -70,22 +74,25 @@ struct Params {
 template <typename OutT, int EPI>
 __global__ void __launch_bounds__(256) split_reduce_kernel(Params p)
 {
-    const int rows = 64 * p.tail_sub;
+    const int rows = p.split_all ? p.M : 64 * p.tail_sub;
     const int cols = epi_glu(EPI) ? p.N / 2 : p.N;
     const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (long)rows * cols) return;
     const int rl = (int)(idx / cols), c = (int)(idx - (long)rl * cols);
-    const int m = p.m_full * BM + rl;
+    const int m = p.split_all ? rl : p.m_full * BM + rl;
     if (m >= p.M) return;
     // Column n of the tile grid; GEGLU output column c holds up column (c / 32) * 64 + c % 32
     // and gate column + 32 of the interleaved W rows.
     const int n = epi_glu(EPI) ? (c / 32) * 64 + (c % 32) : c;
     const int nt = n / BN, cl = n - nt * BN;
-    const float* base = p.part + (size_t)nt * p.split * rows * BN + (size_t)rl * BN + cl;
+    const int slot_rows = p.split_all ? BM : rows;
+    const float* base = p.split_all
+                            ? p.part + ((size_t)((m / BM) * p.n_tiles + nt) * p.split * BM + m % BM) * BN + cl
+                            : p.part + (size_t)nt * p.split * rows * BN + (size_t)rl * BN + cl;
     float v = 0.f, g = 0.f;
     for (int q = 0; q < p.split; ++q) {
-        v += base[(size_t)q * rows * BN];
-        if (epi_glu(EPI)) g += base[(size_t)q * rows * BN + 32];
+        v += base[(size_t)q * slot_rows * BN];
+        if (epi_glu(EPI)) g += base[(size_t)q * slot_rows * BN + 32];
     }
     if (epi_glu(EPI)) {
         static_cast<OutT*>(p.C)[(size_t)m * p.c_rs + (size_t)(c >> 5) * p.c_ss + (c & 31)] =
@@ -124,6 +131,18 @@ __device__ __forceinline__ int fsw(int r) { return (r >> 2) & 3; }
 // last and spread over all XCDs; the parts of one tile stay on one XCD.
 __device__ __forceinline__ void tile_of(const Params& p, int bid, int& mt, int& nt, int& part)
 {
+    if (p.split_all) {
+        // Items (tile, part), a tile's parts adjacent and on one XCD; tiles walk the M
+        // tiles of one N column before the next (the W panel shared within an XCD).
+        const int m_tiles = p.m_full + (p.tail_sub ? 1 : 0);
+        const int items = m_tiles * p.n_tiles * p.split;
+        const int u = (items & 7) == 0 ? (bid & 7) * (items >> 3) + (bid >> 3) : bid;
+        const int t = u / p.split;
+        part = u - t * p.split;
+        nt = t / m_tiles;
+        mt = t - nt * m_tiles;
+        return;
+    }
     const int full = p.m_full * p.n_tiles;
     const int tail_items = p.tail_sub ? p.n_tiles * p.split : 0;
     part = 0;
@@ -206,7 +225,7 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
     }
     // K steps of this item: all of them, or part `part` of `split` for a tail tile.
     const int nk_all = p.K / BK;
-    const int parts = mt == p.m_full ? p.split : 1;
+    const int parts = (p.split_all || mt == p.m_full) ? p.split : 1;
     const int kt0 = (int)((long)nk_all * part / parts);
     const int nk = (int)((long)nk_all * (part + 1) / parts) - kt0;
     auto issue = [&](int kt) {
@@ -294,11 +313,12 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
 
     const int row_w = m0 + wm * 32 * MSUB + 4 * q16;  // + 16 i + r: output row
     const int col_w = n0 + wn * 64 + r16;            // + 16 j: output column (W row)
-    if (p.split > 1 && mt == p.m_full) {
-        // Split tail tile: store this part's FP32 partial; split_reduce_kernel, the
-        // next launch on the stream, adds the parts and applies the epilogue.
-        const int rows = 64 * p.tail_sub;
-        float* base = p.part + ((size_t)nt * p.split + part) * rows * BN;
+    if (p.split > 1 && (p.split_all || mt == p.m_full)) {
+        // Split tile: store this part's FP32 partial; split_reduce_kernel, the next
+        // launch on the stream, adds the parts and applies the epilogue.
+        const int rows = p.split_all ? BM : 64 * p.tail_sub;
+        float* base = p.split_all ? p.part + (((size_t)mt * p.n_tiles + nt) * p.split + part) * BM * BN
+                                  : p.part + ((size_t)nt * p.split + part) * rows * BN;
 #pragma unroll
         for (int i = 0; i < 2 * MSUB; ++i)
 #pragma unroll
@@ -432,7 +452,22 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     // (at most 16 parts, at least 4 K steps each), within the caller's workspace.
     // With M < 256 the tail row is the whole GEMM (a short prompt's projections).
     p.split = 1;
-    if (p.tail_sub && a.split_ws) {
+    p.split_all = 0;
+    const int m_tiles = p.m_full + (p.tail_sub ? 1 : 0);
+    if (a.split_ws && p.m_full && m_tiles * p.n_tiles <= kSplitTargetItems / 2) {
+        // Too few tiles for the CUs (a short sequence's narrow projections): split
+        // every tile along K, at least 4 K steps per part.
+        const size_t per_part = (size_t)m_tiles * p.n_tiles * pingpong::BM * pingpong::BN * sizeof(float);
+        int sp = std::min(16, kSplitTargetItems / (m_tiles * p.n_tiles));
+        sp = std::min(sp, std::max(1, a.K / pingpong::BK / 4));
+        while (sp > 1 && (size_t)sp * per_part > a.split_ws_bytes) --sp;
+        if (sp > 1) {
+            p.split = sp;
+            p.split_all = 1;
+            p.part = static_cast<float*>(a.split_ws);
+        }
+    }
+    if (!p.split_all && p.tail_sub && a.split_ws) {
         const size_t per_part = (size_t)p.n_tiles * 64 * p.tail_sub * pingpong::BN * sizeof(float);
         int sp = std::min(16, std::max(1, kSplitTargetItems / p.n_tiles));
         sp = std::min(sp, std::max(1, a.K / pingpong::BK / 4));
@@ -440,7 +475,8 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
         p.split = sp;
         p.part = static_cast<float*>(a.split_ws);
     }
-    const int tiles = p.m_full * p.n_tiles + (p.tail_sub ? p.n_tiles * p.split : 0);
+    const int tiles = p.split_all ? m_tiles * p.n_tiles * p.split
+                                  : p.m_full * p.n_tiles + (p.tail_sub ? p.n_tiles * p.split : 0);
     const dim3 grid(tiles), block(512);
 #define EHIP_PINGPONG(T)                                                                                            \
     do {                                                                                                      \
@@ -459,7 +495,7 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     else EHIP_PINGPONG(bf16);
 #undef EHIP_PINGPONG
     if (p.split > 1) {
-        const long items = (long)64 * p.tail_sub * (epi_glu(a.epilogue) ? a.N / 2 : a.N);
+        const long items = (long)(p.split_all ? a.M : 64 * p.tail_sub) * (epi_glu(a.epilogue) ? a.N / 2 : a.N);
         const dim3 rgrid((unsigned)((items + 255) / 256)), rblock(256);
 #define EHIP_REDUCE(OUT, EPI) hipLaunchKernelGGL((pingpong::split_reduce_kernel<OUT, EPI>), rgrid, rblock, 0, s, p)
         if (a.epilogue == EPI_STORE) {
