@@ -37,6 +37,8 @@ namespace ehip {
 namespace {
 // Target number of tail-row items: one per CU of an MI355X.
 constexpr int kSplitTargetItems = 256;
+// Most K parts a split tile is cut into.
+constexpr int kMaxSplit = 16;
 }
 namespace pingpong {
 
@@ -89,10 +91,23 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(Params p)
     const float* base = p.split_all
                             ? p.part + ((size_t)((m / BM) * p.n_tiles + nt) * p.split * BM + m % BM) * BN + cl
                             : p.part + (size_t)nt * p.split * rows * BN + (size_t)rl * BN + cl;
+    // All parts' loads are issued before the first add (at most kMaxSplit parts), then
+    // added in part order, so the sum does not wait out one load latency per part.
+    float pv[kMaxSplit], pg[kMaxSplit];
+#pragma unroll
+    for (int q = 0; q < kMaxSplit; ++q) {
+        if (q < p.split) {
+            pv[q] = base[(size_t)q * slot_rows * BN];
+            if (epi_glu(EPI)) pg[q] = base[(size_t)q * slot_rows * BN + 32];
+        }
+    }
     float v = 0.f, g = 0.f;
-    for (int q = 0; q < p.split; ++q) {
-        v += base[(size_t)q * slot_rows * BN];
-        if (epi_glu(EPI)) g += base[(size_t)q * slot_rows * BN + 32];
+#pragma unroll
+    for (int q = 0; q < kMaxSplit; ++q) {
+        if (q < p.split) {
+            v += pv[q];
+            if (epi_glu(EPI)) g += pg[q];
+        }
     }
     if (epi_glu(EPI)) {
         static_cast<OutT*>(p.C)[(size_t)m * p.c_rs + (size_t)(c >> 5) * p.c_ss + (c & 31)] =
@@ -458,7 +473,7 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
         // Too few tiles for the CUs (a short sequence's narrow projections): split
         // every tile along K, at least 4 K steps per part.
         const size_t per_part = (size_t)m_tiles * p.n_tiles * pingpong::BM * pingpong::BN * sizeof(float);
-        int sp = std::min(16, kSplitTargetItems / (m_tiles * p.n_tiles));
+        int sp = std::min(kMaxSplit, kSplitTargetItems / (m_tiles * p.n_tiles));
         sp = std::min(sp, std::max(1, a.K / pingpong::BK / 4));
         while (sp > 1 && (size_t)sp * per_part > a.split_ws_bytes) --sp;
         if (sp > 1) {
@@ -469,7 +484,7 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     }
     if (!p.split_all && p.tail_sub && a.split_ws) {
         const size_t per_part = (size_t)p.n_tiles * 64 * p.tail_sub * pingpong::BN * sizeof(float);
-        int sp = std::min(16, std::max(1, kSplitTargetItems / p.n_tiles));
+        int sp = std::min(kMaxSplit, std::max(1, kSplitTargetItems / p.n_tiles));
         sp = std::min(sp, std::max(1, a.K / pingpong::BK / 4));
         while (sp > 1 && (size_t)sp * per_part > a.split_ws_bytes) --sp;
         p.split = sp;

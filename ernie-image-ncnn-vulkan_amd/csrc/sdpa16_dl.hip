@@ -55,6 +55,7 @@ constexpr int V_BASE = 2 * KSTAGE;           // the V ring follows the two K sta
 constexpr int LDS_BYTES = V_BASE + 2 * KV_BYTES;
 constexpr uint32_t kRsrcFlags = 0x00020000;
 constexpr float kRescaleSlack = 8.0f;
+constexpr int kMaxParts = 16;  // most key-range parts of the split query tile
 
 struct Params {
     const void* q; const void* k; const void* v; void* o;
@@ -84,15 +85,30 @@ __global__ void __launch_bounds__(256) combine_kernel(Params p, int tail_q)
     const int ql = (int)((idx / D) % tail_q);
     const int h = (int)(idx / ((long)D * tail_q));
     const float* ml = p.part_ml + ((size_t)h * p.tail_parts * BQ + ql) * 2;
-    float M = -INFINITY;
-    for (int q = 0; q < p.tail_parts; ++q) M = fmaxf(M, ml[(size_t)q * BQ * 2]);
-    float L = 0.f, O = 0.f;
     const float* po = p.part_o + ((size_t)h * p.tail_parts * BQ + ql) * D + d;
-    for (int q = 0; q < p.tail_parts; ++q) {
-        const float m = ml[(size_t)q * BQ * 2];
-        const float w = m == -INFINITY ? 0.f : exp2f(m - M);
-        L += ml[(size_t)q * BQ * 2 + 1] * w;
-        O += po[(size_t)q * BQ * D] * w;
+    // Every part's loads are issued before the first use (at most kMaxParts parts);
+    // the merge then runs in part order.
+    float mv[kMaxParts], lv[kMaxParts], ov[kMaxParts];
+#pragma unroll
+    for (int q = 0; q < kMaxParts; ++q) {
+        if (q < p.tail_parts) {
+            mv[q] = ml[(size_t)q * BQ * 2];
+            lv[q] = ml[(size_t)q * BQ * 2 + 1];
+            ov[q] = po[(size_t)q * BQ * D];
+        }
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < kMaxParts; ++q)
+        if (q < p.tail_parts) M = fmaxf(M, mv[q]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int q = 0; q < kMaxParts; ++q) {
+        if (q < p.tail_parts) {
+            const float w = mv[q] == -INFINITY ? 0.f : exp2f(mv[q] - M);
+            L += lv[q] * w;
+            O += ov[q] * w;
+        }
     }
     const int qi = p.full_qt * BQ + ql;
     static_cast<T*>(p.o)[(size_t)h * p.o_hs + (size_t)qi * p.o_rs + (size_t)(d >> 5) * p.o_ds + (d & 31)] = T(O / L);
@@ -535,7 +551,7 @@ int sdpa16_d128(const SdpaArgs& a, hipStream_t s)
     p.full_qt = a.sq / sdl::BQ;
     const int tail_q = a.sq - p.full_qt * sdl::BQ;
     if (tail_q && p.full_qt && a.split_ws) {
-        int parts = std::min(std::min(16, ntiles), std::max(1, kSdpaSlots / a.heads));
+        int parts = std::min(std::min(sdl::kMaxParts, ntiles), std::max(1, kSdpaSlots / a.heads));
         const size_t per_part = (size_t)a.heads * sdl::BQ * (sdl::D + 2) * sizeof(float);
         while (parts > 1 && (size_t)parts * per_part > a.split_ws_bytes) --parts;
         if (parts > 1) {
