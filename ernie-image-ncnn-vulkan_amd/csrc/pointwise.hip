@@ -179,7 +179,11 @@ __global__ void __launch_bounds__(256) rmsnorm_persist_kernel(const TIn* __restr
 // store instruction covers, per 32-column slab, both rows' 64 bytes, which are
 // adjacent in the tiled layout: four whole 128-byte lines per instruction. Lane l of
 // wave w holds row r0 + (l / 8 % 2) and columns 32 s + 4 (l % 8) .. + 3 of slabs
-// s = 4 (w + 4 i) + l / 16, i < NI.
+// s = 4 (w + 4 i) + l / 16, i < NI. The per-column factors gamma (1 + scale) and
+// shift are folded into LDS once per workgroup rather than held in registers: at
+// 116 VGPRs four workgroups share a CU, which keeps enough row loads in flight to
+// stream at close to copy bandwidth (holding them in registers, 178 VGPRs, halved
+// the workgroups per CU and the achieved bandwidth).
 template <typename TIn, typename TOut, int NI>
 __global__ void __launch_bounds__(256) rmsnorm_pair_k32_kernel(const TIn* __restrict__ x,
                                                                const float* __restrict__ gamma,
@@ -188,33 +192,36 @@ __global__ void __launch_bounds__(256) rmsnorm_pair_k32_kernel(const TIn* __rest
                                                                TOut* __restrict__ out, int out_rows)
 {
     constexpr int width = NI * 512;
+    __shared__ f32x4 mul_l[width / 4], add_l[width / 4];
     __shared__ float red[2][4][2];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, b = (lane >> 3) & 1;
-    int col[NI];
-    f32x4 m[NI], a[NI];
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-        col[i] = 32 * (4 * (wave + 4 * i) + (lane >> 4)) + 4 * (lane & 7);
+    for (int j = tid; j < width / 4; j += 256) {
+        f32x4 m, a;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const float g = gamma ? gamma[col[i] + e] : 1.0f;
-            m[i][e] = scale ? g * (scale[col[i] + e] + 1.0f) : g;
-            a[i][e] = shift ? shift[col[i] + e] : 0.0f;
+            const int c = 4 * j + e;
+            const float g = gamma ? gamma[c] : 1.0f;
+            m[e] = scale ? g * (scale[c] + 1.0f) : g;
+            a[e] = shift ? shift[c] : 0.0f;
         }
+        mul_l[j] = m;
+        add_l[j] = a;
     }
+    int col[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) col[i] = 32 * (4 * (wave + 4 * i) + (lane >> 4)) + 4 * (lane & 7);
     const int pairs = (rows + 1) >> 1;
     int pr = blockIdx.x;
     f32x4 v[NI];
-    auto load = [&](int pair, f32x4 (&dst)[NI]) {
+    auto load = [&](int pair) {
         const int r = 2 * pair + b;
 #pragma unroll
         for (int i = 0; i < NI; ++i)
-            dst[i] = r < rows ? Vec4<TIn>::load(x + (size_t)r * width + col[i]) : f32x4{0.f, 0.f, 0.f, 0.f};
+            v[i] = r < rows ? Vec4<TIn>::load(x + (size_t)r * width + col[i]) : f32x4{0.f, 0.f, 0.f, 0.f};
     };
-    if (pr < pairs) load(pr, v);
+    if (pr < pairs) load(pr);
+    __syncthreads();  // the LDS factors are in place
     for (int it = 0; pr < pairs; pr += gridDim.x, ++it) {
-        f32x4 vn[NI];
-        if (pr + (int)gridDim.x < pairs) load(pr + gridDim.x, vn);
         float ss = 0.f;
 #pragma unroll
         for (int i = 0; i < NI; ++i) ss += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
@@ -232,14 +239,14 @@ __global__ void __launch_bounds__(256) rmsnorm_pair_k32_kernel(const TIn* __rest
         if (r < rows) {
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
+                const f32x4 m = mul_l[col[i] >> 2], a = add_l[col[i] >> 2];
                 f32x4 y;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) y[e] = (v[i][e] * inv) * m[i][e] + a[i][e];
+                for (int e = 0; e < 4; ++e) y[e] = (v[i][e] * inv) * m[e] + a[e];
                 Vec4<TOut>::store(out + ((size_t)(col[i] >> 5) * out_rows + r) * 32 + (col[i] & 31), y);
             }
         }
-#pragma unroll
-        for (int i = 0; i < NI; ++i) v[i] = vn[i];
+        if (pr + (int)gridDim.x < pairs) load(pr + gridDim.x);
     }
 }
 
