@@ -184,6 +184,27 @@ __device__ __forceinline__ float pair_sum(float x)
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// ds_read_b64_tr_b16 (see the V^T fragments below) as inline assembly. Through the
+// builtin, the compiler treats the read as possibly aliasing the K / V tiles still
+// in flight from the direct global->LDS loads and waits for all of them (vmcnt(0))
+// before the first read, which would expose the prefetch latency in every step.
+// The tile read here always landed before the step's barrier, so only the LDS
+// counter matters: lgkm_wait_for waits until at most `after` LDS operations are
+// outstanding and names the destination registers, so no consumer of them can be
+// scheduled above the wait. LDS operations complete in order, so counting only the
+// reads issued here after the awaited one is enough (anything else in flight only
+// makes the wait stricter).
+__device__ __forceinline__ u32x2 ds_read_tr(uint32_t addr, int offset)
+{
+    u32x2 r;
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(offset));
+    return r;
+}
+__device__ __forceinline__ void lgkm_wait_for(u32x2& a, u32x2& b, int after)
+{
+    asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(after));
+}
+
 // Workgroup barrier without the release fence of __syncthreads() (that fence would
 // also wait for the tile still being loaded): LDS reads issued before it have
 // returned and the memory clobber keeps LDS accesses on their side.
@@ -409,20 +430,30 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
             for (int hh = 0; hh < 2; ++hh) l_run = Mfma<T>::rowsum(pf[t][hh], l_run);
     };
     // O^T += V^T P^T; P's register r of (t, hh) is key 32t + 16hh + 8(r/4 & 1) + 4g + r%4.
+    // MFMA k (0..15) takes key block b = k / 4 (keys 16 b .. + 15, i.e. t = b / 2,
+    // hh = b % 2) and value group dt = k % 4; its V^T operand is two transposing
+    // reads, issued two MFMAs ahead of their use.
     auto pv = [&](const uint8_t* vt, const vec8 (&pf)[2][2]) {
+        const uint32_t vb = (uint32_t)(uintptr_t)(lds_ptr_t)vt;
+        uint32_t base[4];
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int dt = 0; dt < 4; ++dt) base[dt] = vb + v_off[dt];
+        u32x2 lo[16], hi[16];
+        auto issue = [&](int k) {
+            lo[k] = ds_read_tr(base[k & 3], 16 * (k >> 2) * ROWB);
+            hi[k] = ds_read_tr(base[k & 3], (16 * (k >> 2) + 8) * ROWB);
+        };
+        issue(0);
+        issue(1);
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const int kb = 32 * t + 16 * hh;
-#pragma unroll
-                for (int dt = 0; dt < 4; ++dt) {
-                    const u32x2 lo = Mfma<T>::tr(vt + v_off[dt] + kb * ROWB);
-                    const u32x2 hi = Mfma<T>::tr(vt + v_off[dt] + (kb + 8) * ROWB);
-                    const u32x4 packed = {lo[0], lo[1], hi[0], hi[1]};
-                    oacc[dt] = Mfma<T>::run(__builtin_bit_cast(vec8, packed), pf[t][hh], oacc[dt]);
-                }
-            }
+        for (int k = 0; k < 16; ++k) {
+            if (k + 2 < 16) issue(k + 2);
+            // Reads issued after MFMA k's two: those of MFMAs k+1 and k+2 (if any).
+            lgkm_wait_for(lo[k], hi[k], 2 * ((k + 2 < 16 ? k + 2 : 15) - k));
+            const u32x4 packed = {lo[k][0], lo[k][1], hi[k][0], hi[k][1]};
+            const int b = k >> 2;
+            oacc[k & 3] = Mfma<T>::run(__builtin_bit_cast(vec8, packed), pf[b >> 1][b & 1], oacc[k & 3]);
+        }
     };
 
     // Software pipeline over the key tiles i = 0 .. n-1 of [it0, it1): step i computes
