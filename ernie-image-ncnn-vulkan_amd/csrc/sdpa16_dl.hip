@@ -204,6 +204,18 @@ __device__ __forceinline__ void lgkm_wait_for(u32x2& a, u32x2& b, int after)
 {
     asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(after));
 }
+// ds_read_b128 of a K fragment the same way (with the builtin load the compiler
+// could not keep a second fragment in flight at this register pressure).
+__device__ __forceinline__ u32x4 ds_read_b128(uint32_t addr, int offset)
+{
+    u32x4 r;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(offset));
+    return r;
+}
+__device__ __forceinline__ void lgkm_wait_for(u32x4& a, int after)
+{
+    asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a) : "i"(after));
+}
 
 // Workgroup barrier without the release fence of __syncthreads() (that fence would
 // also wait for the tile still being loaded): LDS reads issued before it have
@@ -355,7 +367,7 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
     // read as zero through the buffer range, and fall past kv_end anyway).
     const float inv_scale = kLog2e / c;
     const uint32_t dense_row = (uint32_t)(min(my_q, p.sq - 1) * p.sk) * 4u;
-    auto qk = [&](const uint8_t* ks, int kv0, f32x16 (&sacc)[2]) {
+    auto qk_init = [&](const uint8_t* ks, int kv0, f32x16 (&sacc)[2]) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             if constexpr (MASKROW) {
@@ -374,11 +386,24 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) sacc[t][r] = 0.f;
             }
+        }
+    };
+    // K fragment n of a tile: key half n % 2, head-dim slice n / 2, so consecutive
+    // MFMAs accumulate into different halves and never wait on each other.
+    auto kfrag = [&](uint32_t kb, int n) { return ds_read_b128(kb + k_off[n >> 1], (n & 1) * 32 * ROWB); };
+    // Wait for K fragment n when fragments up to n + 2 have been issued.
+    auto kwait = [&](u32x4& f, int n) { lgkm_wait_for(f, n + 2 < 16 ? 2 : 15 - n); };
+    auto qk = [&](const uint8_t* ks, int kv0, f32x16 (&sacc)[2]) {
+        qk_init(ks, kv0, sacc);
+        const uint32_t kb = (uint32_t)(uintptr_t)(lds_ptr_t)ks;
+        u32x4 kf[16];
+        kf[0] = kfrag(kb, 0);
+        kf[1] = kfrag(kb, 1);
 #pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const vec8 kf = *reinterpret_cast<const vec8*>(ks + k_off[s] + t * 32 * ROWB);
-                sacc[t] = Mfma<T>::run(kf, qf[s], sacc[t]);
-            }
+        for (int n = 0; n < 16; ++n) {
+            if (n + 2 < 16) kf[n + 2] = kfrag(kb, n + 2);
+            kwait(kf[n], n);
+            sacc[n & 1] = Mfma<T>::run(__builtin_bit_cast(vec8, kf[n]), qf[n >> 1], sacc[n & 1]);
         }
     };
     // Mask, bound and tile maximum (log2 domain) of tile `it`; raises the running
@@ -471,15 +496,29 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
         if constexpr (decltype(has_next)::value) {
             if (i + 2 < n) issue_k(it0 + i + 2, i & 1);
             issue_v(it0 + i + 1, (i + 1) & 1);
-            qk(kstage((i + 1) & 1), (it0 + i + 1) * BKV, nxt);
-            softmax(cur, cs_cur, pf);
-            // Interleave the 16 K-fragment reads and MFMAs of the next tile with the
-            // softmax of this one (independent work for the VALU under each MFMA).
+            // S of the next tile on the matrix cores, interleaved by hand with the
+            // softmax of this one: each group issues K fragment n + 2, waits for
+            // fragment n, issues MFMA n and turns two scores of this tile into
+            // probabilities (plus a row-sum term when a probability vector is
+            // complete); sched_barrier keeps the groups in this order.
+            qk_init(kstage((i + 1) & 1), (it0 + i + 1) * BKV, nxt);
+            const float m_use = m_run == -INFINITY ? 0.f : m_run;
+            const uint32_t kb = (uint32_t)(uintptr_t)(lds_ptr_t)kstage((i + 1) & 1);
+            u32x4 kf[16];
+            kf[0] = kfrag(kb, 0);
+            kf[1] = kfrag(kb, 1);
 #pragma unroll
             for (int k = 0; k < 16; ++k) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);  // VALU incl. transcendental
+                if (k + 2 < 16) kf[k + 2] = kfrag(kb, k + 2);
+                kwait(kf[k], k);
+                nxt[k & 1] = Mfma<T>::run(__builtin_bit_cast(vec8, kf[k]), qf[k >> 1], nxt[k & 1]);
+#pragma unroll
+                for (int e = 2 * k; e < 2 * k + 2; ++e) {
+                    const int t = e >> 4, r = e & 15;
+                    pf[t][r >> 3][r & 7] = T(__builtin_amdgcn_exp2f(__builtin_fmaf(cur[t][r], cs_cur, -m_use)));
+                }
+                if ((k & 3) == 3) l_run = Mfma<T>::rowsum(pf[k >> 3][(k >> 2) & 1], l_run);
+                __builtin_amdgcn_sched_barrier(0);
             }
             pv(vstage(i & 1), pf);
             cs_nxt = prep(nxt, it0 + i + 1);
