@@ -333,11 +333,12 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
     };
 
     // K fragment (A of S^T = K Q^T): key 32t + lrow, logical chunk 2s + g. The
-    // swizzle depends on lrow only, so per-lane offsets are fixed and the key-half
-    // and stage offsets fold into the instructions' immediate offsets.
-    uint32_t k_off[8];
+    // swizzle depends on lrow only, so per-lane LDS addresses (of stage 0) are fixed
+    // and the key-half and stage offsets fold into the reads' immediate offsets.
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)smem;
+    uint32_t k_addr[8];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) k_off[s] = lrow * ROWB + (((2 * s + g) ^ kswz(lrow)) << 4);
+    for (int s = 0; s < 8; ++s) k_addr[s] = lds0 + lrow * ROWB + (((2 * s + g) ^ kswz(lrow)) << 4);
     // V^T fragment (A of O^T = V^T P^T) by transposing reads: 16-lane group G = lane >> 4
     // (k-half G >> 1, d half 16 (G & 1)), lane j = lane & 15 points at key
     // kb + 4 (G >> 1) + (j >> 2) with kb a multiple of 8, so its swizzle 2 (key & 7)
@@ -345,11 +346,11 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
     const int G = lane >> 4, j = lane & 15;
     const int v_key_off = 4 * (G >> 1) + (j >> 2);
     const int v_d = 16 * (G & 1) + 4 * (j & 3);
-    uint32_t v_off[4];
+    uint32_t v_addr[4];  // LDS addresses in V stage 0
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
         const int d = 32 * dt + v_d;
-        v_off[dt] = v_key_off * ROWB + (((d >> 3) ^ vswz(v_key_off)) << 4) + (d & 7) * 2;
+        v_addr[dt] = lds0 + V_BASE + v_key_off * ROWB + (((d >> 3) ^ vswz(v_key_off)) << 4) + (d & 7) * 2;
     }
 
     f32x16 oacc[4];
@@ -388,20 +389,20 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
             }
         }
     };
-    // K fragment n of a tile: key half n % 2, head-dim slice n / 2, so consecutive
-    // MFMAs accumulate into different halves and never wait on each other.
-    auto kfrag = [&](uint32_t kb, int n) { return ds_read_b128(kb + k_off[n >> 1], (n & 1) * 32 * ROWB); };
+    // K fragment n of the tile in stage `slot` (a compile-time constant at every
+    // call): key half n % 2, head-dim slice n / 2, so consecutive MFMAs accumulate
+    // into different halves and never wait on each other.
+    auto kfrag = [&](int slot, int n) { return ds_read_b128(k_addr[n >> 1], slot * KSTAGE + (n & 1) * 32 * ROWB); };
     // Wait for K fragment n when fragments up to n + 2 have been issued.
     auto kwait = [&](u32x4& f, int n) { lgkm_wait_for(f, n + 2 < 16 ? 2 : 15 - n); };
-    auto qk = [&](const uint8_t* ks, int kv0, f32x16 (&sacc)[2]) {
-        qk_init(ks, kv0, sacc);
-        const uint32_t kb = (uint32_t)(uintptr_t)(lds_ptr_t)ks;
+    auto qk = [&](int slot, int kv0, f32x16 (&sacc)[2]) {
+        qk_init(kstage(slot), kv0, sacc);
         u32x4 kf[16];
-        kf[0] = kfrag(kb, 0);
-        kf[1] = kfrag(kb, 1);
+        kf[0] = kfrag(slot, 0);
+        kf[1] = kfrag(slot, 1);
 #pragma unroll
         for (int n = 0; n < 16; ++n) {
-            if (n + 2 < 16) kf[n + 2] = kfrag(kb, n + 2);
+            if (n + 2 < 16) kf[n + 2] = kfrag(slot, n + 2);
             kwait(kf[n], n);
             sacc[n & 1] = Mfma<T>::run(__builtin_bit_cast(vec8, kf[n]), qf[n >> 1], sacc[n & 1]);
         }
@@ -458,15 +459,11 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
     // MFMA k (0..15) takes key block b = k / 4 (keys 16 b .. + 15, i.e. t = b / 2,
     // hh = b % 2) and value group dt = k % 4; its V^T operand is two transposing
     // reads, issued two MFMAs ahead of their use.
-    auto pv = [&](const uint8_t* vt, const vec8 (&pf)[2][2]) {
-        const uint32_t vb = (uint32_t)(uintptr_t)(lds_ptr_t)vt;
-        uint32_t base[4];
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) base[dt] = vb + v_off[dt];
+    auto pv = [&](int slot, const vec8 (&pf)[2][2]) {
         u32x2 lo[16], hi[16];
         auto issue = [&](int k) {
-            lo[k] = ds_read_tr(base[k & 3], 16 * (k >> 2) * ROWB);
-            hi[k] = ds_read_tr(base[k & 3], (16 * (k >> 2) + 8) * ROWB);
+            lo[k] = ds_read_tr(v_addr[k & 3], slot * KV_BYTES + 16 * (k >> 2) * ROWB);
+            hi[k] = ds_read_tr(v_addr[k & 3], slot * KV_BYTES + (16 * (k >> 2) + 8) * ROWB);
         };
         issue(0);
         issue(1);
@@ -490,26 +487,27 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
     f32x16 sa[2], sb[2];
     vec8 pf[2][2];
     float cs_cur = c, cs_nxt = c;
-    auto step = [&](int i, f32x16 (&cur)[2], f32x16 (&nxt)[2], auto has_next) {
+    // P = i % 2 as a compile-time constant: K_{i+1} sits in stage 1 - P, V_i in stage P.
+    auto step = [&](int i, f32x16 (&cur)[2], f32x16 (&nxt)[2], auto has_next, auto parity) {
+        constexpr int P = decltype(parity)::value;
         __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // this wave's loads of K_{i+1}, V_i landed
         lds_barrier();                                         // ... every wave's; tile i-1 fully consumed
         if constexpr (decltype(has_next)::value) {
-            if (i + 2 < n) issue_k(it0 + i + 2, i & 1);
-            issue_v(it0 + i + 1, (i + 1) & 1);
+            if (i + 2 < n) issue_k(it0 + i + 2, P);
+            issue_v(it0 + i + 1, 1 - P);
             // S of the next tile on the matrix cores, interleaved by hand with the
             // softmax of this one: each group issues K fragment n + 2, waits for
             // fragment n, issues MFMA n and turns two scores of this tile into
             // probabilities (plus a row-sum term when a probability vector is
             // complete); sched_barrier keeps the groups in this order.
-            qk_init(kstage((i + 1) & 1), (it0 + i + 1) * BKV, nxt);
+            qk_init(kstage(1 - P), (it0 + i + 1) * BKV, nxt);
             const float m_use = m_run == -INFINITY ? 0.f : m_run;
-            const uint32_t kb = (uint32_t)(uintptr_t)(lds_ptr_t)kstage((i + 1) & 1);
             u32x4 kf[16];
-            kf[0] = kfrag(kb, 0);
-            kf[1] = kfrag(kb, 1);
+            kf[0] = kfrag(1 - P, 0);
+            kf[1] = kfrag(1 - P, 1);
 #pragma unroll
             for (int k = 0; k < 16; ++k) {
-                if (k + 2 < 16) kf[k + 2] = kfrag(kb, k + 2);
+                if (k + 2 < 16) kf[k + 2] = kfrag(1 - P, k + 2);
                 kwait(kf[k], k);
                 nxt[k & 1] = Mfma<T>::run(__builtin_bit_cast(vec8, kf[k]), qf[k >> 1], nxt[k & 1]);
 #pragma unroll
@@ -520,36 +518,38 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
                 if ((k & 3) == 3) l_run = Mfma<T>::rowsum(pf[k >> 3][(k >> 2) & 1], l_run);
                 __builtin_amdgcn_sched_barrier(0);
             }
-            pv(vstage(i & 1), pf);
+            pv(P, pf);
             cs_nxt = prep(nxt, it0 + i + 1);
         } else {
             softmax(cur, cs_cur, pf);
-            pv(vstage(i & 1), pf);
+            pv(P, pf);
         }
     };
     typedef std::integral_constant<bool, true> more;
     typedef std::integral_constant<bool, false> last;
+    typedef std::integral_constant<int, 0> even;
+    typedef std::integral_constant<int, 1> odd;
     if (n > 0) {
         issue_k(it0, 0);
         issue_v(it0, 0);
         if (n > 1) issue_k(it0 + 1, 1);
         __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
         lds_barrier();
-        qk(kstage(0), it0 * BKV, sa);
+        qk(0, it0 * BKV, sa);
         cs_cur = prep(sa, it0);
-        int i = 0;
+        int i = 0;  // always even at the top of the loop
         for (; i + 2 < n; i += 2) {
-            step(i, sa, sb, more());
+            step(i, sa, sb, more(), even());
             cs_cur = cs_nxt;
-            step(i + 1, sb, sa, more());
+            step(i + 1, sb, sa, more(), odd());
             cs_cur = cs_nxt;
         }
         if (n - i == 2) {
-            step(i, sa, sb, more());
+            step(i, sa, sb, more(), even());
             cs_cur = cs_nxt;
-            step(i + 1, sb, sa, last());
+            step(i + 1, sb, sa, last(), odd());
         } else {
-            step(i, sa, sb, last());
+            step(i, sa, sb, last(), even());
         }
     }
 
