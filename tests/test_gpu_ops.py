@@ -151,7 +151,8 @@ def test_sdpa_full_size_rows_against_oracle(ctx, dt):
     qs, ks, vs = (stored(t, dt).reshape(S, H, d).transpose(1, 0, 2).copy() for t in (q, k, v))
     mask = np.zeros(S, np.float32)
     mask[valid:] = -1e30
-    for r0, r1 in ((0, 64), (2048, 2112), (4096, 4160)):
+    # Rows 2240..2303 are the last two waves of their 128-query workgroup.
+    for r0, r1 in ((0, 64), (2048, 2112), (2240, 2304), (4096, 4160)):
         ref = O.sdpa(qs, ks, vs, mask=mask, q_range=(r0, r1))[:, r0:r1]
         got = out[:, r0:r1]
         if dt == E.FP32:
@@ -160,6 +161,29 @@ def test_sdpa_full_size_rows_against_oracle(ctx, dt):
         else:
             g = kat.gate(got, ref, *kat.BLOCK_GATES[NAMES[dt]])
             assert g["passed"], g
+
+
+@pytest.mark.parametrize("dt", [E.FP16, E.BF16], ids=lambda d: NAMES[d])
+@pytest.mark.parametrize("S,H,valid", [(256, 2, 256), (512, 3, 500), (456, 2, 456), (300, 1, 290), (1088, 2, 1060)])
+def test_sdpa_full_tiles_and_remainder(ctx, dt, S, H, valid):
+    # Unmasked attention at lengths around the kernel's 128-query workgroup tile:
+    # exact tiles, tiles plus a partial last tile of 72 / 44 / 64 queries (split
+    # along the keys) and valid-key counts that are not multiples of 64. Every row
+    # of every head is compared with the oracle.
+    d = 128
+    q = O.normal((S, H * d), 21)
+    k = O.normal((S, H * d), 22)
+    v = O.normal((S, H * d), 23)
+    o = empty((S, H * d), dt)
+    strides = (d, H * d, d, H * d, d, H * d, d, H * d)
+    ctx.sdpa(dev(q, dt), dev(k, dt), dev(v, dt), o, dt, H, H, S, S, d, strides, valid_keys=valid)
+    out = host(o).reshape(S, H, d).transpose(1, 0, 2)
+    qs, ks, vs = (stored(t, dt).reshape(S, H, d).transpose(1, 0, 2).copy() for t in (q, k, v))
+    mask = np.zeros(S, np.float32)
+    mask[valid:] = -1e30
+    ref = O.sdpa(qs, ks, vs, mask=mask)
+    g = kat.gate(out, ref, *kat.BLOCK_GATES[NAMES[dt]])
+    assert g["passed"], g
 
 
 @pytest.mark.parametrize("dt", ALL_DT, ids=lambda d: NAMES[d])
