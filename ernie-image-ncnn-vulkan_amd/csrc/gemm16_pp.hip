@@ -136,9 +136,14 @@ template <> struct Mfma<bf16> {
 };
 
 // Physical chunk = logical chunk ^ fsw(row). A fragment read has 16 lanes at rows
-// r0..r0+15 (r0 a multiple of 16) and one logical chunk: the bytes mod 256 are
-// 64 (r % 4) + 16 (chunk ^ (r / 4 % 4)), all 16 distinct.
-__device__ __forceinline__ int fsw(int r) { return (r >> 2) & 3; }
+// r0..r0+15 (r0 a multiple of 16) and one logical chunk. The LDS serves a
+// ds_read_b128 eight lanes (128 bytes) at a time, so each group of eight rows
+// must cover 8 distinct 16-byte slots mod 128: rows r and r + 1 sit 64 bytes
+// apart, and XOR-ing the chunk with row bits 1-2 spreads the four row pairs
+// over the four chunks. (Row bits 2-3, conflict-free for 16 lanes over 256
+// bytes, leaves two-way conflicts in every group of eight: measured 269 against
+// 424 GB/s per CU.)
+__device__ __forceinline__ int fsw(int r) { return (r >> 1) & 3; }
 
 // Tile order: workgroup b runs on XCD b % 8. Each XCD gets a contiguous share of
 // the full-height tiles (walked 4 M tiles per N sweep) and then its share of the
