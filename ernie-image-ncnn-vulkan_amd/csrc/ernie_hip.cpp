@@ -361,7 +361,7 @@ constexpr int kSplitItems = 256;
 // tile: up to 16 parts per head of 128 queries x (128 values + m, l) FP32.
 size_t split_bytes(int S, int heads)
 {
-    const size_t gemm = (size_t)kSplitItems * 256 * 256 * sizeof(float);
+    const size_t gemm = 2 * (size_t)kSplitItems * 256 * 256 * sizeof(float);
     const size_t attn = S % 128 ? (size_t)heads * 16 * 128 * (128 + 2) * sizeof(float) : 0;
     return std::max(gemm, attn);
 }

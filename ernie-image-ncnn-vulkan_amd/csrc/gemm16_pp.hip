@@ -69,17 +69,96 @@ struct Params {
     // [m_tiles][n_tiles][split][BM][BN]; else [n_tiles][split][64 * tail_sub][BN].
     int split_all;
     float* part;
+    // Late split: the last `late` full tiles of the tile order (a partial last round
+    // of workgroups) are each split into `late_split` K parts, so that round fills
+    // the CUs with shorter items. Partials [late][late_split][BM][BN] at late_part.
+    int late, late_split;
+    float* late_part;
 };
 
-// Sums the K parts of the split tail tiles and applies the epilogue: one thread per
-// output column (GEGLU: per up/gate column pair) and tail row.
+// Full tile f of the tile order -> (mt, nt): GM M tiles per N sweep, so the
+// workgroups that run together share A and W panels.
+__device__ __forceinline__ void full_order(const Params& p, int f, int& mt, int& nt)
+{
+    constexpr int GM = 4;
+    const int group_size = GM * p.n_tiles;
+    const int group = f / group_size;
+    const int first_m = group * GM;
+    const int gm = min(p.m_full - first_m, GM);
+    const int in_group = f - group * group_size;
+    mt = first_m + in_group % gm;
+    nt = in_group / gm;
+}
+
+// The epilogue of a reduced element: row m, output column c (GEGLU / SwiGLU: of
+// N / 2), tile-grid column n, summed value v (and gate sum g).
+template <typename OutT, int EPI>
+__device__ __forceinline__ void reduce_store(const Params& p, int m, int c, int n, float v, float g)
+{
+    if (epi_glu(EPI)) {
+        static_cast<OutT*>(p.C)[(size_t)m * p.c_rs + (size_t)(c >> 5) * p.c_ss + (c & 31)] =
+            OutT(v * glu_act<EPI == EPI_SWIGLU>(g));
+    } else if (EPI == EPI_STORE) {
+        if (p.bias) v += p.bias[n];
+        static_cast<OutT*>(p.C)[(size_t)m * p.ldc + n] = OutT(v);
+    } else {
+        static_cast<float*>(p.C)[(size_t)m * p.ldc + n] = p.resid[(size_t)m * p.ld_resid + n] + p.gate[n] * v;
+    }
+}
+
+// Sum of `parts` partials `stride` floats apart, in part order, every load issued
+// before the first add (at most kMaxSplit parts), so the sum does not wait out one
+// load latency per part.
+template <int EPI>
+__device__ __forceinline__ void sum_parts(const float* base, size_t stride, int parts, float& v, float& g)
+{
+    float pv[kMaxSplit], pg[kMaxSplit];
+#pragma unroll
+    for (int q = 0; q < kMaxSplit; ++q) {
+        if (q < parts) {
+            pv[q] = base[(size_t)q * stride];
+            if (epi_glu(EPI)) pg[q] = base[(size_t)q * stride + 32];
+        }
+    }
+    v = 0.f;
+    g = 0.f;
+#pragma unroll
+    for (int q = 0; q < kMaxSplit; ++q) {
+        if (q < parts) {
+            v += pv[q];
+            if (epi_glu(EPI)) g += pg[q];
+        }
+    }
+}
+
+// Sums the K parts of the split tiles and applies the epilogue: one thread per
+// output column (GEGLU: per up/gate column pair) and row, first over the tail row
+// (or every row when split_all), then over the late-split tiles.
 template <typename OutT, int EPI>
 __global__ void __launch_bounds__(256) split_reduce_kernel(Params p)
 {
-    const int rows = p.split_all ? p.M : 64 * p.tail_sub;
+    const int rows = p.split <= 1 ? 0 : (p.split_all ? p.M : 64 * p.tail_sub);
     const int cols = epi_glu(EPI) ? p.N / 2 : p.N;
     const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (long)rows * cols) return;
+    if (idx >= (long)rows * cols) {
+        // Late-split tile li: BM rows x BN grid columns (BN / 2 output columns for GLU).
+        const int cols_t = epi_glu(EPI) ? BN / 2 : BN;
+        const long j = idx - (long)rows * cols;
+        if (j >= (long)p.late * BM * cols_t) return;
+        const int li = (int)(j / (BM * cols_t));
+        const int rem = (int)(j - (long)li * BM * cols_t);
+        const int rl = rem / cols_t, cc = rem - rl * cols_t;
+        int mt, nt;
+        full_order(p, p.m_full * p.n_tiles - p.late + li, mt, nt);
+        const int m = mt * BM + rl;
+        const int c = (epi_glu(EPI) ? nt * (BN / 2) : nt * BN) + cc;
+        const int n = epi_glu(EPI) ? (c / 32) * 64 + (c % 32) : c;
+        float v, g;
+        sum_parts<EPI>(p.late_part + ((size_t)li * p.late_split * BM + rl) * BN + (n - nt * BN), (size_t)BM * BN,
+                       p.late_split, v, g);
+        reduce_store<OutT, EPI>(p, m, c, n, v, g);
+        return;
+    }
     const int rl = (int)(idx / cols), c = (int)(idx - (long)rl * cols);
     const int m = p.split_all ? rl : p.m_full * BM + rl;
     if (m >= p.M) return;
@@ -91,33 +170,9 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(Params p)
     const float* base = p.split_all
                             ? p.part + ((size_t)((m / BM) * p.n_tiles + nt) * p.split * BM + m % BM) * BN + cl
                             : p.part + (size_t)nt * p.split * rows * BN + (size_t)rl * BN + cl;
-    // All parts' loads are issued before the first add (at most kMaxSplit parts), then
-    // added in part order, so the sum does not wait out one load latency per part.
-    float pv[kMaxSplit], pg[kMaxSplit];
-#pragma unroll
-    for (int q = 0; q < kMaxSplit; ++q) {
-        if (q < p.split) {
-            pv[q] = base[(size_t)q * slot_rows * BN];
-            if (epi_glu(EPI)) pg[q] = base[(size_t)q * slot_rows * BN + 32];
-        }
-    }
-    float v = 0.f, g = 0.f;
-#pragma unroll
-    for (int q = 0; q < kMaxSplit; ++q) {
-        if (q < p.split) {
-            v += pv[q];
-            if (epi_glu(EPI)) g += pg[q];
-        }
-    }
-    if (epi_glu(EPI)) {
-        static_cast<OutT*>(p.C)[(size_t)m * p.c_rs + (size_t)(c >> 5) * p.c_ss + (c & 31)] =
-            OutT(v * glu_act<EPI == EPI_SWIGLU>(g));
-    } else if (EPI == EPI_STORE) {
-        if (p.bias) v += p.bias[n];
-        static_cast<OutT*>(p.C)[(size_t)m * p.ldc + n] = OutT(v);
-    } else {
-        static_cast<float*>(p.C)[(size_t)m * p.ldc + n] = p.resid[(size_t)m * p.ld_resid + n] + p.gate[n] * v;
-    }
+    float v, g;
+    sum_parts<EPI>(base, (size_t)slot_rows * BN, p.split, v, g);
+    reduce_store<OutT, EPI>(p, m, c, n, v, g);
 }
 
 template <typename T> struct Mfma;
@@ -146,11 +201,13 @@ template <> struct Mfma<bf16> {
 __device__ __forceinline__ int fsw(int r) { return (r >> 1) & 3; }
 
 // Tile order: workgroup b runs on XCD b % 8. Each XCD gets a contiguous share of
-// the full-height tiles (walked 4 M tiles per N sweep) and then its share of the
+// the full-height tiles (walked 4 M tiles per N sweep), then of the late-split
+// items (the last `late` full tiles, each in `late_split` K parts) and then of the
 // tail-row items (a tail tile split into `split` K parts), so the short items run
-// last and spread over all XCDs; the parts of one tile stay on one XCD.
-__device__ __forceinline__ void tile_of(const Params& p, int bid, int& mt, int& nt, int& part)
+// last and spread over all XCDs. li = index of a late-split tile, else -1.
+__device__ __forceinline__ void tile_of(const Params& p, int bid, int& mt, int& nt, int& part, int& li)
 {
+    li = -1;
     if (p.split_all) {
         // Items (tile, part), a tile's parts adjacent and on one XCD; tiles walk the M
         // tiles of one N column before the next (the W panel shared within an XCD).
@@ -163,39 +220,33 @@ __device__ __forceinline__ void tile_of(const Params& p, int bid, int& mt, int& 
         mt = t - nt * m_tiles;
         return;
     }
-    const int full = p.m_full * p.n_tiles;
+    const int main_full = p.m_full * p.n_tiles - p.late;
+    const int late_items = p.late * p.late_split;
     const int tail_items = p.tail_sub ? p.n_tiles * p.split : 0;
     part = 0;
-    int f;
-    if ((full & 7) == 0 && (tail_items & 7) == 0) {
+    int region, u;
+    if ((main_full & 7) == 0 && (late_items & 7) == 0 && (tail_items & 7) == 0) {
         const int x = bid & 7, j = bid >> 3;
-        const int per = full >> 3;
-        if (j >= per) {
-            const int u = x * (tail_items >> 3) + (j - per);
-            mt = p.m_full;
-            nt = u / p.split;
-            part = u - nt * p.split;
-            return;
-        }
-        f = x * per + j;
+        const int a = main_full >> 3, b = late_items >> 3;
+        if (j < a) { region = 0; u = x * a + j; }
+        else if (j < a + b) { region = 1; u = x * b + (j - a); }
+        else { region = 2; u = x * (tail_items >> 3) + (j - a - b); }
     } else {
-        if (bid >= full) {
-            const int u = bid - full;
-            mt = p.m_full;
-            nt = u / p.split;
-            part = u - nt * p.split;
-            return;
-        }
-        f = bid;
+        if (bid < main_full) { region = 0; u = bid; }
+        else if (bid < main_full + late_items) { region = 1; u = bid - main_full; }
+        else { region = 2; u = bid - main_full - late_items; }
     }
-    constexpr int GM = 4;
-    const int group_size = GM * p.n_tiles;
-    const int group = f / group_size;
-    const int first_m = group * GM;
-    const int gm = min(p.m_full - first_m, GM);
-    const int in_group = f - group * group_size;
-    mt = first_m + in_group % gm;
-    nt = in_group / gm;
+    if (region == 0) {
+        full_order(p, u, mt, nt);
+    } else if (region == 1) {
+        li = u / p.late_split;
+        part = u - li * p.late_split;
+        full_order(p, main_full + li, mt, nt);
+    } else {
+        mt = p.m_full;
+        nt = u / p.split;
+        part = u - nt * p.split;
+    }
 }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -220,7 +271,7 @@ __device__ __forceinline__ void wait_vm(int n)
 }
 
 template <typename T, typename OutT, int EPI, int MSUB>
-__device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, uint8_t* smem)
+__device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, int li, uint8_t* smem)
 {
     typedef typename Mfma<T>::vec vec8;
     const int m0 = mt * BM, n0 = nt * BN;
@@ -245,7 +296,7 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
     }
     // K steps of this item: all of them, or part `part` of `split` for a tail tile.
     const int nk_all = p.K / BK;
-    const int parts = (p.split_all || mt == p.m_full) ? p.split : 1;
+    const int parts = (p.split_all || mt == p.m_full) ? p.split : (li >= 0 ? p.late_split : 1);
     const int kt0 = (int)((long)nk_all * part / parts);
     const int nk = (int)((long)nk_all * (part + 1) / parts) - kt0;
     auto issue = [&](int kt) {
@@ -333,12 +384,13 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
 
     const int row_w = m0 + wm * 32 * MSUB + 4 * q16;  // + 16 i + r: output row
     const int col_w = n0 + wn * 64 + r16;            // + 16 j: output column (W row)
-    if (p.split > 1 && (p.split_all || mt == p.m_full)) {
+    if (li >= 0 || (p.split > 1 && (p.split_all || mt == p.m_full))) {
         // Split tile: store this part's FP32 partial; split_reduce_kernel, the next
         // launch on the stream, adds the parts and applies the epilogue.
-        const int rows = p.split_all ? BM : 64 * p.tail_sub;
-        float* base = p.split_all ? p.part + (((size_t)mt * p.n_tiles + nt) * p.split + part) * BM * BN
-                                  : p.part + ((size_t)nt * p.split + part) * rows * BN;
+        const int rows = (li >= 0 || p.split_all) ? BM : 64 * p.tail_sub;
+        float* base = li >= 0       ? p.late_part + ((size_t)li * p.late_split + part) * BM * BN
+                      : p.split_all ? p.part + (((size_t)mt * p.n_tiles + nt) * p.split + part) * BM * BN
+                                    : p.part + ((size_t)nt * p.split + part) * rows * BN;
 #pragma unroll
         for (int i = 0; i < 2 * MSUB; ++i)
 #pragma unroll
@@ -426,12 +478,12 @@ template <typename T, typename OutT, int EPI>
 __global__ void __launch_bounds__(512, 1) kernel(Params p)
 {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
-    int mt, nt, part;
-    tile_of(p, blockIdx.x, mt, nt, part);
-    if (mt < p.m_full) tile<T, OutT, EPI, 4>(p, mt, nt, part, smem);
-    else if (p.tail_sub == 1) tile<T, OutT, EPI, 1>(p, mt, nt, part, smem);
-    else if (p.tail_sub == 2) tile<T, OutT, EPI, 2>(p, mt, nt, part, smem);
-    else tile<T, OutT, EPI, 3>(p, mt, nt, part, smem);
+    int mt, nt, part, li;
+    tile_of(p, blockIdx.x, mt, nt, part, li);
+    if (mt < p.m_full) tile<T, OutT, EPI, 4>(p, mt, nt, part, li, smem);
+    else if (p.tail_sub == 1) tile<T, OutT, EPI, 1>(p, mt, nt, part, li, smem);
+    else if (p.tail_sub == 2) tile<T, OutT, EPI, 2>(p, mt, nt, part, li, smem);
+    else tile<T, OutT, EPI, 3>(p, mt, nt, part, li, smem);
 }
 
 }  // namespace pingpong
@@ -495,8 +547,29 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
         p.split = sp;
         p.part = static_cast<float*>(a.split_ws);
     }
+    // A last round of workgroups at most half full (the full tiles modulo one per
+    // CU): split those tiles along K so that round fills the CUs with shorter
+    // items. Their partials follow the tail row's in the workspace.
+    p.late = 0;
+    p.late_split = 1;
+    p.late_part = nullptr;
+    const int full = p.m_full * p.n_tiles;
+    const int last_round = full % kSplitTargetItems;
+    if (!p.split_all && a.split_ws && full > kSplitTargetItems && last_round <= kSplitTargetItems / 2 && last_round > 0) {
+        const size_t tail_bytes =
+            p.tail_sub ? ((size_t)p.split * p.n_tiles * 64 * p.tail_sub * pingpong::BN * sizeof(float) + 255) / 256 * 256 : 0;
+        const size_t per_part = (size_t)last_round * pingpong::BM * pingpong::BN * sizeof(float);
+        int sp = std::min(kMaxSplit, kSplitTargetItems / last_round);
+        sp = std::min(sp, std::max(1, a.K / pingpong::BK / 4));
+        while (sp > 1 && tail_bytes + (size_t)sp * per_part > a.split_ws_bytes) --sp;
+        if (sp > 1) {
+            p.late = last_round;
+            p.late_split = sp;
+            p.late_part = reinterpret_cast<float*>(static_cast<char*>(a.split_ws) + tail_bytes);
+        }
+    }
     const int tiles = p.split_all ? m_tiles * p.n_tiles * p.split
-                                  : p.m_full * p.n_tiles + (p.tail_sub ? p.n_tiles * p.split : 0);
+                                  : full - p.late + p.late * p.late_split + (p.tail_sub ? p.n_tiles * p.split : 0);
     const dim3 grid(tiles), block(512);
 #define EHIP_PINGPONG(T)                                                                                            \
     do {                                                                                                      \
@@ -514,8 +587,10 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     if (a.dtype == DT_F16) EHIP_PINGPONG(f16);
     else EHIP_PINGPONG(bf16);
 #undef EHIP_PINGPONG
-    if (p.split > 1) {
-        const long items = (long)(p.split_all ? a.M : 64 * p.tail_sub) * (epi_glu(a.epilogue) ? a.N / 2 : a.N);
+    if (p.split > 1 || p.late) {
+        const long cols = epi_glu(a.epilogue) ? a.N / 2 : a.N;
+        const long items = (p.split > 1 ? (long)(p.split_all ? a.M : 64 * p.tail_sub) * cols : 0) +
+                           (long)p.late * pingpong::BM * (epi_glu(a.epilogue) ? pingpong::BN / 2 : pingpong::BN);
         const dim3 rgrid((unsigned)((items + 255) / 256)), rblock(256);
 #define EHIP_REDUCE(OUT, EPI) hipLaunchKernelGGL((pingpong::split_reduce_kernel<OUT, EPI>), rgrid, rblock, 0, s, p)
         if (a.epilogue == EPI_STORE) {

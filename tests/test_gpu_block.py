@@ -39,6 +39,25 @@ def test_block_small_against_oracle(ctx, dt):
     assert g2["passed"], g2
 
 
+@pytest.mark.parametrize("dt", [E.FP16, E.BF16], ids=lambda d: NAMES[d])
+def test_block_last_round_split_against_oracle(ctx, dt):
+    # Width 1024 (8 heads), FFN 4096, S = 2368 = 9 x 256 + 64 (48 x 44 image tokens,
+    # 256 text slots, 200 valid). The up/gate GEMM has 9 x 32 = 288 full 256 x 256
+    # tiles, 32 more than one round of 256 workgroups: those 32 are split along K,
+    # next to the split 64-row tail row. The narrower projections split every tile.
+    dim, ffn = 1024, 4096
+    w = small_block(dim=dim, ffn=ffn, seed=7)
+    x, mods, cos, sin, mask = small_inputs(S=2368, dim=dim, image=(48, 44), valid=200, seed=8)
+    ctx.block_upload(5, w, dim, ffn, dt)
+    valid = int(np.sum(mask == 0))
+    got = run_block(ctx, 5, x, mods, cos, sin, mask, valid)
+    ref = O.block_forward(w, x, mods, cos, sin, mask)
+    g = kat.gate(got, ref, *kat.BLOCK_GATES[NAMES[dt]])
+    assert g["passed"], g
+    np.testing.assert_array_equal(run_block(ctx, 5, x, mods, cos, sin, mask, valid), got)  # repeat-deterministic
+    ctx.call("block_release", 5)
+
+
 @pytest.mark.parametrize("dt", ALL_DT, ids=lambda d: NAMES[d])
 def test_block_config0_against_oracle(ctx, dt):
     # One ERNIE block at full width (4096, 32 heads, FFN 12288), S = 1056

@@ -84,10 +84,12 @@ def full_text_block():
 
 
 @pytest.mark.parametrize("dt", ALL_DT, ids=lambda d: NAMES[d])
-@pytest.mark.parametrize("S", [64, 33])
+@pytest.mark.parametrize("S", [64, 33, 2048])
 def test_text_block_full_width_against_oracle(ctx, full_text_block, dt, S):
     # S = 64 is a reference text bucket (tests/fixtures/text-s64.ncnn.param); 33 leaves
-    # a ragged key tile. x ~ 0.2 N(0, 1) as tools/export_text_block.py:74.
+    # a ragged key tile; at 2048 the up/gate GEMM has 8 x 72 = 576 tiles, so its last
+    # 64 run split along K, and the o_proj / down GEMMs split every tile. x ~ 0.2 N(0, 1)
+    # as tools/export_text_block.py:74.
     w = full_text_block
     ctx.text_block_upload(3, w, 3072, 32, 8, 9216, dt)
     cos, sin, mask = O.text_constants(yarn_like_frequencies(), S)
