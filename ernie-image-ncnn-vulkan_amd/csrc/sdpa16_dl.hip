@@ -19,8 +19,10 @@
 //     way in. Key rows at or past the valid-key bound lie past the buffer range and
 //     load as zeros.
 //   * Software pipeline: while the matrix cores compute S of tile i+1, the VALU turns
-//     S of tile i into probabilities (sched_group_barrier interleaves the two), then
-//     P_i V_i accumulates and tile i+1's maximum is taken.
+//     S of tile i into probabilities, in 16 hand-ordered groups (K fragment n + 2
+//     read, fragment n awaited, MFMA n, two probabilities) that sched_barrier keeps
+//     in order; then P_i V_i accumulates and tile i+1's maximum is taken. The LDS
+//     reads are inline assembly with explicit lgkmcnt waits (see ds_read_tr).
 //   * Row sums use v_dot2_f32_{f16,bf16} on the rounded probabilities the MFMA
 //     consumes, so numerator and denominator see the same weights.
 //   * V^T fragments come from ds_read_b64_tr_b16: within each 16-lane group, lane
@@ -128,13 +130,8 @@ template <> struct Mfma<f16> {
         for (int i = 0; i < 8; i += 2) acc = __builtin_amdgcn_fdot2(f16x2{p[i], p[i + 1]}, one, acc, false);
         return acc;
     }
-    typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 tr4;
     static __device__ __forceinline__ f32x16 run(vec a, vec b, f32x16 c)
     { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
-    static __device__ __forceinline__ u32x2 tr(const void* p)
-    {
-        return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) tr4*)p));
-    }
 };
 template <> struct Mfma<bf16> {
     typedef bf16x8 vec;
@@ -145,13 +142,8 @@ template <> struct Mfma<bf16> {
         for (int i = 0; i < 8; i += 2) acc = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{p[i], p[i + 1]}, one, acc, false);
         return acc;
     }
-    typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 tr4;
     static __device__ __forceinline__ f32x16 run(vec a, vec b, f32x16 c)
     { return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0); }
-    static __device__ __forceinline__ u32x2 tr(const void* p)
-    {
-        return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) tr4*)p));
-    }
 };
 
 // K rows: 16-byte chunk c of key row r at physical chunk c ^ (r & 15).
