@@ -656,6 +656,10 @@ int head_gemm(ernie_hip_ctx* ctx, const void* a, const void* w, const float* bia
     GemmArgs g;
     g.A = a; g.lda = K; g.W = w; g.ldw = K; g.M = M; g.N = N; g.K = K; g.dtype = dt;
     g.epilogue = EPI_STORE; g.C = c; g.ldc = N; g.c_dtype = ERNIE_DTYPE_FP32; g.bias = bias;
+    // The split-K scratch lets the narrow projections (4096 -> 128 output channels: 16
+    // tiles; the text rows: one partial row of tiles) spread over the CUs.
+    int rc = split_workspace(ctx, M, 1, &g.split_ws, &g.split_ws_bytes);
+    if (rc) return rc;
     Timed t(ctx, P_HEADS, 2.0 * M * N * K, gemm_bytes(M, N, K, (double)esize(dt), 4));
     return kernel_status(ctx, gemm(g, ctx->stream), "head gemm");
 }

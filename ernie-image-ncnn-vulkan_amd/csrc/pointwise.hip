@@ -422,6 +422,43 @@ __global__ void __launch_bounds__(256) gemv_kernel(const T* __restrict__ W, cons
     if (lane == 0) y[n] = acc + (b ? b[n] : 0.f);
 }
 
+// Four outputs per wave, 16 per workgroup, for K a multiple of 8 with 16-bit W: each
+// lane reads 16 bytes of each of its wave's four W rows per step (one 1-KiB request
+// per row and wave) and the matching eight x values (SiLU'd on the fly), which stay
+// in L1 / L2 across the waves; no LDS staging of x per workgroup.
+template <typename T>
+__global__ void __launch_bounds__(256) gemv4_kernel(const T* __restrict__ W, const float* __restrict__ b,
+                                                    const float* __restrict__ x, int N, int K, int silu,
+                                                    float* __restrict__ y)
+{
+    typedef T t8 __attribute__((ext_vector_type(8)));
+    const int lane = threadIdx.x & 63;
+    const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 4;
+    if (n0 >= N) return;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int k = lane * 8; k < K; k += 512) {
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(x + k), x1 = *reinterpret_cast<const f32x4*>(x + k + 4);
+        float xv[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        if (silu) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xv[e] = xv[e] / (1.0f + expf(-xv[e]));
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            if (n0 + r < N) {
+                const t8 w = *reinterpret_cast<const t8*>(W + (size_t)(n0 + r) * K + k);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[r] += float(w[e]) * xv[e];
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float v = wave_sum(acc[r]);
+        if (lane == 0 && n0 + r < N) y[n0 + r] = v + (b ? b[n0 + r] : 0.f);
+    }
+}
+
 template <typename T>
 __global__ void transpose_tokens_kernel(const float* __restrict__ latent, int ch, int hw, T* __restrict__ out)
 {
@@ -664,6 +701,15 @@ int fill_normal(void* out, int dt, size_t n, uint64_t seed, uint64_t offset, flo
 int gemv(const void* W, int wdt, const float* b, const float* x, int N, int K, int silu, float* y, hipStream_t s)
 {
     if (!W || !x || !y || N < 1 || K < 1 || K > 16384) return -1;
+    if (wdt != DT_F32 && K % 8 == 0 && reinterpret_cast<uintptr_t>(W) % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0) {
+        const dim3 grid4((N + 15) / 16), block4(256);
+        if (wdt == DT_F16)
+            hipLaunchKernelGGL(gemv4_kernel<f16>, grid4, block4, 0, s, static_cast<const f16*>(W), b, x, N, K, silu, y);
+        else if (wdt == DT_BF16)
+            hipLaunchKernelGGL(gemv4_kernel<bf16>, grid4, block4, 0, s, static_cast<const bf16*>(W), b, x, N, K, silu, y);
+        else return -1;
+        return launch_status();
+    }
     const dim3 grid((N + 3) / 4), block(256);
     const size_t lds = sizeof(float) * K;
     if (wdt == DT_F32)
