@@ -155,6 +155,33 @@ def test_heads_against_oracle(ctx, dt):
     assert g["passed"], g
 
 
+@pytest.mark.parametrize("dt", [E.FP16, E.BF16], ids=lambda d: NAMES[d])
+def test_heads_full_size_against_oracle(ctx, dt):
+    # The 1024x1024 heads: 64x64 latent tokens and 64 text rows at width 4096. The
+    # 4096 -> 128 output projection has 16 tiles and splits every tile along K; the
+    # 64 text rows are one split partial row of tiles; the time MLP and both adaLN
+    # projections run in the four-row GEMV.
+    dim = 4096
+    hw_ = heads_for(dim)
+    ctx.heads_upload(hw_, dim, 128, 3072, dt)
+    latent = O.normal((128, 64, 64), 13)
+    text = O.normal((64, 3072), 14)
+    feat = O.timestep_features(875.0)[:dim].copy()
+    S = 4096 + 64
+    x, c, mods = empty((S, dim)), empty((dim,)), empty((6, dim))
+    ctx.input_head(dev(latent), 4096, dev(text), 64, dev(feat), x, c, mods)
+    xr, cr, mr = O.input_head({k: hw_[k] for k in O.INPUT_HEAD_FIELDS}, latent, text, feat)
+    gates = kat.HEAD_GATES[NAMES[dt]]
+    for got, ref in ((x, xr), (c, cr), (mods, mr)):
+        g = kat.gate(host(got), ref, *gates)
+        assert g["passed"], g
+    pred = empty((128, 4096))
+    ctx.output_head(dev(xr), S, 4096, dev(cr), pred)
+    out_w = {"mod_w": hw_["out_mod_w"], "mod_b": hw_["out_mod_b"], "proj_w": hw_["proj_w"], "proj_b": hw_["proj_b"]}
+    g = kat.gate(host(pred), O.output_head(out_w, xr, cr, 4096), *gates)
+    assert g["passed"], g
+
+
 def oracle_dit(blocks_w, heads_w, latent, text, feat, cos, sin, mask):
     x, c, mods = O.input_head({k: heads_w[k] for k in O.INPUT_HEAD_FIELDS}, latent, text, feat)
     for w in blocks_w:
