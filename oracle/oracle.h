@@ -2,8 +2,8 @@
 //
 // CPU oracle for the ERNIE-Image DiT block path.
 //
-// TEST INFRASTRUCTURE ONLY. This library is the checker for the HIP
-// implementation: only the test suite, the smoke check and the CPU-baseline
+// TEST INFRASTRUCTURE ONLY. The HIP implementation is compared against this
+// library: only the test suite, the smoke check and the CPU-baseline
 // leg of the benchmark may load it. The product library never links it and
 // never falls back to it.
 //

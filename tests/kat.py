@@ -38,7 +38,7 @@ def gate(actual, ref, atol, rtol, nrmse):
     return m
 
 
-def north_star_fp32(actual, ref):
+def fp32_block_rule(actual, ref):
     """FP32 block rule: max |d| <= 1e-4 * max |ref|."""
     m = metrics(actual, ref)
     m["passed"] = m["finite"] and m["max_abs_error"] <= 1e-4 * m["reference_max_abs"]

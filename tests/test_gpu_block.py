@@ -32,7 +32,7 @@ def test_block_small_against_oracle(ctx, dt):
     g = kat.gate(got, ref, *kat.BLOCK_GATES[NAMES[dt]])
     assert g["passed"], g
     if dt == E.FP32:
-        assert kat.north_star_fp32(got, ref)["passed"]
+        assert kat.fp32_block_rule(got, ref)["passed"]
     # The mask alone (valid_keys = 0) and the count alone give the same block.
     again = run_block(ctx, 0, x, mods, cos, sin, mask, 0)
     g2 = kat.gate(again, ref, *kat.BLOCK_GATES[NAMES[dt]])
@@ -71,7 +71,7 @@ def test_block_config0_against_oracle(ctx, dt):
     g = kat.gate(got, ref, *kat.BLOCK_GATES[NAMES[dt]])
     assert g["passed"], g
     if dt == E.FP32:
-        m = kat.north_star_fp32(got, ref)
+        m = kat.fp32_block_rule(got, ref)
         assert m["passed"], m
     # Repeat-determinism (probes/block_runner.cpp:196-203): bitwise identical.
     np.testing.assert_array_equal(run_block(ctx, 1, x, mods, cos, sin, mask, 1056), got)
@@ -273,7 +273,7 @@ def test_facade_block_sequence_validation_and_parity():
     secs = fac.run_block_sequence([0], dev(x), 40, dim, md, dev(cos), dev(sin), out, mask=dev(mask),
                                   valid_prefix=valid)
     assert secs.shape == (1,) and secs[0] > 0
-    m = kat.north_star_fp32(host(out), O.block_forward(w, x, mods, cos, sin, mask))
+    m = kat.fp32_block_rule(host(out), O.block_forward(w, x, mods, cos, sin, mask))
     assert m["passed"], m
     with pytest.raises(E.ErnieInvalidRequest):
         fac.run_block_sequence([0] * 37, dev(x), 40, dim, md, dev(cos), dev(sin), out)

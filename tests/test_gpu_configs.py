@@ -59,7 +59,7 @@ def test_long_text_fp32_per_block(ctx):
         t0 = time.perf_counter()
         ref = O.block_forward(small_block(DIM, FFN, seed=4, block=b), cur, mods, cos, sin, mask)
         print(f"block {b}: oracle {time.perf_counter() - t0:.1f} s", flush=True)
-        m = kat.north_star_fp32(got, ref)
+        m = kat.fp32_block_rule(got, ref)
         assert m["passed"], (b, m)
         g = kat.gate(got, ref, *kat.BLOCK_GATES["fp32"])
         assert g["passed"], (b, g)

@@ -99,7 +99,7 @@ def test_text_block_full_width_against_oracle(ctx, full_text_block, dt, S):
     g = kat.gate(got, ref, *kat.TEXT_GATES[NAMES[dt]])
     assert g["passed"], g
     if dt == E.FP32:
-        m = kat.north_star_fp32(got, ref)
+        m = kat.fp32_block_rule(got, ref)
         assert m["passed"], m
     np.testing.assert_array_equal(run_text_block(ctx, 3, x, cos, sin, mask), got)  # repeat-deterministic
     # Causal by position instead of the mask tensor.

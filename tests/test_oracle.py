@@ -265,7 +265,7 @@ def test_block_matches_torch_fp64():
     x, mods, cos, sin, mask = small_inputs()
     out = O.block_forward(w, x, mods, cos, sin, mask)
     ref = torch_block_fp64(w, x, mods, cos, sin, mask)
-    m = kat.north_star_fp32(out, ref)
+    m = kat.fp32_block_rule(out, ref)
     assert m["passed"] and m["nrmse"] < 2e-6, m
 
 

@@ -86,7 +86,7 @@ def test_text_block_oracle_matches_torch_fp64():
     x = O.normal((S, HIDDEN), 31, std=0.2)
     out = O.text_block_forward(w, x, cos, sin, mask, HEADS, KV_HEADS)
     ref = torch_text_block_fp64(w, x, cos, sin, mask, HEADS, KV_HEADS)
-    m = kat.north_star_fp32(out, ref)
+    m = kat.fp32_block_rule(out, ref)
     assert m["passed"] and m["nrmse"] < 2e-6, m
 
 
