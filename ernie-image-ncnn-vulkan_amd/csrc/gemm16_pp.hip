@@ -74,6 +74,10 @@ struct Params {
     // the CUs with shorter items. Partials [late][late_split][BM][BN] at late_part.
     int late, late_split;
     float* late_part;
+    // vec: every output row, residual row and the gate / bias vectors start 16-byte
+    // aligned (8-byte for 16-bit outputs) and N % 4 == 0, so a lane's four consecutive
+    // columns move as one vector; else element by element.
+    int vec;
 };
 
 // Full tile f of the tile order -> (mt, nt): GM M tiles per N sweep, so the
@@ -176,9 +180,10 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(Params p)
 }
 
 template <typename T> struct Mfma;
-// 16 x 16 x 32 MFMA. Operands: lane l supplies row l % 16, k = 8 (l / 16) .. + 7
-// (A: output rows, B: output columns = W rows). Result: lane l holds column l % 16,
-// register r row 4 (l / 16) + r.
+// 16 x 16 x 32 MFMA D = X Y^T. Operands: lane l supplies row l % 16 of X or Y,
+// k = 8 (l / 16) .. + 7. Result: lane l holds D column l % 16 (a row of Y), register
+// r D row 4 (l / 16) + r (a row of X). The tile passes W as X and A as Y, so a lane
+// holds one output row and four consecutive output columns: 8- or 16-byte stores.
 template <> struct Mfma<f16> {
     typedef f16x8 vec;
     static __device__ __forceinline__ f32x4 run(vec a, vec b, f32x4 c)
@@ -315,7 +320,7 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
     const int r16 = lane & 15, q16 = lane >> 4;
     const uint32_t frag = r16 * ROWB + ((q16 ^ fsw(r16)) << 4);
 
-    // acc[i][j]: rows 16i + 4 q16 + r of this wave's 32 MSUB rows, column 16j + r16
+    // acc[i][j][r]: row 16i + r16 of this wave's 32 MSUB rows, column 16j + 4 q16 + r
     // of its 64 columns.
     f32x4 acc[2 * MSUB][4];
 #pragma unroll
@@ -341,7 +346,7 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
 #pragma unroll
         for (int i = 0; i < 2 * MSUB; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = Mfma<T>::run(af[i], bf[j], acc[i][j]);
+            for (int j = 0; j < 4; ++j) acc[i][j] = Mfma<T>::run(bf[j], af[i], acc[i][j]);
     };
     // Loads requested after stage s, per wave, when s must have landed: 4 x min(NS-2, nk-1-s).
     auto wait_stage = [&](int s) { wait_vm(4 * min(NS - 2, nk - 1 - s)); };
@@ -382,8 +387,8 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
         }
     }
 
-    const int row_w = m0 + wm * 32 * MSUB + 4 * q16;  // + 16 i + r: output row
-    const int col_w = n0 + wn * 64 + r16;            // + 16 j: output column (W row)
+    const int row_w = m0 + wm * 32 * MSUB + r16;  // + 16 i: output row
+    const int col_w = n0 + wn * 64 + 4 * q16;      // + 16 j + r: output column (W row)
     if (li >= 0 || (p.split > 1 && (p.split_all || mt == p.m_full))) {
         // Split tile: store this part's FP32 partial; split_reduce_kernel, the next
         // launch on the stream, adds the parts and applies the epilogue.
@@ -394,79 +399,100 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
 #pragma unroll
         for (int i = 0; i < 2 * MSUB; ++i)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int rl = row_w - m0 + 16 * i + r;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) base[(size_t)rl * BN + (col_w - n0) + 16 * j] = acc[i][j][r];
-            }
+            for (int j = 0; j < 4; ++j)
+                *reinterpret_cast<f32x4*>(base + (size_t)(row_w - m0 + 16 * i) * BN + (col_w - n0) + 16 * j) = acc[i][j];
         return;
     }
 
     if constexpr (EPI == EPI_GATE_RESID) {
         // C = resid + gate * acc, C possibly aliasing resid. Each element is read and
         // written by this lane only, so the gate values and a 32-row block's residuals
-        // are loaded before any of the block's stores: 32 loads in flight per lane
-        // instead of one load-wait-store round trip per element.
-        float gv[4];
+        // are loaded before any of the block's stores: 8 loads of 16 bytes in flight
+        // per lane instead of one load-wait-store round trip per element.
+        float* C = static_cast<float*>(p.C);
+        if (p.vec) {
+            f32x4 gv[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int n = col_w + 16 * j;
-            gv[j] = n < p.N ? p.gate[n] : 0.f;
-        }
+            for (int j = 0; j < 4; ++j) {
+                const int n = col_w + 16 * j;
+                gv[j] = n < p.N ? *reinterpret_cast<const f32x4*>(p.gate + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+            }
 #pragma unroll
-        for (int i2 = 0; i2 < MSUB; ++i2) {
-            float rv[2][4][4];
+            for (int i2 = 0; i2 < MSUB; ++i2) {
+                f32x4 rv[2][4];
 #pragma unroll
-            for (int ii = 0; ii < 2; ++ii)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int m = row_w + 16 * (2 * i2 + ii) + r, n = col_w + 16 * j;
-                        rv[ii][r][j] = m < p.M && n < p.N ? p.resid[(size_t)m * p.ld_resid + n] : 0.f;
-                    }
-#pragma unroll
-            for (int ii = 0; ii < 2; ++ii)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
+                for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        const int m = row_w + 16 * (2 * i2 + ii) + r, n = col_w + 16 * j;
-                        if (m < p.M && n < p.N)
-                            static_cast<float*>(p.C)[(size_t)m * p.ldc + n] =
-                                __builtin_fmaf(gv[j], acc[2 * i2 + ii][j][r], rv[ii][r][j]);
+                        const int m = row_w + 16 * (2 * i2 + ii), n = col_w + 16 * j;
+                        rv[ii][j] = m < p.M && n < p.N ? *reinterpret_cast<const f32x4*>(p.resid + (size_t)m * p.ld_resid + n)
+                                                       : f32x4{0.f, 0.f, 0.f, 0.f};
                     }
+#pragma unroll
+                for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int m = row_w + 16 * (2 * i2 + ii), n = col_w + 16 * j;
+                        f32x4 o;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) o[r] = __builtin_fmaf(gv[j][r], acc[2 * i2 + ii][j][r], rv[ii][j][r]);
+                        if (m < p.M && n < p.N) *reinterpret_cast<f32x4*>(C + (size_t)m * p.ldc + n) = o;
+                    }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 2 * MSUB; ++i) {
+                const int m = row_w + 16 * i;
+                if (m >= p.M) continue;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int n = col_w + 16 * j + r;
+                        if (n < p.N)
+                            C[(size_t)m * p.ldc + n] = __builtin_fmaf(p.gate[n], acc[i][j][r], p.resid[(size_t)m * p.ld_resid + n]);
+                    }
+            }
         }
         return;
     }
+    typedef OutT out4 __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (int i = 0; i < 2 * MSUB; ++i) {
+        const int m = row_w + 16 * i;
+        if (m >= p.M) continue;
+        if (epi_glu(EPI)) {
+            // This wave's 64 W rows are 32 up rows then the 32 matching gate rows:
+            // output columns 32 g .. 32 g + 31, g = (n0 + 64 wn) / 64.
+            if (n0 + wn * 64 >= p.N) continue;
+            OutT* c = static_cast<OutT*>(p.C) + (size_t)m * p.c_rs + (size_t)((n0 + wn * 64) >> 6) * p.c_ss + 4 * q16;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = row_w + 16 * i + r;
-            if (m >= p.M) continue;
-            if (epi_glu(EPI)) {
-                // This wave's 64 W rows are 32 up rows then the 32 matching gate rows:
-                // output columns 32 g .. 32 g + 31, g = (n0 + 64 wn) / 64.
-                const size_t cg = (size_t)((n0 + wn * 64) >> 6) * p.c_ss;
+            for (int j = 0; j < 2; ++j) {
+                out4 o;
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    if (n0 + wn * 64 < p.N)
-                        static_cast<OutT*>(p.C)[(size_t)m * p.c_rs + cg + 16 * j + r16] =
-                            OutT(acc[i][j][r] * glu_act<EPI == EPI_SWIGLU>(acc[i][j + 2][r]));
-                }
-            } else {
+                for (int r = 0; r < 4; ++r) o[r] = OutT(acc[i][j][r] * glu_act<EPI == EPI_SWIGLU>(acc[i][j + 2][r]));
+                if (p.vec) *reinterpret_cast<out4*>(c + 16 * j) = o;
+                else
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int n = col_w + 16 * j;
-                    if (n >= p.N) continue;
-                    float v = acc[i][j][r];
-                    if (EPI == EPI_STORE) {
-                        if (p.bias) v += p.bias[n];
-                        static_cast<OutT*>(p.C)[(size_t)m * p.ldc + n] = OutT(v);
-                    } else {
-                        const float rr = p.resid[(size_t)m * p.ld_resid + n];
-                        static_cast<float*>(p.C)[(size_t)m * p.ldc + n] = rr + p.gate[n] * v;
+                    for (int r = 0; r < 4; ++r) c[16 * j + r] = o[r];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int n = col_w + 16 * j;
+                if (n >= p.N) continue;
+                OutT* c = static_cast<OutT*>(p.C) + (size_t)m * p.ldc + n;
+                if (p.vec) {
+                    f32x4 v = acc[i][j];
+                    if (p.bias) v += *reinterpret_cast<const f32x4*>(p.bias + n);
+                    *reinterpret_cast<out4*>(c) = out4{OutT(v[0]), OutT(v[1]), OutT(v[2]), OutT(v[3])};
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        if (n + r >= p.N) continue;
+                        float v = acc[i][j][r];
+                        if (p.bias) v += p.bias[n + r];
+                        c[r] = OutT(v);
                     }
                 }
             }
@@ -514,6 +540,15 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     p.a_kstep = a.a_k32_rows ? a.a_k32_rows * pingpong::ROWB : pingpong::ROWB;
     p.c_rs = a.c_k32_rows ? 32 : a.ldc;
     p.c_ss = a.c_k32_rows ? 32L * a.c_k32_rows : 32;
+    {
+        auto aligned = [](const void* q, size_t b) { return (uintptr_t)q % b == 0; };
+        const size_t out_bytes = a.epilogue == EPI_GATE_RESID || a.c_dtype == DT_F32 ? 4 : 2;
+        bool v = aligned(a.C, 4 * out_bytes) && a.N % 4 == 0 &&
+                 (epi_glu(a.epilogue) ? p.c_rs % 4 == 0 && p.c_ss % 4 == 0 : a.ldc % 4 == 0);
+        if (a.epilogue == EPI_STORE && a.bias) v = v && aligned(a.bias, 16);
+        if (a.epilogue == EPI_GATE_RESID) v = v && aligned(a.resid, 16) && aligned(a.gate, 16) && a.ld_resid % 4 == 0;
+        p.vec = v;
+    }
     p.w_bytes = (uint32_t)((long)a.N * a.ldw * 2);
     p.w_row_bytes = a.w_k32 ? pingpong::ROWB : (int)(a.ldw * 2);
     p.w_kstep = a.w_k32 ? a.N * pingpong::ROWB : pingpong::ROWB;
