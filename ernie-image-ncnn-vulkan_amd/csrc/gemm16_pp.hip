@@ -78,6 +78,7 @@ struct Params {
     // aligned (8-byte for 16-bit outputs) and N % 4 == 0, so a lane's four consecutive
     // columns move as one vector; else element by element.
     int vec;
+    int items;  // work items (tiles and tile parts); workgroup b takes items b, b + grid, ...
 };
 
 // Full tile f of the tile order -> (mt, nt): GM M tiles per N sweep, so the
@@ -275,8 +276,17 @@ __device__ __forceinline__ void wait_vm(int n)
     else __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
 }
 
+__device__ __forceinline__ int item_parts(const Params& p, int mt, int li)
+{
+    return (p.split_all || mt == p.m_full) ? p.split : (li >= 0 ? p.late_split : 1);
+}
+
+// One work item. `pre`: its first NS stages were requested by the previous item of this
+// workgroup. nmt >= 0 names the next item (nmt, nnt, npart, nli), whose first NS stages
+// this one requests once its own ring is drained, before its epilogue.
 template <typename T, typename OutT, int EPI, int MSUB>
-__device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, int li, uint8_t* smem)
+__device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, int li, uint8_t* smem, bool pre,
+                                     int nmt, int nnt, int npart, int nli)
 {
     typedef typename Mfma<T>::vec vec8;
     const int m0 = mt * BM, n0 = nt * BN;
@@ -292,29 +302,34 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
     // with two 1-KiB instructions each; lane l lands at bytes [16l, 16l+16), i.e.
     // row (l >> 2), physical chunk l & 3 = logical chunk (l & 3) ^ fsw(row).
     uint32_t a_src[2], w_src[2];
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-        const int row = wave * 32 + q * 16 + (lane >> 2);
-        const int c = (lane & 3) ^ fsw(row);
-        a_src[q] = (uint32_t)((long)(m0 + row) * p.a_row_bytes + c * 16);
-        w_src[q] = (uint32_t)((long)(n0 + row) * p.w_row_bytes + c * 16);
-    }
-    // K steps of this item: all of them, or part `part` of `split` for a tail tile.
-    const int nk_all = p.K / BK;
-    const int parts = (p.split_all || mt == p.m_full) ? p.split : (li >= 0 ? p.late_split : 1);
-    const int kt0 = (int)((long)nk_all * part / parts);
-    const int nk = (int)((long)nk_all * (part + 1) / parts) - kt0;
-    auto issue = [&](int kt) {
-        uint8_t* st = smem + (kt & (NS - 1)) * STAGE;
-        const int koff = (kt0 + kt) * p.a_kstep, koff_w = (kt0 + kt) * p.w_kstep;
+    auto sources = [&](int m_0, int n_0, uint32_t* as, uint32_t* ws) {
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(st + (wave * 32 + q * 16) * ROWB), 16, a_src[q],
-                                                     koff, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(st + A_BYTES + (wave * 32 + q * 16) * ROWB), 16,
-                                                     w_src[q], koff_w, 0, 0);
+            const int row = wave * 32 + q * 16 + (lane >> 2);
+            const int c = (lane & 3) ^ fsw(row);
+            as[q] = (uint32_t)((long)(m_0 + row) * p.a_row_bytes + c * 16);
+            ws[q] = (uint32_t)((long)(n_0 + row) * p.w_row_bytes + c * 16);
         }
     };
+    sources(m0, n0, a_src, w_src);
+    // K steps of this item: all of them, or part `part` of `split` for a tail tile.
+    const int nk_all = p.K / BK;
+    const int parts = item_parts(p, mt, li);
+    const int kt0 = (int)((long)nk_all * part / parts);
+    const int nk = (int)((long)nk_all * (part + 1) / parts) - kt0;
+    // Stage kt (of the item starting at K step k0) into ring slot kt % NS.
+    auto issue_at = [&](const uint32_t* as, const uint32_t* ws, int k0, int kt) {
+        uint8_t* st = smem + (kt & (NS - 1)) * STAGE;
+        const int koff = (k0 + kt) * p.a_kstep, koff_w = (k0 + kt) * p.w_kstep;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(st + (wave * 32 + q * 16) * ROWB), 16, as[q],
+                                                     koff, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(st + A_BYTES + (wave * 32 + q * 16) * ROWB), 16,
+                                                     ws[q], koff_w, 0, 0);
+        }
+    };
+    auto issue = [&](int kt) { issue_at(a_src, w_src, kt0, kt); };
 
     // Fragment of 16 rows x 32 k: lane l reads row l % 16, logical chunk l / 16.
     const int r16 = lane & 15, q16 = lane >> 4;
@@ -351,11 +366,17 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
     // Loads requested after stage s, per wave, when s must have landed: 4 x min(NS-2, nk-1-s).
     auto wait_stage = [&](int s) { wait_vm(4 * min(NS - 2, nk - 1 - s)); };
 
-    // Prologue: request stages 0..NS-1, wait for stage 0 everywhere.
+    // Prologue: request stages 0..NS-1 (unless the previous item did), wait for stage 0
+    // everywhere. After a previous item, its epilogue's stores are counted too: wait
+    // for everything.
+    if (!pre) {
 #pragma unroll
-    for (int s = 0; s < NS; ++s)
-        if (s < nk) issue(s);
-    wait_vm(4 * min(NS - 1, nk - 1));
+        for (int s = 0; s < NS; ++s)
+            if (s < nk) issue(s);
+        wait_vm(4 * min(NS - 1, nk - 1));
+    } else {
+        wait_vm(0);
+    }
     phase_barrier();
 
     // Phase 2t+1: group 0 computes stage t, group 1 reads stage t and requests
@@ -385,6 +406,19 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
             mfma_cluster();
             phase_barrier();  // end of phase 2t+2
         }
+    }
+
+    // The last barrier above follows every wave's last LDS read: the ring is free for
+    // the next item's first stages, which then land during this epilogue.
+    if (nmt >= 0) {
+        const int nparts = item_parts(p, nmt, nli);
+        const int nkt0 = (int)((long)nk_all * npart / nparts);
+        const int nnk = (int)((long)nk_all * (npart + 1) / nparts) - nkt0;
+        uint32_t na[2], nw[2];
+        sources(nmt * BM, nnt * BN, na, nw);
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+            if (s < nnk) issue_at(na, nw, nkt0, s);
     }
 
     const int row_w = m0 + wm * 32 * MSUB + r16;  // + 16 i: output row
@@ -504,15 +538,40 @@ template <typename T, typename OutT, int EPI>
 __global__ void __launch_bounds__(512, 1) kernel(Params p)
 {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
-    int mt, nt, part, li;
-    tile_of(p, blockIdx.x, mt, nt, part, li);
-    if (mt < p.m_full) tile<T, OutT, EPI, 4>(p, mt, nt, part, li, smem);
-    else if (p.tail_sub == 1) tile<T, OutT, EPI, 1>(p, mt, nt, part, li, smem);
-    else if (p.tail_sub == 2) tile<T, OutT, EPI, 2>(p, mt, nt, part, li, smem);
-    else tile<T, OutT, EPI, 3>(p, mt, nt, part, li, smem);
+    // Items blockIdx.x, + gridDim.x, ...: with gridDim.x a multiple of 8 every item of
+    // a workgroup maps to the XCD its blockIdx.x runs on.
+    int bid = blockIdx.x, mt, nt, part, li;
+    tile_of(p, bid, mt, nt, part, li);
+    bool pre = false;
+    for (;;) {
+        const int nb = bid + (int)gridDim.x;
+        int nmt = -1, nnt = 0, npart = 0, nli = -1;
+        if (nb < p.items) tile_of(p, nb, nmt, nnt, npart, nli);
+        if (mt < p.m_full) tile<T, OutT, EPI, 4>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli);
+        else if (p.tail_sub == 1) tile<T, OutT, EPI, 1>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli);
+        else if (p.tail_sub == 2) tile<T, OutT, EPI, 2>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli);
+        else tile<T, OutT, EPI, 3>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli);
+        if (nb >= p.items) break;
+        bid = nb; mt = nmt; nt = nnt; part = npart; li = nli;
+        pre = true;
+    }
 }
 
 }  // namespace pingpong
+
+// CUs of the current device, rounded down to a multiple of 8 (one per XCD slot).
+static int cu_count()
+{
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 8) n = 256;
+        cached[dev] = n / 8 * 8;
+    }
+    return cached[dev];
+}
 
 int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
 {
@@ -605,7 +664,9 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     }
     const int tiles = p.split_all ? m_tiles * p.n_tiles * p.split
                                   : full - p.late + p.late * p.late_split + (p.tail_sub ? p.n_tiles * p.split : 0);
-    const dim3 grid(tiles), block(512);
+    // One workgroup per CU (the LDS ring allows no second), each walking its items.
+    p.items = tiles;
+    const dim3 grid(std::min(tiles, cu_count())), block(512);
 #define EHIP_PINGPONG(T)                                                                                            \
     do {                                                                                                      \
         if (a.epilogue == EPI_STORE) {                                                                        \
