@@ -45,6 +45,9 @@ def parse():
     ap.add_argument("--valid-text", type=int, default=40)
     ap.add_argument("--cpu-baseline", choices=("on", "off"), default="on")
     ap.add_argument("--cpu-tokens", type=int, default=4160, help="tokens of the single-block CPU sample")
+    ap.add_argument("--event-stride", type=int, default=4,
+                    help="with --events dominant, bracket every n-th launch of the dominant class: each event "
+                         "record leaves a ~5.7 us hole in the queue, which sampling keeps out of the timed steps")
     ap.add_argument("--events", choices=("dominant", "all"), default="dominant",
                     help="HIP events in the timed steps: around the dominant kernel class only (its roofline), or "
                          "around every launch; the per-class table always comes from one extra profiled step")
@@ -232,9 +235,13 @@ def main():
     ctx.profile(False)
     table = ctx.profile_query()
     dom = max(mfma_cls, key=lambda c: table[c]["ms"])
-    # Timed steps: events bracket only the dominant class (or every launch with --events all).
+    # Timed steps: events bracket every --event-stride-th launch of the dominant class (or
+    # every launch with --events all); the roofline's launch duration is their average.
     ctx.profile_reset()
-    ctx.profile(True, classes=None if args.events == "all" else [dom])
+    if args.events == "all":
+        ctx.profile(True)
+    else:
+        ctx.profile(True, classes=[dom], stride=max(1, args.event_stride))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     step_s, _ = run(args.steps, 0)

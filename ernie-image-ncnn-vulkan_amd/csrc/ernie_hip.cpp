@@ -85,6 +85,8 @@ struct ernie_hip_ctx {
     // Event timing.
     bool profiling = false;
     unsigned profile_mask = ~0u;  // classes that record events while profiling
+    int profile_stride = 1;       // record every profile_stride-th launch of a class
+    long class_seen[32] = {};     // launches of each class since the last reset
     std::vector<hipEvent_t> event_pool;
     size_t event_next = 0;
     std::vector<Launch> pending;
@@ -184,7 +186,7 @@ struct Timed {
     hipEvent_t start = nullptr;
     Timed(ernie_hip_ctx* c, int k, double f, double b) : ctx(c), cls(k), flop(f), bytes(b)
     {
-        if (ctx->profiling && (ctx->profile_mask >> cls & 1u)) {
+        if (ctx->profiling && (ctx->profile_mask >> cls & 1u) && ctx->class_seen[cls]++ % ctx->profile_stride == 0) {
             start = next_event(ctx);
             if (start) (void)hipEventRecord(start, ctx->stream);
         }
@@ -1403,6 +1405,14 @@ int ernie_hip_profile_classes(ernie_hip_ctx* ctx, unsigned class_mask)
 {
     if (!ctx) return ERNIE_ERROR;
     ctx->profile_mask = class_mask;
+    return ERNIE_OK;
+}
+
+int ernie_hip_profile_stride(ernie_hip_ctx* ctx, int stride)
+{
+    if (!ctx || stride < 1) return ERNIE_ERROR;
+    ctx->profile_stride = stride;
+    for (long& n : ctx->class_seen) n = 0;
     return ERNIE_OK;
 }
 

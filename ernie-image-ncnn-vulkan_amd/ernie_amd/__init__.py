@@ -119,6 +119,7 @@ def hip():
                                               c_int, c_vp]),
             "ernie_hip_profile_enable": (c_int, [c_vp, c_int]),
             "ernie_hip_profile_classes": (c_int, [c_vp, ctypes.c_uint]),
+            "ernie_hip_profile_stride": (c_int, [c_vp, c_int]),
             "ernie_hip_profile_collect": (c_int, [c_vp]),
             "ernie_hip_profile_reset": (c_int, [c_vp]),
             "ernie_hip_profile_query": (c_int, [c_vp, c_int, ctypes.POINTER(c_long), ctypes.POINTER(c_double),
@@ -485,10 +486,12 @@ class Context:
                   ptr(mask), valid_keys, ctypes.cast(ids, c_vp), len(blocks), ptr(pred))
 
     # ---- profiling -----------------------------------------------------------
-    def profile(self, enable, classes=None):
-        """Event timing on/off; `classes` (names from PROFILE_CLASSES) limits which launches are bracketed."""
+    def profile(self, enable, classes=None, stride=1):
+        """Event timing on/off; `classes` (names from PROFILE_CLASSES) limits which launches are
+        bracketed, `stride` brackets only every stride-th launch of each of them."""
         mask = 0xFFFFFFFF if classes is None else sum(1 << PROFILE_CLASSES.index(c) for c in classes)
         self.call("profile_classes", mask)
+        self.call("profile_stride", stride)
         self.call("profile_enable", 1 if enable else 0)
 
     def profile_reset(self):

@@ -247,6 +247,10 @@ int ernie_hip_profile_enable(ernie_hip_ctx* ctx, int enable);
  * timed run brackets only the kernel it measures. No reference counterpart: the
  * reference times whole blocks on the host clock (src/block_sequence.cpp:83-88, 247-253). */
 int ernie_hip_profile_classes(ernie_hip_ctx* ctx, unsigned class_mask);
+/* Brackets only every `stride`-th launch of each recorded class (default 1: every one).
+ * Each event record leaves a few-microsecond hole in the queue, so a timed run samples
+ * a kernel's launches instead of bracketing all of them. No reference counterpart. */
+int ernie_hip_profile_stride(ernie_hip_ctx* ctx, int stride);
 /* Synchronises and folds recorded launches into the totals. */
 int ernie_hip_profile_collect(ernie_hip_ctx* ctx);
 int ernie_hip_profile_reset(ernie_hip_ctx* ctx);
