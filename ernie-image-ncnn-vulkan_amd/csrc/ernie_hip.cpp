@@ -7,6 +7,9 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <map>
+#include <mutex>
+#include <unordered_map>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -88,6 +91,14 @@ struct ernie_hip_ctx {
     int profile_stride = 1;       // record every profile_stride-th launch of a class
     long class_seen[32] = {};     // launches of each class since the last reset
     std::vector<hipEvent_t> event_pool;
+    // Freed device blocks kept for reuse, by size: hipFree synchronises the whole device,
+    // which drained the queue several times per denoise step. A reused block's earlier
+    // work was enqueued on this context's stream before any new work on it.
+    std::multimap<size_t, void*> free_cache;
+    std::unordered_map<void*, size_t> live;
+    size_t cached_bytes = 0;
+    std::mutex alloc_mu;
+    int* finite_flag = nullptr;
     size_t event_next = 0;
     std::vector<Launch> pending;
     long launches[ERNIE_PROFILE_CLASSES] = {};
@@ -778,6 +789,8 @@ void ernie_hip_destroy(ernie_hip_ctx* ctx)
     dev_free(ctx->dit_act);
     dev_free(ctx->split_ws);
     for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
+    for (auto& kv : ctx->free_cache) (void)hipFree(kv.second);
+    if (ctx->finite_flag) (void)hipFree(ctx->finite_flag);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
 }
@@ -787,6 +800,8 @@ const char* ernie_hip_last_error(const ernie_hip_ctx* ctx) { return ctx ? ctx->e
 int ernie_hip_set_stream(ernie_hip_ctx* ctx, void* stream)
 {
     if (!ctx) return ERNIE_ERROR;
+    // Cached blocks may still be in use by work on the old stream: let it finish first.
+    if (ctx->stream != static_cast<hipStream_t>(stream) && ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     ctx->stream = static_cast<hipStream_t>(stream);
     return ERNIE_OK;
 }
@@ -801,16 +816,50 @@ int ernie_hip_synchronize(ernie_hip_ctx* ctx)
     return hip_status(ctx, hipStreamSynchronize(ctx->stream), "synchronize");
 }
 
+// Freed blocks the cache keeps at most (larger frees go back to the driver).
+constexpr size_t kCacheCapBytes = size_t(8) << 30;
+
 int ernie_hip_malloc(ernie_hip_ctx* ctx, size_t bytes, void** out)
 {
     if (!ctx || !out) return ERNIE_ERROR;
     *out = nullptr;
-    return hip_status(ctx, hipMalloc(out, bytes ? bytes : 1), "malloc");
+    const size_t b = ((bytes ? bytes : 1) + 255) / 256 * 256;
+    {
+        std::lock_guard<std::mutex> lock(ctx->alloc_mu);
+        auto it = ctx->free_cache.find(b);
+        if (it != ctx->free_cache.end()) {
+            *out = it->second;
+            ctx->free_cache.erase(it);
+            ctx->cached_bytes -= b;
+            ctx->live[*out] = b;
+            return ERNIE_OK;
+        }
+    }
+    const int rc = hip_status(ctx, hipMalloc(out, b), "malloc");
+    if (!rc) {
+        std::lock_guard<std::mutex> lock(ctx->alloc_mu);
+        ctx->live[*out] = b;
+    }
+    return rc;
 }
 
 int ernie_hip_free(ernie_hip_ctx* ctx, void* ptr)
 {
     if (!ctx) return ERNIE_ERROR;
+    if (!ptr) return ERNIE_OK;
+    {
+        std::lock_guard<std::mutex> lock(ctx->alloc_mu);
+        auto it = ctx->live.find(ptr);
+        if (it != ctx->live.end()) {
+            const size_t b = it->second;
+            ctx->live.erase(it);
+            if (ctx->cached_bytes + b <= kCacheCapBytes) {
+                ctx->free_cache.emplace(b, ptr);
+                ctx->cached_bytes += b;
+                return ERNIE_OK;
+            }
+        }
+    }
     return hip_status(ctx, hipFree(ptr), "free");
 }
 
@@ -924,15 +973,15 @@ int ernie_hip_euler_step(ernie_hip_ctx* ctx, const float* x, const float* v, flo
 int ernie_hip_finite(ernie_hip_ctx* ctx, const float* x, size_t count, int* finite)
 {
     if (!ctx || !finite) return ERNIE_ERROR;
-    int* flag = nullptr;
-    int rc = hip_status(ctx, hipMalloc(&flag, sizeof(int)), "finite flag");
+    int rc = ERNIE_OK;
+    if (!ctx->finite_flag) rc = hip_status(ctx, hipMalloc(&ctx->finite_flag, sizeof(int)), "finite flag");
     if (rc) return rc;
+    int* flag = ctx->finite_flag;
     int host = 0;
     rc = hip_status(ctx, hipMemcpyAsync(flag, &host, sizeof(int), hipMemcpyHostToDevice, ctx->stream), "finite flag");
     if (!rc) rc = kernel_status(ctx, finite_flags(x, count, flag, ctx->stream), "finite");
     if (!rc) rc = hip_status(ctx, hipMemcpyAsync(&host, flag, sizeof(int), hipMemcpyDeviceToHost, ctx->stream), "finite");
     if (!rc) rc = hip_status(ctx, hipStreamSynchronize(ctx->stream), "finite");
-    (void)hipFree(flag);
     if (!rc) *finite = host ? 0 : 1;
     return rc;
 }

@@ -48,7 +48,10 @@ int ernie_hip_set_stream(ernie_hip_ctx* ctx, void* hip_stream);
 void* ernie_hip_own_stream(ernie_hip_ctx* ctx);
 void* ernie_hip_get_stream(ernie_hip_ctx* ctx);
 int ernie_hip_synchronize(ernie_hip_ctx* ctx);
-/* Device memory owned by the context's caller-facing allocator (for harnesses). */
+/* Device memory owned by the context's caller-facing allocator. Freed blocks (up to
+ * 8 GiB) are kept for reuse by later allocations of the same rounded size and released
+ * by ernie_hip_destroy: hipFree synchronises the device. Reuse is ordered by the
+ * context stream, so memory freed here must not be in use on another stream. */
 int ernie_hip_malloc(ernie_hip_ctx* ctx, size_t bytes, void** out);
 int ernie_hip_free(ernie_hip_ctx* ctx, void* ptr);
 int ernie_hip_memcpy_h2d(ernie_hip_ctx* ctx, void* dst, const void* src, size_t bytes);
