@@ -23,20 +23,67 @@ sys.path.insert(0, str(ROOT / "ernie-image-ncnn-vulkan_amd"))
 METRIC = "DiT denoise steps/s at 1024×1024 fp16 (36 blk); SDPA+GEMM % MFMA peak"
 PEAK = {"fp16": 2.5e15, "bf16": 2.5e15, "fp32": 157.3e12}
 HBM_PEAK = 8.0e12
-# HBM bytes per launch of each kernel class at this workload (FP16, S=4160): the
-# class's main kernel plus its split-K reduction (GEMM) or key-range combine (SDPA)
-# launch, from two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) scaled by the same
-# counters' reading for a plain 512 MiB FP32 copy (x2.000 fetch, x1.000 write); the
-# runs and the per-dispatch table are in profiles/denoise_1024_fp16_hbm_traffic.md.
-MEASURED_TRAFFIC = {"fp16": {"gemm_up_gate": 1.540e9 + 1.42e7, "gemm_qkv": 8.390e8 + 1.734e7,
-                             "sdpa": 2.335e8 + 1.945e7}}
 DIM, FFN, LATENT_CH, TEXT_DIM = 4096, 12288, 128, 3072
+SCHEDULE_STEPS = 8  # the turbo schedule the headline denoise runs
+# HBM bytes per launch of each kernel class at the headline workload come from the
+# committed rocprofv3 counter summary (FETCH_SIZE and WRITE_SIZE runs, each scaled by
+# the counter's reading for a plain copy of known size). The summary records a hash of
+# the kernel sources it was measured on; when the sources have changed since, the
+# figure no longer describes these kernels and `traffic` is reported as null.
+TRAFFIC_PROFILE = ROOT / "profiles" / "denoise_1024_fp16_hbm_traffic.md"
+KERNEL_SOURCES = ROOT / "ernie-image-ncnn-vulkan_amd" / "csrc"
+
+
+def kernel_sources_sha256():
+    """SHA-256 over the HIP kernel sources (file names and bytes, sorted by name)."""
+    import hashlib
+    h = hashlib.sha256()
+    for f in sorted(KERNEL_SOURCES.iterdir()):
+        if f.suffix in (".hip", ".hpp", ".cpp"):
+            h.update(f.name.encode() + b"\0" + f.read_bytes())
+    return h.hexdigest()
+
+
+def measured_traffic(precision, kernel):
+    """(bytes per launch, note) for a kernel class from the committed counter summary."""
+    if precision != "fp16" or not TRAFFIC_PROFILE.exists():
+        return None, "no counter summary for this configuration"
+    import re
+    m = re.search(r"```json traffic\n(.*?)\n```", TRAFFIC_PROFILE.read_text(), re.S)
+    if not m:
+        return None, "counter summary has no traffic record"
+    rec = json.loads(m.group(1))
+    if rec.get("kernel_sources_sha256") != kernel_sources_sha256():
+        return None, "counter summary was measured on other kernel sources"
+    return rec["bytes_per_launch"].get(kernel), f"{TRAFFIC_PROFILE.relative_to(ROOT)} (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)"
+
+
+def host_cpu():
+    """Model name, logical CPUs and physical cores of the host (from /proc/cpuinfo)."""
+    model, cores = None, set()
+    try:
+        phys = core = None
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            key, _, val = (t.strip() for t in line.partition(":"))
+            if key == "model name" and model is None:
+                model = val
+            elif key == "physical id":
+                phys = val
+            elif key == "core id":
+                core = val
+                cores.add((phys, core))
+    except OSError:
+        pass
+    return {"model": model, "logical_cpus": os.cpu_count(), "physical_cores": len(cores) or None,
+            "affinity_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None}
 
 
 def parse():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=8)
+    ap.add_argument("--steps", type=int, default=8,
+                    help="Euler steps timed: back-to-back 8-step turbo denoises, the last one partial (its last "
+                         "steps, by start_step) when --steps is not a multiple of 8")
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--blocks", type=int, default=36)
     ap.add_argument("--precision", choices=("fp16", "bf16", "fp32"), default="fp16")
@@ -89,7 +136,7 @@ def cpu_baseline(tokens):
     return {"value": 1.0 / (36.0 * block_s), "unit": "steps/s", "cores": threads, "kind": "port",
             "sample": f"1 FP32 DiT block (dim 4096, FFN 12288, S={tokens}) of the C++ oracle, "
                       f"{block_s:.2f} s, extrapolated x36 blocks per step (heads and Euler excluded)",
-            "block_seconds": block_s, "block_seconds_4_threads": block4_s}
+            "block_seconds": block_s, "block_seconds_4_threads": block4_s, "host": host_cpu()}
 
 
 def text_cpu_baseline(bucket, threads):
@@ -217,21 +264,30 @@ def main():
     start_latent = latent.clone()
     torch.cuda.synchronize()
 
-    def run(steps, start_step):
-        latent.copy_(start_latent)
-        torch.cuda.synchronize()
-        return fac.denoise(blocks, latent, H, W, text, args.text, cos_d, sin_d, mask_d, valid,
-                           steps, start_step=start_step, dtype=dt)
+    def run(n):
+        """n Euler steps as back-to-back 8-step turbo denoises, each from the same start
+        latent; a last partial denoise runs the final n % 8 steps of the schedule."""
+        secs = []
+        done = 0
+        while done < n:
+            k = min(SCHEDULE_STEPS, n - done)
+            latent.copy_(start_latent)
+            s_, _ = fac.denoise(blocks, latent, H, W, text, args.text, cos_d, sin_d, mask_d, valid,
+                                SCHEDULE_STEPS, start_step=SCHEDULE_STEPS - k, dtype=dt)
+            secs += list(s_)
+            done += k
+        return secs
 
     if args.warmup > 0:
-        run(max(args.warmup, 1), 0)
+        run(args.warmup)
+    torch.cuda.synchronize()
     print(f"bench: warmup done ({args.warmup} steps)", file=sys.stderr, flush=True)
     mfma_cls = ("gemm_qkv", "sdpa", "gemm_out", "gemm_up_gate", "gemm_down")
     # One untimed step with events around every launch: the per-class table and
     # the class that dominates device time.
     ctx.profile_reset()
     ctx.profile(True)
-    run(1, 0)
+    run(1)
     ctx.profile(False)
     table = ctx.profile_query()
     dom = max(mfma_cls, key=lambda c: table[c]["ms"])
@@ -244,7 +300,7 @@ def main():
         ctx.profile(True, classes=[dom], stride=max(1, args.event_stride))
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    step_s, _ = run(args.steps, 0)
+    step_s = run(args.steps)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ctx.profile(False)
@@ -259,6 +315,8 @@ def main():
     avg_s = d["ms"] / max(d["launches"], 1) * 1e-3
     flop_per_launch = d["flop"] / max(d["launches"], 1)
     achieved = flop_per_launch / avg_s if avg_s > 0 else 0.0
+    traffic, traffic_note = measured_traffic(args.precision, dom) if (args.grid == 64 and args.blocks == 36) else \
+        (None, "counter summary covers the 36-block 1024x1024 workload only")
     kernels = {c: {"launches": table[c]["launches"], "avg_us": table[c]["ms"] * 1e3 / max(table[c]["launches"], 1),
                    "tflops": (table[c]["flop"] / (table[c]["ms"] * 1e-3) / 1e12) if table[c]["ms"] and table[c]["flop"]
                    else None,
@@ -268,15 +326,15 @@ def main():
         "metric": METRIC, "value": args.steps / elapsed, "unit": "steps/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": elapsed / args.steps * 1e3, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": args.precision, "data": "synthetic",
-        "config": {"workload": f"{args.steps}-step flow-matching Euler DiT denoise at {16 * W}x{16 * H} "
-                               f"(latent [128,{H},{W}], {hw} image + {args.text} text tokens, {args.valid_text} valid, "
-                               f"S={S}), {args.blocks} blocks, dim 4096, 32 heads x 128, FFN 12288 gated erf-GELU, "
-                               f"{args.precision} storage / fp32 accumulate, turbo schedule shift 4, CFG 1",
+        "config": {"workload": f"8-step flow-matching Euler DiT denoise (turbo schedule, shift 4, CFG 1) at "
+                               f"{16 * W}x{16 * H} (latent [128,{H},{W}], {hw} image + {args.text} text tokens, "
+                               f"{args.valid_text} valid, S={S}), {args.blocks} blocks, dim 4096, 32 heads x 128, "
+                               f"FFN 12288 gated erf-GELU, {args.precision} storage / fp32 accumulate; {args.steps} "
+                               f"steps timed as back-to-back 8-step denoises",
                    "blocks": args.blocks, "tokens": S, "latent": [LATENT_CH, H, W], "text_tokens": args.text,
-                   "valid_text": args.valid_text},
+                   "valid_text": args.valid_text, "schedule_steps": SCHEDULE_STEPS},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved / 1e12, "peak": peak / 1e12,
-                     "unit": "TFLOP/s", "frac": achieved / peak,
-                     "traffic": MEASURED_TRAFFIC.get(args.precision, {}).get(dom) if args.grid == 64 else None,
+                     "unit": "TFLOP/s", "frac": achieved / peak, "traffic": traffic, "traffic_source": traffic_note,
                      "flop_per_launch": flop_per_launch, "avg_launch_us": avg_s * 1e6},
         "events": args.events,
         "mfma_util_sdpa_gemm": (tot_flop / (tot_ms * 1e-3)) / peak if tot_ms else None,

@@ -98,7 +98,17 @@ struct ernie_hip_ctx {
     std::unordered_map<void*, size_t> live;
     size_t cached_bytes = 0;
     std::mutex alloc_mu;
+    // Finiteness flags: [ERNIE_FINITE_SLOTS] for the asynchronous check plus one for
+    // ernie_hip_finite, on the device; their pinned host copies and completion events.
     int* finite_flag = nullptr;
+    int* finite_host = nullptr;
+    hipEvent_t finite_event[ERNIE_FINITE_SLOTS] = {};
+    bool finite_pending[ERNIE_FINITE_SLOTS] = {};
+    // Stream markers (ernie_hip_marker_*) and the per-block events of a timed block
+    // sequence: created once, reused by every call.
+    hipEvent_t marker[ERNIE_MARKERS] = {};
+    bool marker_recorded[ERNIE_MARKERS] = {};
+    std::vector<hipEvent_t> seq_events;
     size_t event_next = 0;
     std::vector<Launch> pending;
     long launches[ERNIE_PROFILE_CLASSES] = {};
@@ -133,6 +143,39 @@ int kernel_status(ernie_hip_ctx* ctx, int rc, const char* what)
 bool valid_dtype(int dt) { return dt == ERNIE_DTYPE_FP32 || dt == ERNIE_DTYPE_FP16 || dt == ERNIE_DTYPE_BF16; }
 size_t esize(int dt) { return dt == ERNIE_DTYPE_FP32 ? 4 : 2; }
 
+// Returns the freed blocks kept for reuse to the driver. hipFree synchronises the device,
+// so this runs only when an allocation failed or the caller asks (ernie_hip_trim).
+size_t release_cache(ernie_hip_ctx* ctx)
+{
+    std::lock_guard<std::mutex> lock(ctx->alloc_mu);
+    const size_t released = ctx->cached_bytes;
+    for (auto& kv : ctx->free_cache) (void)hipFree(kv.second);
+    ctx->free_cache.clear();
+    ctx->cached_bytes = 0;
+    return released;
+}
+
+// hipMalloc; when the device is out of memory while freed blocks of other sizes are
+// cached, they are released (after the stream's work that may still use them) and the
+// allocation is tried once more.
+hipError_t device_malloc(ernie_hip_ctx* ctx, void** out, size_t bytes)
+{
+    hipError_t e = hipMalloc(out, bytes);
+    if (e != hipErrorOutOfMemory) return e;
+    (void)hipGetLastError();
+    size_t cached = 0;
+    {
+        std::lock_guard<std::mutex> lock(ctx->alloc_mu);
+        cached = ctx->cached_bytes;
+    }
+    if (!cached) return e;
+    (void)hipStreamSynchronize(ctx->stream);
+    release_cache(ctx);
+    e = hipMalloc(out, bytes);
+    if (e != hipSuccess) (void)hipGetLastError();
+    return e;
+}
+
 int dev_alloc(ernie_hip_ctx* ctx, DeviceBuffer& b, size_t bytes, const char* what)
 {
     if (b.ptr && b.bytes >= bytes) return ERNIE_OK;
@@ -144,7 +187,7 @@ int dev_alloc(ernie_hip_ctx* ctx, DeviceBuffer& b, size_t bytes, const char* wha
         b.bytes = 0;
     }
     if (!bytes) return ERNIE_OK;
-    const hipError_t e = hipMalloc(&b.ptr, bytes);
+    const hipError_t e = device_malloc(ctx, &b.ptr, bytes);
     if (e != hipSuccess) {
         b.ptr = nullptr;
         return hip_status(ctx, e, what);
@@ -738,6 +781,32 @@ int output_head(ernie_hip_ctx* ctx, const float* x, int hw, const float* c, floa
     return kernel_status(ctx, tokens_to_latent(projv, hw, h.latent_ch, pred, s), "output unpatchify");
 }
 
+// At least n timing events in the context's pool (created once, reused by later calls).
+int sequence_events(ernie_hip_ctx* ctx, int n)
+{
+    while ((int)ctx->seq_events.size() < n) {
+        hipEvent_t e = nullptr;
+        const int rc = hip_status(ctx, hipEventCreate(&e), "event create");
+        if (rc) return rc;
+        ctx->seq_events.push_back(e);
+    }
+    return ERNIE_OK;
+}
+
+// Records the closing event after `count` timed items, waits for it once and writes the
+// device time between consecutive events.
+int sequence_seconds(ernie_hip_ctx* ctx, int count, double* seconds)
+{
+    int rc = hip_status(ctx, hipEventRecord(ctx->seq_events[count], ctx->stream), "block timing");
+    if (!rc) rc = hip_status(ctx, hipEventSynchronize(ctx->seq_events[count]), "block timing");
+    for (int i = 0; i < count && !rc; ++i) {
+        float ms = 0.f;
+        rc = hip_status(ctx, hipEventElapsedTime(&ms, ctx->seq_events[i], ctx->seq_events[i + 1]), "block timing");
+        seconds[i] = ms * 1e-3;
+    }
+    return rc;
+}
+
 int check_block_call(ernie_hip_ctx* ctx, int index, int S, const void* x, const void* out, const void* mods,
                      const void* cos_t, const void* sin_t, int valid_keys)
 {
@@ -789,8 +858,15 @@ void ernie_hip_destroy(ernie_hip_ctx* ctx)
     dev_free(ctx->dit_act);
     dev_free(ctx->split_ws);
     for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
-    for (auto& kv : ctx->free_cache) (void)hipFree(kv.second);
+    for (hipEvent_t e : ctx->seq_events) (void)hipEventDestroy(e);
+    for (hipEvent_t e : ctx->marker)
+        if (e) (void)hipEventDestroy(e);
+    for (hipEvent_t e : ctx->finite_event)
+        if (e) (void)hipEventDestroy(e);
+    release_cache(ctx);
+    for (auto& kv : ctx->live) (void)hipFree(kv.first);
     if (ctx->finite_flag) (void)hipFree(ctx->finite_flag);
+    if (ctx->finite_host) (void)hipHostFree(ctx->finite_host);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
 }
@@ -835,7 +911,7 @@ int ernie_hip_malloc(ernie_hip_ctx* ctx, size_t bytes, void** out)
             return ERNIE_OK;
         }
     }
-    const int rc = hip_status(ctx, hipMalloc(out, b), "malloc");
+    const int rc = hip_status(ctx, device_malloc(ctx, out, b), "malloc");
     if (!rc) {
         std::lock_guard<std::mutex> lock(ctx->alloc_mu);
         ctx->live[*out] = b;
@@ -861,6 +937,13 @@ int ernie_hip_free(ernie_hip_ctx* ctx, void* ptr)
         }
     }
     return hip_status(ctx, hipFree(ptr), "free");
+}
+
+size_t ernie_hip_trim(ernie_hip_ctx* ctx)
+{
+    if (!ctx) return 0;
+    (void)hipStreamSynchronize(ctx->stream);
+    return release_cache(ctx);
 }
 
 int ernie_hip_memcpy_h2d(ernie_hip_ctx* ctx, void* dst, const void* src, size_t bytes)
@@ -970,20 +1053,102 @@ int ernie_hip_euler_step(ernie_hip_ctx* ctx, const float* x, const float* v, flo
     return kernel_status(ctx, euler_step(x, v, delta, count, out, ctx->stream), "euler");
 }
 
+// Lazily creates the finiteness flags (device), their pinned host copies and events.
+static int finite_setup(ernie_hip_ctx* ctx)
+{
+    if (ctx->finite_flag) return ERNIE_OK;
+    constexpr int n = ERNIE_FINITE_SLOTS + 1;
+    int rc = hip_status(ctx, device_malloc(ctx, reinterpret_cast<void**>(&ctx->finite_flag), n * sizeof(int)),
+                        "finite flags");
+    if (!rc) rc = hip_status(ctx, hipHostMalloc(reinterpret_cast<void**>(&ctx->finite_host), n * sizeof(int), 0),
+                             "finite flags");
+    for (int i = 0; i < ERNIE_FINITE_SLOTS && !rc; ++i)
+        rc = hip_status(ctx, hipEventCreateWithFlags(&ctx->finite_event[i], hipEventDisableTiming), "finite event");
+    if (rc) {
+        for (hipEvent_t& e : ctx->finite_event)
+            if (e) (void)hipEventDestroy(e), e = nullptr;
+        if (ctx->finite_host) (void)hipHostFree(ctx->finite_host);
+        if (ctx->finite_flag) (void)hipFree(ctx->finite_flag);
+        ctx->finite_host = nullptr;
+        ctx->finite_flag = nullptr;
+    }
+    return rc;
+}
+
+// Clears flag `index`, checks x into it and queues its copy to the pinned host slot.
+static int finite_enqueue(ernie_hip_ctx* ctx, const float* x, size_t count, int index)
+{
+    int rc = finite_setup(ctx);
+    int* flag = ctx ? ctx->finite_flag + index : nullptr;
+    if (!rc) rc = kernel_status(ctx, fill_int(flag, 0, 1, ctx->stream), "finite flag");
+    if (!rc) rc = kernel_status(ctx, finite_flags(x, count, flag, ctx->stream), "finite");
+    if (!rc) rc = hip_status(ctx, hipMemcpyAsync(ctx->finite_host + index, flag, sizeof(int), hipMemcpyDeviceToHost,
+                                                 ctx->stream), "finite");
+    return rc;
+}
+
 int ernie_hip_finite(ernie_hip_ctx* ctx, const float* x, size_t count, int* finite)
 {
-    if (!ctx || !finite) return ERNIE_ERROR;
-    int rc = ERNIE_OK;
-    if (!ctx->finite_flag) rc = hip_status(ctx, hipMalloc(&ctx->finite_flag, sizeof(int)), "finite flag");
-    if (rc) return rc;
-    int* flag = ctx->finite_flag;
-    int host = 0;
-    rc = hip_status(ctx, hipMemcpyAsync(flag, &host, sizeof(int), hipMemcpyHostToDevice, ctx->stream), "finite flag");
-    if (!rc) rc = kernel_status(ctx, finite_flags(x, count, flag, ctx->stream), "finite");
-    if (!rc) rc = hip_status(ctx, hipMemcpyAsync(&host, flag, sizeof(int), hipMemcpyDeviceToHost, ctx->stream), "finite");
+    if (!ctx || !finite || (!x && count)) return ERNIE_ERROR;
+    int rc = finite_enqueue(ctx, x, count, ERNIE_FINITE_SLOTS);
     if (!rc) rc = hip_status(ctx, hipStreamSynchronize(ctx->stream), "finite");
-    if (!rc) *finite = host ? 0 : 1;
+    if (!rc) *finite = ctx->finite_host[ERNIE_FINITE_SLOTS] ? 0 : 1;
     return rc;
+}
+
+int ernie_hip_finite_begin(ernie_hip_ctx* ctx, const float* x, size_t count, int slot)
+{
+    if (!ctx) return ERNIE_ERROR;
+    if (slot < 0 || slot >= ERNIE_FINITE_SLOTS) return fail(ctx, ERNIE_ERROR, "finite slot out of range");
+    if (!x && count) return fail(ctx, ERNIE_ERROR, "null finite input");
+    int rc = finite_enqueue(ctx, x, count, slot);
+    if (!rc) rc = hip_status(ctx, hipEventRecord(ctx->finite_event[slot], ctx->stream), "finite event");
+    ctx->finite_pending[slot] = rc == ERNIE_OK;
+    return rc;
+}
+
+int ernie_hip_finite_end(ernie_hip_ctx* ctx, int slot, int* finite)
+{
+    if (!ctx || !finite) return ERNIE_ERROR;
+    if (slot < 0 || slot >= ERNIE_FINITE_SLOTS || !ctx->finite_pending[slot])
+        return fail(ctx, ERNIE_ERROR, "no finite check pending in this slot");
+    ctx->finite_pending[slot] = false;
+    const int rc = hip_status(ctx, hipEventSynchronize(ctx->finite_event[slot]), "finite wait");
+    if (!rc) *finite = ctx->finite_host[slot] ? 0 : 1;
+    return rc;
+}
+
+int ernie_hip_marker_record(ernie_hip_ctx* ctx, int marker)
+{
+    if (!ctx) return ERNIE_ERROR;
+    if (marker < 0 || marker >= ERNIE_MARKERS) return fail(ctx, ERNIE_ERROR, "marker out of range");
+    if (!ctx->marker[marker]) {
+        const int rc = hip_status(ctx, hipEventCreate(&ctx->marker[marker]), "marker");
+        if (rc) return rc;
+    }
+    const int rc = hip_status(ctx, hipEventRecord(ctx->marker[marker], ctx->stream), "marker");
+    ctx->marker_recorded[marker] = rc == ERNIE_OK;
+    return rc;
+}
+
+int ernie_hip_marker_elapsed(ernie_hip_ctx* ctx, int from, int to, double* seconds)
+{
+    if (!ctx || !seconds) return ERNIE_ERROR;
+    if (from < 0 || to < 0 || from >= ERNIE_MARKERS || to >= ERNIE_MARKERS || !ctx->marker_recorded[from] ||
+        !ctx->marker_recorded[to])
+        return fail(ctx, ERNIE_ERROR, "marker not recorded");
+    int rc = hip_status(ctx, hipEventSynchronize(ctx->marker[to]), "marker wait");
+    float ms = 0.f;
+    if (!rc) rc = hip_status(ctx, hipEventElapsedTime(&ms, ctx->marker[from], ctx->marker[to]), "marker elapsed");
+    if (!rc) *seconds = ms * 1e-3;
+    return rc;
+}
+
+int ernie_hip_transpose(ernie_hip_ctx* ctx, const void* in, int dtype, int rows, int cols, void* out)
+{
+    if (!ctx) return ERNIE_ERROR;
+    if (in == out && rows > 1 && cols > 1) return fail(ctx, ERNIE_ERROR, "transpose cannot run in place");
+    return kernel_status(ctx, transpose2d(in, dtype, rows, cols, out, ctx->stream), "transpose");
 }
 
 int ernie_hip_fill_normal(ernie_hip_ctx* ctx, void* out, int dtype, size_t count, uint64_t seed, uint64_t offset,
@@ -1136,33 +1301,12 @@ int ernie_hip_block_sequence(ernie_hip_ctx* ctx, const int* blocks, int count, c
             return fail(ctx, ERNIE_ERROR, "blocks differ in width");
     }
     // One event before each block and one after the last; a single wait at the end.
-    std::vector<hipEvent_t> ev;
-    if (seconds) {
-        ev.resize(count + 1, nullptr);
-        for (auto& e : ev)
-            if (hipEventCreate(&e) != hipSuccess) {
-                for (auto& f : ev)
-                    if (f) (void)hipEventDestroy(f);
-                return fail(ctx, ERNIE_ERROR, "event create");
-            }
-    }
-    int rc = ERNIE_OK;
+    int rc = seconds ? sequence_events(ctx, count + 1) : ERNIE_OK;
     for (int i = 0; i < count && !rc; ++i) {
-        if (seconds) (void)hipEventRecord(ev[i], ctx->stream);
+        if (seconds) (void)hipEventRecord(ctx->seq_events[i], ctx->stream);
         rc = block_forward(ctx, ctx->blocks[blocks[i]], i == 0 ? x : out, out, mods, cos_t, sin_t, mask, valid_keys, S);
     }
-    if (seconds) {
-        if (!rc) {
-            (void)hipEventRecord(ev[count], ctx->stream);
-            rc = hip_status(ctx, hipEventSynchronize(ev[count]), "block timing");
-        }
-        for (int i = 0; i < count && !rc; ++i) {
-            float ms = 0.f;
-            (void)hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
-            seconds[i] = ms * 1e-3;
-        }
-        for (auto& e : ev) (void)hipEventDestroy(e);
-    }
+    if (seconds && !rc) rc = sequence_seconds(ctx, count, seconds);
     return rc;
 }
 
@@ -1282,34 +1426,13 @@ int ernie_hip_text_block_sequence(ernie_hip_ctx* ctx, const int* blocks, int cou
         if (ctx->text_blocks[blocks[i]].hidden != ctx->text_blocks[blocks[0]].hidden)
             return fail(ctx, ERNIE_ERROR, "text blocks differ in width");
     }
-    std::vector<hipEvent_t> ev;
-    if (seconds) {
-        ev.resize(count + 1, nullptr);
-        for (auto& e : ev)
-            if (hipEventCreate(&e) != hipSuccess) {
-                for (auto& f : ev)
-                    if (f) (void)hipEventDestroy(f);
-                return fail(ctx, ERNIE_ERROR, "event create");
-            }
-    }
-    int rc = ERNIE_OK;
+    int rc = seconds ? sequence_events(ctx, count + 1) : ERNIE_OK;
     for (int i = 0; i < count && !rc; ++i) {
-        if (seconds) (void)hipEventRecord(ev[i], ctx->stream);
+        if (seconds) (void)hipEventRecord(ctx->seq_events[i], ctx->stream);
         rc = text_block_forward(ctx, ctx->text_blocks[blocks[i]], i == 0 ? x : out, out, cos_t, sin_t, mask, causal,
                                 S);
     }
-    if (seconds) {
-        if (!rc) {
-            (void)hipEventRecord(ev[count], ctx->stream);
-            rc = hip_status(ctx, hipEventSynchronize(ev[count]), "text block timing");
-        }
-        for (int i = 0; i < count && !rc; ++i) {
-            float ms = 0.f;
-            (void)hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
-            seconds[i] = ms * 1e-3;
-        }
-        for (auto& e : ev) (void)hipEventDestroy(e);
-    }
+    if (seconds && !rc) rc = sequence_seconds(ctx, count, seconds);
     return rc;
 }
 

@@ -105,6 +105,10 @@ int gelu_inplace(void* x, int dtype, size_t n, hipStream_t s);
 int residual_add(const void* a, int a_dtype, const void* b, int b_dtype, float* out, size_t n, hipStream_t s);
 int euler_step(const float* x, const float* v, float delta, size_t n, float* out, hipStream_t s);
 int finite_flags(const float* x, size_t n, int* flag, hipStream_t s);
+// out [cols][rows] = in [rows][cols] transposed (element type dt; in and out must not overlap).
+int transpose2d(const void* in, int dt, int rows, int cols, void* out, hipStream_t s);
+// p[0..n) = value by a kernel (no memset node, so the clear may be captured in a graph).
+int fill_int(int* p, int value, size_t n, hipStream_t s);
 int convert(const void* in, int in_dtype, void* out, int out_dtype, size_t n, hipStream_t s);
 int fill_normal(void* out, int dtype, size_t n, uint64_t seed, uint64_t offset, float mean, float std_dev,
                 hipStream_t s);

@@ -370,6 +370,31 @@ __global__ void finite_kernel(const float* __restrict__ x, size_t n, int* __rest
     if (bad) atomicOr(flag, 1);
 }
 
+// out[c][r] = in[r][c] for one element size (2 or 4 bytes), 32 x 32 tiles through LDS
+// so both the reads and the writes are row-contiguous. Grid (ceil(cols/32),
+// ceil(rows/32)), block 32 x 8.
+template <typename E>
+__global__ void __launch_bounds__(256) transpose_kernel(const E* __restrict__ in, E* __restrict__ out, int rows, int cols)
+{
+    __shared__ E tile[32][33];
+    const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+    const int tx = threadIdx.x, ty = threadIdx.y;
+    for (int i = ty; i < 32; i += 8) {
+        const int r = r0 + i, c = c0 + tx;
+        if (r < rows && c < cols) tile[i][tx] = in[(size_t)r * cols + c];
+    }
+    __syncthreads();
+    for (int i = ty; i < 32; i += 8) {
+        const int c = c0 + i, r = r0 + tx;
+        if (c < cols && r < rows) out[(size_t)c * rows + r] = tile[tx][i];
+    }
+}
+
+__global__ void fill_int_kernel(int* __restrict__ p, int value, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = value;
+}
+
 __global__ void convert_kernel(const void* __restrict__ in, int idt, void* __restrict__ out, int odt, size_t n)
 {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
@@ -678,6 +703,29 @@ int finite_flags(const float* x, size_t n, int* flag, hipStream_t s)
     if (!x || !flag) return -1;
     if (!n) return 0;
     hipLaunchKernelGGL(finite_kernel, dim3(grid_for(n)), dim3(256), 0, s, x, n, flag);
+    return launch_status();
+}
+
+int transpose2d(const void* in, int dt, int rows, int cols, void* out, hipStream_t s)
+{
+    if (!in || !out || !valid_dt(dt) || rows < 0 || cols < 0) return -1;
+    if (!rows || !cols) return 0;
+    const dim3 grid((cols + 31) / 32, (rows + 31) / 32), block(32, 8);
+    if (grid.y > 65535) return -1;
+    if (dt == DT_F32)
+        hipLaunchKernelGGL(transpose_kernel<uint32_t>, grid, block, 0, s, static_cast<const uint32_t*>(in),
+                           static_cast<uint32_t*>(out), rows, cols);
+    else
+        hipLaunchKernelGGL(transpose_kernel<uint16_t>, grid, block, 0, s, static_cast<const uint16_t*>(in),
+                           static_cast<uint16_t*>(out), rows, cols);
+    return launch_status();
+}
+
+int fill_int(int* p, int value, size_t n, hipStream_t s)
+{
+    if (!p) return -1;
+    if (!n) return 0;
+    hipLaunchKernelGGL(fill_int_kernel, dim3(grid_for(n)), dim3(256), 0, s, p, value, n);
     return launch_status();
 }
 

@@ -92,6 +92,12 @@ def hip():
             "ernie_hip_qk_norm_rope": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_long, c_vp, c_vp, c_vp]),
             "ernie_hip_euler_step": (c_int, [c_vp, c_vp, c_vp, c_float, c_size_t, c_vp]),
             "ernie_hip_finite": (c_int, [c_vp, c_vp, c_size_t, ctypes.POINTER(c_int)]),
+            "ernie_hip_finite_begin": (c_int, [c_vp, c_vp, c_size_t, c_int]),
+            "ernie_hip_finite_end": (c_int, [c_vp, c_int, ctypes.POINTER(c_int)]),
+            "ernie_hip_marker_record": (c_int, [c_vp, c_int]),
+            "ernie_hip_marker_elapsed": (c_int, [c_vp, c_int, c_int, ctypes.POINTER(c_double)]),
+            "ernie_hip_trim": (c_size_t, [c_vp]),
+            "ernie_hip_transpose": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_vp]),
             "ernie_hip_fill_normal": (c_int, [c_vp, c_vp, c_int, c_size_t, c_u64, c_u64, c_float, c_float]),
             "ernie_hip_convert": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_size_t]),
             "ernie_hip_block_upload": (c_int, [c_vp, c_int, c_vp, c_int, c_int, c_int]),
@@ -156,6 +162,15 @@ class HostTensor(ctypes.Structure):
     _fields_ = [("data", c_vp), ("dtype", c_int)]
 
 
+class OpBlob(ctypes.Structure):
+    """ernie_op_blob (include/ernie.h)."""
+    _fields_ = [("data", c_vp), ("dtype", c_int), ("w", c_int), ("h", c_int), ("c", c_int)]
+
+
+# ernie_stage_observer / ernie_step_observer (include/ernie.h).
+STAGE_OBSERVER = ctypes.CFUNCTYPE(None, ctypes.c_char_p, c_vp, c_int, c_int, c_int, c_vp)
+STEP_OBSERVER = ctypes.CFUNCTYPE(None, c_int, c_vp, c_vp, c_size_t, c_vp)
+
 GRAPH_CONTRACTS = ("unreviewed", "component", "runtime")
 # Weighted layers of a block graph in .bin order (tools/build_dit_weights.py:19-31).
 BLOCK_WEIGHT_LAYERS = ("rmsn_8", "gemm_0", "gemm_1", "gemm_2", "rmsn_9", "rmsn_10", "gemm_3", "rmsn_11", "gemm_4",
@@ -182,6 +197,13 @@ def facade():
                                                  c_int, c_vp, c_vp, cp, c_size_t]),
             "ernie_denoise": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_int,
                                       c_int, c_int, c_int, c_vp, c_vp, cp, c_size_t]),
+            "ernie_denoise_observed": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_int, c_vp, c_int, c_vp, c_vp, c_vp,
+                                               c_int, c_int, c_int, c_int, c_int, c_vp, c_vp, STEP_OBSERVER, c_vp,
+                                               cp, c_size_t]),
+            "ernie_run_dit": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_int, c_vp, c_int, c_vp, c_int, c_vp, c_vp,
+                                      c_vp, c_int, c_int, c_vp, c_vp, STAGE_OBSERVER, c_vp, cp, c_size_t]),
+            "ernie_op_forward": (c_int, [c_vp, cp, cp, c_vp, c_size_t, ctypes.POINTER(OpBlob), c_int,
+                                         ctypes.POINTER(OpBlob), c_int, cp, c_size_t]),
             "ernie_text_constants": (c_int, [c_vp, c_int, c_vp, c_vp, c_vp, cp, c_size_t]),
             "ernie_text_embeddings": (c_int, [c_vp, c_size_t, c_int, c_vp, c_int, c_int, c_vp, cp, c_size_t]),
             "ernie_run_text_blocks": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_int, c_vp, c_vp, c_vp, c_int, c_int,
@@ -394,6 +416,25 @@ class Context:
         self.call("finite", ptr(x), count, ctypes.byref(f))
         return bool(f.value)
 
+    def finite_begin(self, x, count, slot):
+        self.call("finite_begin", ptr(x), count, slot)
+
+    def finite_end(self, slot):
+        f = c_int()
+        self.call("finite_end", slot, ctypes.byref(f))
+        return bool(f.value)
+
+    def marker(self, index):
+        self.call("marker_record", index)
+
+    def marker_elapsed(self, first, last):
+        s = c_double()
+        self.call("marker_elapsed", first, last, ctypes.byref(s))
+        return s.value
+
+    def trim(self):
+        return int(self.L.ernie_hip_trim(self.ctx))
+
     def fill_normal(self, out, dtype, count, seed, offset=0, mean=0.0, std=1.0):
         self.call("fill_normal", ptr(out), dtype, count, seed, offset, mean, std)
 
@@ -571,6 +612,53 @@ class Facade:
         if rc < 0:
             _raise(rc, e.value)
         return secs
+
+    def op_forward(self, op_type, params, inputs, outputs=(), weights=None):
+        """One registered op (ernie_op_forward). inputs / outputs: (tensor, dtype, w, h, c) tuples."""
+        import numpy as np
+        w = None if weights is None else np.ascontiguousarray(weights, np.float32)
+        ins = (OpBlob * max(len(inputs), 1))(*[OpBlob(ptr(t), dt, a, b, c) for t, dt, a, b, c in inputs])
+        outs = (OpBlob * max(len(outputs), 1))(*[OpBlob(ptr(t), dt, a, b, c) for t, dt, a, b, c in outputs])
+        e = _err()
+        rc = self.L.ernie_op_forward(self.dev, op_type.encode(), params.encode(), None if w is None else w.ctypes.data,
+                                     0 if w is None else w.size, ins, len(inputs), outs, len(outputs), e, 512)
+        if rc:
+            _raise(rc, e.value)
+
+    def run_dit(self, blocks, latent, height, width, text, text_tokens, features, dim, cos, sin, prediction,
+                mask=None, valid_prefix=0, dtype=FP16, timing=False, observer=None):
+        """Facade run_dit; observer(stage, device_ptr, w, h, c) is called per stage."""
+        import numpy as np
+        ids = (c_int * max(len(blocks), 1))(*blocks)
+        secs = np.zeros(max(len(blocks), 1), np.float64) if timing else None
+        cb = STAGE_OBSERVER(lambda st, p, w_, h_, c_, u: observer(st.decode(), p, w_, h_, c_)) if observer else \
+            ctypes.cast(None, STAGE_OBSERVER)
+        e = _err()
+        rc = self.L.ernie_run_dit(self.dev, ctypes.cast(ids, c_vp), len(blocks), ptr(latent), height, width, ptr(text),
+                                  text_tokens, ptr(features), dim, ptr(cos), ptr(sin), ptr(mask), valid_prefix, dtype,
+                                  ptr(prediction), None if secs is None else secs.ctypes.data, cb, None, e, 512)
+        if rc:
+            _raise(rc, e.value)
+        return None if secs is None else secs[:len(blocks)]
+
+    def denoise_observed(self, blocks, latent, height, width, text, text_tokens, cos, sin, mask, valid_prefix, steps,
+                         start_step=0, dtype=FP16, collect_details=False, observer=None):
+        """Facade denoise with a step observer(step, prediction_ptr, sample_ptr, count)."""
+        import numpy as np
+        ids = (c_int * max(len(blocks), 1))(*blocks)
+        n = max(steps, 1)
+        secs = np.zeros(n, np.float64)
+        ts = np.zeros(n, np.float32)
+        cb = STEP_OBSERVER(lambda i, p, s_, cnt, u: observer(i, p, s_, cnt)) if observer else \
+            ctypes.cast(None, STEP_OBSERVER)
+        e = _err()
+        rc = self.L.ernie_denoise_observed(self.dev, ctypes.cast(ids, c_vp), len(blocks), ptr(latent), height, width,
+                                           ptr(text), text_tokens, ptr(cos), ptr(sin), ptr(mask), valid_prefix, steps,
+                                           start_step, dtype, int(bool(collect_details)), secs.ctypes.data,
+                                           ts.ctypes.data, cb, None, e, 512)
+        if rc:
+            _raise(rc, e.value)
+        return secs[:max(steps - start_step, 0)], ts[:max(steps - start_step, 0)]
 
     def denoise(self, blocks, latent, height, width, text, text_tokens, cos, sin, mask, valid_prefix, steps,
                 start_step=0, dtype=FP16):

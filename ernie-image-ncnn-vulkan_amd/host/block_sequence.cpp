@@ -61,25 +61,34 @@ DeviceMat run_block_sequence(const std::vector<BlockModel>& models, const Device
         }
     }
     DeviceMat current = DeviceMat::create(device, dim, S, 1, 2);
-    const float* in = input.data;
-    for (size_t i = 0; i < models.size(); ++i) {
-        const auto start = Clock::now();
-        double seconds = 0;
-        const int index = models[i].index;
-        const int rc = ernie_hip_block_sequence(ctx, &index, 1, in, current.data, mods.data, cos.data, sin.data,
-                                                mask_arg(mask), mask.valid_prefix, S, &seconds);
+    std::vector<int> indices;
+    for (const auto& m : models) indices.push_back(m.index);
+    const int count = int(indices.size());
+    std::vector<double> seconds(indices.size(), 0.0);
+    // Without an observer every block is queued in one call and timed with device events
+    // (one wait at the end); an observer sees each block's output as it completes, so the
+    // blocks then run one call each (the reference's per-block extract,
+    // src/block_sequence.cpp:73-89).
+    const auto start = Clock::now();
+    const int batch = observer ? 1 : count;
+    for (int first = 0; first < count; first += batch) {
+        const int rc = ernie_hip_block_sequence(ctx, &indices[first], batch, first ? current.data : input.data,
+                                                current.data, mods.data, cos.data, sin.data, mask_arg(mask),
+                                                mask.valid_prefix, S, &seconds[first]);
         if (rc) {
             if (stats.collect_details)
-                stats.details.push_back({int(i), "extract_compute_composite", "failed",
+                stats.details.push_back({first, "extract_compute_composite", "failed",
                                          std::chrono::duration<double>(Clock::now() - start).count()});
             check_status(rc, ctx, "extract block output");
         }
-        in = current.data;
-        stats.load_seconds.push_back(0.0);
-        stats.compute_seconds.push_back(seconds);
-        stats.compute_submissions += 1;
-        if (stats.collect_details) stats.details.push_back({int(i), "extract_compute_composite", "complete", seconds});
-        if (observer) observer("block-" + std::to_string(i), current);
+        for (int i = first; i < first + batch; ++i) {
+            stats.load_seconds.push_back(0.0);
+            stats.compute_seconds.push_back(seconds[i]);
+            stats.compute_submissions += 1;
+            if (stats.collect_details)
+                stats.details.push_back({i, "extract_compute_composite", "complete", seconds[i]});
+        }
+        if (observer) observer("block-" + std::to_string(first), current);
     }
     return current;
 }

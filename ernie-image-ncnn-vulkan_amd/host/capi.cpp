@@ -5,10 +5,13 @@
 #include <cstring>
 #include <exception>
 #include <stdexcept>
+#include <string>
 
 #include "ernie/block_files.h"
 #include "ernie/conditioning.h"
 #include "ernie/denoiser.h"
+#include "ernie/dit.h"
+#include "ernie/ops.h"
 #include "ernie/sha256.h"
 #include "ernie/text_encoder.h"
 
@@ -174,6 +177,41 @@ int ernie_run_block_sequence(ernie_device* device, const int* blocks, int count,
     });
 }
 
+int ernie_op_forward(ernie_device* device, const char* type, const char* params, const float* weights,
+                     size_t weight_count, const ernie_op_blob* inputs, int input_count, ernie_op_blob* outputs,
+                     int output_count, char* err, size_t errlen)
+{
+    return guarded(err, errlen, [&]() -> int {
+        if (!device || !type || input_count < 0 || output_count < 0 || (input_count && !inputs) ||
+            (output_count && !outputs) || (weight_count && !weights))
+            throw std::invalid_argument("null op argument");
+        ernie::OpRegistry registry;
+        if (ernie::register_layers(registry)) throw std::runtime_error("op registration failed");
+        ernie::OpParams p = ernie::OpParams::parse(params ? params : "");
+        p.weights.assign(weights, weights + weight_count);
+        auto tensor = [](const ernie_op_blob& b) {
+            ernie::OpTensor t;
+            t.data = b.data;
+            t.dtype = b.dtype;
+            t.w = b.w;
+            t.h = b.h;
+            t.c = b.c;
+            return t;
+        };
+        std::vector<ernie::OpTensor> in, out;
+        for (int i = 0; i < input_count; ++i) in.push_back(tensor(inputs[i]));
+        for (int i = 0; i < output_count; ++i) out.push_back(tensor(outputs[i]));
+        ernie::Option option = option_for(device->device, ERNIE_DTYPE_FP32);
+        if (!registry.has(type)) {
+            set_err(err, errlen, (std::string("no registered op ") + type).c_str());
+            return ERNIE_ERROR;
+        }
+        const int rc = registry.forward(type, device->device, in, out, p, option);
+        if (rc) set_err(err, errlen, (std::string(type) + " rejected the call or failed").c_str());
+        return rc;
+    });
+}
+
 int ernie_text_constants(const float* inverse_frequencies, int bucket, float* cos_out, float* sin_out,
                          float* mask_out, char* err, size_t errlen)
 {
@@ -225,10 +263,11 @@ int ernie_run_text_blocks(ernie_device* device, const int* blocks, int count, co
     });
 }
 
-int ernie_denoise(ernie_device* device, const int* blocks, int count, float* latent, int height, int width,
-                  const float* text, int text_tokens, const float* cos_t, const float* sin_t, const float* mask,
-                  int valid_prefix, int steps, int start_step, int storage_dtype, double* step_seconds,
-                  float* step_timesteps, char* err, size_t errlen)
+int ernie_denoise_observed(ernie_device* device, const int* blocks, int count, float* latent, int height, int width,
+                           const float* text, int text_tokens, const float* cos_t, const float* sin_t,
+                           const float* mask, int valid_prefix, int steps, int start_step, int storage_dtype,
+                           int collect_details, double* step_seconds, float* step_timesteps,
+                           ernie_step_observer observer, void* user, char* err, size_t errlen)
 {
     return guarded(err, errlen, [&]() -> int {
         if (!device || !blocks || count < 0) throw std::invalid_argument("null denoise argument");
@@ -242,8 +281,15 @@ int ernie_denoise(ernie_device* device, const int* blocks, int count, float* lat
             wrap(sin_t, 128, S), m};
         std::vector<ernie::DenoiseStepStats> stats;
         const auto& d = device->device;
+        ernie::StepObserver step_observer;
+        if (observer)
+            step_observer = [&](size_t step, const ernie::DeviceMat& prediction, const ernie::DeviceMat& sample) {
+                d.synchronize();
+                observer(int(step), prediction.data, sample.data, sample.total(), user);
+            };
         const auto result = ernie::denoise(model, wrap(latent, width, height, 128, 3), constants, steps,
-                                           option_for(d, storage_dtype), stats, {}, start_step);
+                                           option_for(d, storage_dtype), stats, step_observer, start_step,
+                                           collect_details != 0);
         ernie::check_status(ernie_hip_convert(d.ctx(), result.data, ERNIE_DTYPE_FP32, latent, ERNIE_DTYPE_FP32,
                                               result.total()),
                             d.ctx(), "copy denoised latent");
@@ -252,6 +298,52 @@ int ernie_denoise(ernie_device* device, const int* blocks, int count, float* lat
             if (step_seconds) step_seconds[i] = stats[i].elapsed_seconds;
             if (step_timesteps) step_timesteps[i] = stats[i].timestep;
         }
+        return ERNIE_OK;
+    });
+}
+
+int ernie_denoise(ernie_device* device, const int* blocks, int count, float* latent, int height, int width,
+                  const float* text, int text_tokens, const float* cos_t, const float* sin_t, const float* mask,
+                  int valid_prefix, int steps, int start_step, int storage_dtype, double* step_seconds,
+                  float* step_timesteps, char* err, size_t errlen)
+{
+    return ernie_denoise_observed(device, blocks, count, latent, height, width, text, text_tokens, cos_t, sin_t,
+                                  mask, valid_prefix, steps, start_step, storage_dtype, 0, step_seconds,
+                                  step_timesteps, nullptr, nullptr, err, errlen);
+}
+
+int ernie_run_dit(ernie_device* device, const int* blocks, int count, const float* latent, int height, int width,
+                  const float* text, int text_tokens, const float* time_features, int dim, const float* cos_t,
+                  const float* sin_t, const float* mask, int valid_prefix, int storage_dtype, float* prediction,
+                  double* block_seconds, ernie_stage_observer observer, void* user, char* err, size_t errlen)
+{
+    return guarded(err, errlen, [&]() -> int {
+        if (!device || !blocks || count < 0 || !latent || !time_features || !prediction || dim < 1)
+            throw std::invalid_argument("null run_dit argument");
+        ernie::DitModel model;
+        for (int i = 0; i < count; ++i) model.blocks.push_back({blocks[i]});
+        const int S = height * width + text_tokens;
+        ernie::DeviceMat m = mask ? wrap(mask, S) : ernie::DeviceMat{};
+        m.valid_prefix = valid_prefix;
+        const std::vector<ernie::DeviceMat> inputs{
+            wrap(latent, width, height, 128, 3), text_tokens ? wrap(text, 3072, text_tokens, 1, 2) : ernie::DeviceMat{},
+            wrap(time_features, dim), wrap(cos_t, 128, S), wrap(sin_t, 128, S), m};
+        ernie::DitStats stats;
+        stats.collect_details = block_seconds != nullptr;
+        ernie::StageObserver stage_observer;
+        if (observer)
+            stage_observer = [&](const std::string& stage, const ernie::DeviceMat& t) {
+                observer(stage.c_str(), t.data, t.w, t.h, t.c, user);
+            };
+        const auto& d = device->device;
+        const auto result = ernie::run_dit(model, inputs, option_for(d, storage_dtype), stats, stage_observer);
+        ernie::check_status(ernie_hip_convert(d.ctx(), result.data, ERNIE_DTYPE_FP32, prediction, ERNIE_DTYPE_FP32,
+                                              result.total()),
+                            d.ctx(), "copy prediction");
+        d.synchronize();
+        if (block_seconds)
+            for (size_t i = 0; i < stats.blocks.compute_seconds.size(); ++i)
+                block_seconds[i] = stats.blocks.compute_seconds[i];
         return ERNIE_OK;
     });
 }

@@ -2,6 +2,7 @@
 // Compiled with -ffp-contract=off, as the reference compiles denoiser.cpp.
 #include "ernie/denoiser.h"
 
+#include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <stdexcept>
@@ -45,16 +46,60 @@ DeviceMat denoise(const DenoiseModel& model, const DeviceMat& initial, const std
     if (start_step < 0 || start_step > steps) throw std::invalid_argument("Denoising start step must be in [0,steps]");
     if (!option.device) throw std::invalid_argument("Device denoiser requires a device");
     const Device& device = *option.device;
+    ernie_hip_ctx* ctx = device.ctx();
     const auto schedule = FlowSchedule::turbo(steps);
     stats.clear();
     DeviceMat sample = DeviceMat::create(device, initial.w, initial.h, initial.c, 3);
-    check_status(ernie_hip_convert(device.ctx(), initial.data, ERNIE_DTYPE_FP32, sample.data, ERNIE_DTYPE_FP32,
-                                   initial.total()),
-                 device.ctx(), "copy initial latent");
+    check_status(ernie_hip_convert(ctx, initial.data, ERNIE_DTYPE_FP32, sample.data, ERNIE_DTYPE_FP32, initial.total()),
+                 ctx, "copy initial latent");
     if (!finite_latent(device, sample)) throw std::invalid_argument("Initial latent is not finite");
-    DeviceMat features = DeviceMat::create(device, 4096);
+    const int executed = steps - start_step;
+    if (!executed) return sample;
+
+    // The time features of every executed step (computed on the host in the reference's
+    // FP32 order, src/denoiser.cpp:22-39) go to the device in one copy before the loop,
+    // instead of one blocking upload per step.
+    DeviceMat features = DeviceMat::create(device, 4096, executed, 1, 2);
+    {
+        std::vector<float> host(size_t(executed) * 4096);
+        for (int k = 0; k < executed; ++k) {
+            const auto f = timestep_features(schedule.timesteps[start_step + k]);
+            std::copy(f.begin(), f.end(), host.begin() + size_t(k) * 4096);
+        }
+        features.upload(device, host.data(), host.size());
+    }
+
+    // Each step is queued without a wait. Its finiteness flag is read one step behind:
+    // step i's check is awaited after step i + 1's DiT has been queued, so the device
+    // never runs dry; a non-finite step is still reported as that step, and the
+    // observer still sees its prediction and sample (step i + 1's Euler update, which
+    // replaces the sample, is queued after the check). elapsed_seconds is the device
+    // time from the end of the previous step (or the loop start) to the end of this one,
+    // from stream markers 0..2.
+    struct Pending {
+        size_t stat;
+        int step, slot, mark_from, mark_to;
+        DeviceMat prediction;
+    };
+    std::vector<Pending> pending;
+    auto resolve = [&]() {
+        Pending p = pending.back();
+        pending.clear();
+        int finite = 0;
+        check_status(ernie_hip_finite_end(ctx, p.slot, &finite), ctx, "Latent finite check");
+        double seconds = 0;
+        check_status(ernie_hip_marker_elapsed(ctx, p.mark_from, p.mark_to, &seconds), ctx, "Step timing");
+        DenoiseStepStats& st = stats[p.stat];
+        st.elapsed_seconds = seconds;
+        if (!finite) throw std::runtime_error("Non-finite latent after denoise step " + std::to_string(p.step + 1));
+        st.complete = true;
+        if (observer) observer(size_t(p.step), p.prediction, sample);
+    };
+
+    check_status(ernie_hip_marker_record(ctx, 0), ctx, "Step timing");
     DitModel dit{model.blocks};
     for (int i = start_step; i < steps; ++i) {
+        const int k = i - start_step;
         const auto start = Clock::now();
         DenoiseStepStats step;
         step.dit.collect_details = collect_details;
@@ -62,23 +107,25 @@ DeviceMat denoise(const DenoiseModel& model, const DeviceMat& initial, const std
         step.delta = schedule.delta(i);
         DeviceMat prediction;
         try {
-            const auto host_features = timestep_features(step.timestep);
-            features.upload(device, host_features.data(), host_features.size());
-            const std::vector<DeviceMat> inputs{sample, constants[0], features, constants[1], constants[2], constants[3]};
+            const std::vector<DeviceMat> inputs{sample,         constants[0], features.view(size_t(k) * 4096, 4096),
+                                                constants[1], constants[2], constants[3]};
             prediction = run_dit(dit, inputs, option, step.dit);
-            euler_step(device, sample, prediction, step.delta, sample);
-            if (!finite_latent(device, sample))
-                throw std::runtime_error("Non-finite latent after denoise step " + std::to_string(i + 1));
         } catch (...) {
+            // An earlier step's failure comes first (resolve throws it); else this one's.
+            if (!pending.empty()) resolve();
             step.elapsed_seconds = std::chrono::duration<double>(Clock::now() - start).count();
             stats.push_back(step);
             throw;
         }
-        step.elapsed_seconds = std::chrono::duration<double>(Clock::now() - start).count();
-        step.complete = true;
+        if (!pending.empty()) resolve();
+        euler_step(device, sample, prediction, step.delta, sample);
+        const int slot = k % 2;
+        check_status(ernie_hip_finite_begin(ctx, sample.data, sample.total(), slot), ctx, "Latent finite check");
+        check_status(ernie_hip_marker_record(ctx, (k + 1) % 3), ctx, "Step timing");
         stats.push_back(step);
-        if (observer) observer(size_t(i), prediction, sample);
+        pending.push_back({stats.size() - 1, i, slot, k % 3, (k + 1) % 3, prediction});
     }
+    resolve();
     return sample;
 }
 

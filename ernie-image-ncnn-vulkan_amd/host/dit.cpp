@@ -2,15 +2,32 @@
 // run_dit (src/dit.cpp:104-131): input head -> x, c and six modulations; the
 // blocks; output head -> prediction. Heads and blocks stay resident, so nothing
 // is loaded or released between stages.
+//
+// Without an observer or collect_details the whole DiT is queued on the context
+// stream and nothing waits for it. An observer sees every block output, as the
+// reference's does (it passes the observer into run_block_sequence,
+// src/dit.cpp:126 -> src/block_sequence.cpp:89): the blocks then run one call
+// each. collect_details times the heads and every block with device events and
+// waits once, at the end.
 #include "ernie/dit.h"
 
-#include <chrono>
 #include <stdexcept>
 
 namespace ernie {
 namespace {
-using Clock = std::chrono::steady_clock;
+
+// Stream markers of a timed DiT: before the input head, after it, after the blocks,
+// after the output head.
+enum { kMarkStart = 60, kMarkHead = 61, kMarkBlocks = 62, kMarkEnd = 63 };
+
+double marker_seconds(ernie_hip_ctx* ctx, int from, int to)
+{
+    double s = 0;
+    check_status(ernie_hip_marker_elapsed(ctx, from, to, &s), ctx, "DiT timing");
+    return s;
 }
+
+}  // namespace
 
 DeviceMat run_dit(const DitModel& model, const std::vector<DeviceMat>& inputs, const Option& option, DitStats& stats,
                   const StageObserver& observer)
@@ -41,37 +58,58 @@ DeviceMat run_dit(const DitModel& model, const std::vector<DeviceMat>& inputs, c
     DeviceMat c = cm.view(0, dim), mods = cm.view(dim, dim, 6, 1, 2);
     DeviceMat prediction = DeviceMat::create(device, latent.w, latent.h, latent.c, 3);
 
-    auto start = Clock::now();
+    if (collect_details) check_status(ernie_hip_marker_record(ctx, kMarkStart), ctx, "DiT timing");
     check_status(ernie_hip_input_head(ctx, latent.data, hw, T ? text.data : nullptr, T, features.data, x.data, c.data,
                                       mods.data),
                  ctx, "input head");
+    if (collect_details) check_status(ernie_hip_marker_record(ctx, kMarkHead), ctx, "DiT timing");
     if (observer) {
-        device.synchronize();
+        device.synchronize();  // the observer may read the tensors by any route
         observer("head-0", x);
         observer("head-1", c);
         for (int i = 0; i < 6; ++i) observer("head-" + std::to_string(i + 2), mods.view(size_t(i) * dim, dim));
     }
-    stats.input_head_seconds = std::chrono::duration<double>(Clock::now() - start).count();
 
     std::vector<int> indices;
     for (const auto& b : model.blocks) indices.push_back(b.index);
+    const int count = int(indices.size());
     std::vector<double> seconds(indices.size(), 0.0);
-    check_status(ernie_hip_block_sequence(ctx, indices.data(), int(indices.size()), x.data, x.data, mods.data, cos.data,
-                                          sin.data, mask_arg(mask), mask.valid_prefix, S,
-                                          seconds.data()),
-                 ctx, "extract block output");
-    stats.blocks.peak_loaded_nets = int(indices.size());
-    for (size_t i = 0; i < seconds.size(); ++i) {
-        stats.blocks.load_seconds.push_back(0.0);
-        stats.blocks.compute_seconds.push_back(seconds[i]);
-        stats.blocks.compute_submissions += 1;
-        if (collect_details) stats.blocks.details.push_back({int(i), "extract_compute_composite", "complete", seconds[i]});
+    double* timing = collect_details ? seconds.data() : nullptr;
+    if (observer) {
+        // One block per call, the observer after each ("block-i").
+        for (int i = 0; i < count; ++i) {
+            check_status(ernie_hip_block_sequence(ctx, &indices[i], 1, x.data, x.data, mods.data, cos.data, sin.data,
+                                                  mask_arg(mask), mask.valid_prefix, S, timing ? timing + i : nullptr),
+                         ctx, "extract block output");
+            device.synchronize();
+            observer("block-" + std::to_string(i), x);
+        }
+    } else {
+        check_status(ernie_hip_block_sequence(ctx, indices.data(), count, x.data, x.data, mods.data, cos.data, sin.data,
+                                              mask_arg(mask), mask.valid_prefix, S, timing),
+                     ctx, "extract block output");
     }
-    if (observer) observer("block-" + std::to_string(indices.size() - 1), x);
+    if (collect_details) check_status(ernie_hip_marker_record(ctx, kMarkBlocks), ctx, "DiT timing");
+    stats.blocks.peak_loaded_nets = count;
+    stats.blocks.compute_submissions = count;
+    // Per-block device time is measured only when details are collected; otherwise no
+    // entry is recorded and a metrics consumer attributes the step's whole time to
+    // compute (as src/pipeline.cpp:56-66 does with what remains unaccounted).
+    if (collect_details)
+        for (int i = 0; i < count; ++i) {
+            stats.blocks.load_seconds.push_back(0.0);
+            stats.blocks.compute_seconds.push_back(seconds[i]);
+            stats.blocks.details.push_back({i, "extract_compute_composite", "complete", seconds[i]});
+        }
 
-    start = Clock::now();
     check_status(ernie_hip_output_head(ctx, x.data, S, hw, c.data, prediction.data), ctx, "output head");
-    stats.output_head_seconds = std::chrono::duration<double>(Clock::now() - start).count();
+    if (collect_details) {
+        check_status(ernie_hip_marker_record(ctx, kMarkEnd), ctx, "DiT timing");
+        stats.input_head_seconds = marker_seconds(ctx, kMarkStart, kMarkHead);
+        stats.output_head_seconds = marker_seconds(ctx, kMarkBlocks, kMarkEnd);
+        stats.details.push_back({"input-head", "compute", "complete", stats.input_head_seconds});
+        stats.details.push_back({"output-head", "compute", "complete", stats.output_head_seconds});
+    }
     return prediction;
 }
 

@@ -19,6 +19,8 @@ struct DenoiseModel {
 struct DenoiseStepStats {
     float timestep = 0, delta = 0;
     DitStats dit;
+    // Device time from the end of the previous step (or the loop start) to the end of
+    // this one; steps are queued without waiting, so host time would not measure them.
     double elapsed_seconds = 0;
     bool complete = false;
 };

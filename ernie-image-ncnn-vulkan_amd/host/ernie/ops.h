@@ -30,6 +30,9 @@ struct OpParams {
     std::vector<float> weights;  // e.g. the RMSNorm gamma (FP32), uploaded by the op
     int get(int id, int fallback) const;
     float get(int id, float fallback) const;
+    // "0=4096 1=1.000000e-6 2=1": the id=value list of a .param layer line; a value
+    // with '.', 'e' or 'E' is a float, else an int. Throws std::invalid_argument.
+    static OpParams parse(const std::string& text);
 };
 
 // Returns 0 / -1 / -100 like ncnn::Layer::forward.

@@ -23,18 +23,20 @@ struct GpuAllocationError : std::runtime_error {
 // Throws for a non-zero ernie_hip status (-100 -> GpuAllocationError).
 void check_status(int status, const ernie_hip_ctx* ctx, const char* action);
 
-// Device context: plays the role of the VulkanDevice + session allocators.
+// Device context: plays the role of the VulkanDevice + session allocators. The
+// ernie_hip context is shared with every DeviceMat allocated on it, so it is destroyed
+// when the Device and the last of those tensors are gone, in whichever order.
 class Device {
 public:
     explicit Device(int index = 0);
-    ~Device();
     Device(const Device&) = delete;
     Device& operator=(const Device&) = delete;
-    ernie_hip_ctx* ctx() const { return ctx_; }
+    ernie_hip_ctx* ctx() const { return ctx_.get(); }
+    const std::shared_ptr<ernie_hip_ctx>& shared_ctx() const { return ctx_; }
     void synchronize() const;
 
 private:
-    ernie_hip_ctx* ctx_ = nullptr;
+    std::shared_ptr<ernie_hip_ctx> ctx_;
 };
 
 // Refcounted FP32 device tensor with ncnn's w/h/c dimension naming (w fastest).

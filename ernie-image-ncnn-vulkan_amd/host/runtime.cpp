@@ -15,14 +15,14 @@ void check_status(int status, const ernie_hip_ctx* ctx, const char* action)
 
 Device::Device(int index)
 {
-    const int rc = ernie_hip_create(index, &ctx_);
+    ernie_hip_ctx* ctx = nullptr;
+    const int rc = ernie_hip_create(index, &ctx);
     if (rc == ERNIE_ALLOCATION_FAILED) throw GpuAllocationError("Create device context");
-    if (rc != ERNIE_OK || !ctx_) throw std::runtime_error("No HIP device " + std::to_string(index));
+    if (rc != ERNIE_OK || !ctx) throw std::runtime_error("No HIP device " + std::to_string(index));
+    ctx_ = std::shared_ptr<ernie_hip_ctx>(ctx, ernie_hip_destroy);
 }
 
-Device::~Device() { ernie_hip_destroy(ctx_); }
-
-void Device::synchronize() const { check_status(ernie_hip_synchronize(ctx_), ctx_, "synchronize"); }
+void Device::synchronize() const { check_status(ernie_hip_synchronize(ctx()), ctx(), "synchronize"); }
 
 DeviceMat DeviceMat::create(const Device& device, int w, int h, int c, int dims)
 {
@@ -31,7 +31,9 @@ DeviceMat DeviceMat::create(const Device& device, int w, int h, int c, int dims)
     ernie_hip_ctx* ctx = device.ctx();
     check_status(ernie_hip_malloc(ctx, size_t(w) * h * c * sizeof(float), &p), ctx, "Allocate device tensor");
     DeviceMat m;
-    m.holder = std::shared_ptr<void>(p, [ctx](void* q) { ernie_hip_free(ctx, q); });
+    // The deleter keeps the context alive: a tensor may outlive its Device.
+    std::shared_ptr<ernie_hip_ctx> owner = device.shared_ctx();
+    m.holder = std::shared_ptr<void>(p, [owner](void* q) { ernie_hip_free(owner.get(), q); });
     m.data = static_cast<float*>(p);
     m.w = w;
     m.h = h;

@@ -61,6 +61,52 @@ int ernie_denoise(ernie_device* device, const int* blocks, int count, float* lat
                   int valid_prefix, int steps, int start_step, int storage_dtype, double* step_seconds,
                   float* step_timesteps, char* err, size_t errlen);
 
+/* Observer of run_dit's stages (the StageObserver of src/dit.h:17-40): "head-0"
+ * (x [S][dim]), "head-1" (c [dim]) and "head-2".."head-7" (the six modulations) after the
+ * input head, then "block-i" after block i (x). `data` is device FP32 memory of w*h*c
+ * values, readable during the callback only (the device has finished writing it). */
+typedef void (*ernie_stage_observer)(const char* stage, const float* data, int w, int h, int c, void* user);
+/* run_dit (src/dit.h:17-40; src/dit.cpp:104-131): latent [128][height][width], text
+ * [text_tokens][3072], time features [dim] (4096 for the ERNIE model), cos/sin [S][128],
+ * mask [S] (all device FP32) -> prediction [128][height][width] (device FP32).
+ * block_seconds (nullable, `count` entries) requests per-block device timing
+ * (DitStats::collect_details). */
+int ernie_run_dit(ernie_device* device, const int* blocks, int count, const float* latent, int height, int width,
+                  const float* text, int text_tokens, const float* time_features, int dim, const float* cos_t,
+                  const float* sin_t, const float* mask, int valid_prefix, int storage_dtype, float* prediction,
+                  double* block_seconds, ernie_stage_observer observer, void* user, char* err, size_t errlen);
+/* Observer of denoise steps (src/denoiser.h:26-33): absolute step index, the step's
+ * prediction and the sample after its Euler update (device FP32, `count` values each),
+ * readable during the callback only. */
+typedef void (*ernie_step_observer)(int step, const float* prediction, const float* sample, size_t count,
+                                    void* user);
+/* ernie_denoise with a step observer (nullable) and DitStats::collect_details. */
+int ernie_denoise_observed(ernie_device* device, const int* blocks, int count, float* latent, int height, int width,
+                           const float* text, int text_tokens, const float* cos_t, const float* sin_t,
+                           const float* mask, int valid_prefix, int steps, int start_step, int storage_dtype,
+                           int collect_details, double* step_seconds, float* step_timesteps,
+                           ernie_step_observer observer, void* user, char* err, size_t errlen);
+
+/* ---- the op registry (register_layers, src/ernie_gelu.cpp:108-116) -------------- */
+/* One blob of an op call: device data, element type (ERNIE_DTYPE_*), ncnn dims w/h/c
+ * with w fastest and no channel padding. */
+typedef struct {
+    void* data;
+    int dtype;
+    int w, h, c;
+} ernie_op_blob;
+/* Registers the reference's custom layers ("ErnieGELU", "RMSNorm", "LayerNorm",
+ * "ErnieResidualAdd", "SDPA") plus "Gemm" into an OpRegistry and runs one forward of
+ * `type`, as a one-layer ncnn graph of that op would (probes/rmsnorm_probe.cpp:44-53,
+ * tests/test_bf16_gemm.cpp:64-75): `params` is the layer line's parameter list
+ * ("0=4096 1=1.000000e-6 2=1"; a value with '.', 'e' or 'E' is a float), `weights` its
+ * FP32 model data in .bin order without section tags. output_count 0 runs an in-place
+ * op on inputs[0]. Returns the layer's status (0, -1 rejected, -100 allocation) or -22
+ * for malformed parameter text; queued on the device stream. */
+int ernie_op_forward(ernie_device* device, const char* type, const char* params, const float* weights,
+                     size_t weight_count, const ernie_op_blob* inputs, int input_count, ernie_op_blob* outputs,
+                     int output_count, char* err, size_t errlen);
+
 /* ---- Mistral text path (src/text_encoder.h) ------------------------------------ */
 /* text_constants (src/text_encoder.cpp:92-118) on the host from the 64 YaRN inverse
  * frequencies: cos/sin [bucket][128], causal mask [bucket][bucket]. */

@@ -50,10 +50,16 @@ void* ernie_hip_get_stream(ernie_hip_ctx* ctx);
 int ernie_hip_synchronize(ernie_hip_ctx* ctx);
 /* Device memory owned by the context's caller-facing allocator. Freed blocks (up to
  * 8 GiB) are kept for reuse by later allocations of the same rounded size and released
- * by ernie_hip_destroy: hipFree synchronises the device. Reuse is ordered by the
- * context stream, so memory freed here must not be in use on another stream. */
+ * by ernie_hip_trim or ernie_hip_destroy: hipFree synchronises the device. Reuse is
+ * ordered by the context stream, so memory freed here must not be in use on another
+ * stream. Blocks still allocated are freed by ernie_hip_destroy, which must therefore
+ * come after the last ernie_hip_free of the context. */
 int ernie_hip_malloc(ernie_hip_ctx* ctx, size_t bytes, void** out);
 int ernie_hip_free(ernie_hip_ctx* ctx, void* ptr);
+/* Waits for the context stream and returns every cached freed block to the driver;
+ * returns the bytes released. An allocation that finds the device out of memory does
+ * the same once before it fails. */
+size_t ernie_hip_trim(ernie_hip_ctx* ctx);
 int ernie_hip_memcpy_h2d(ernie_hip_ctx* ctx, void* dst, const void* src, size_t bytes);
 int ernie_hip_memcpy_d2h(ernie_hip_ctx* ctx, void* dst, const void* src, size_t bytes);
 
@@ -116,10 +122,29 @@ int ernie_hip_euler_step(ernie_hip_ctx* ctx, const float* x, const float* v, flo
                          float* out);
 /* finite_latent (src/latent_ops.cpp:60-70): synchronises; *finite = 1 if all finite. */
 int ernie_hip_finite(ernie_hip_ctx* ctx, const float* x, size_t count, int* finite);
+/* The same check split in two so a denoise step needs no queue drain. The reference
+ * submits its finite shader and waits (VulkanLatentOps::finite_latent,
+ * src/latent_ops.cpp:160-183); here _begin queues the check of x and the copy of its
+ * flag to pinned host memory in `slot`, and _end waits for that copy only (work queued
+ * after _begin keeps the device busy meanwhile). One check may be pending per slot. */
+#define ERNIE_FINITE_SLOTS 4
+int ernie_hip_finite_begin(ernie_hip_ctx* ctx, const float* x, size_t count, int slot);
+int ernie_hip_finite_end(ernie_hip_ctx* ctx, int slot, int* finite);
+/* Stream markers: pooled HIP events recorded on the context stream without a wait;
+ * _elapsed waits for marker `to` and returns the device time from `from` to `to`. They
+ * stand in for the host clock the reference reads around each synchronous submission
+ * (src/denoiser.cpp:104-146, src/block_sequence.cpp:241-253). */
+#define ERNIE_MARKERS 64
+int ernie_hip_marker_record(ernie_hip_ctx* ctx, int marker);
+int ernie_hip_marker_elapsed(ernie_hip_ctx* ctx, int from, int to, double* seconds);
 /* Counter-based N(mean, std) synthetic data directly in device memory. */
 int ernie_hip_fill_normal(ernie_hip_ctx* ctx, void* out, int dtype, size_t count, uint64_t seed,
                           uint64_t offset, float mean, float std_dev);
 int ernie_hip_convert(ernie_hip_ctx* ctx, const void* in, int in_dtype, void* out, int out_dtype, size_t count);
+/* out [cols][rows] = in [rows][cols] (element type dtype; separate buffers): the operand
+ * and result transposes of ncnn's Gemm (2=transA, 14=output_transpose), which the
+ * registry's "Gemm" applies around the NT kernel. */
+int ernie_hip_transpose(ernie_hip_ctx* ctx, const void* in, int dtype, int rows, int cols, void* out);
 
 /* ---- resident block weights (replaces per-block Net load/destroy,
  *      src/block_sequence.cpp:137-142, 241-261; all 36 blocks fit in HBM) ------- */

@@ -1,7 +1,8 @@
 """Parity at the full sizes of the reference's larger runs.
 
 * Long-text FP32 run at 1376x768: 86x48 image tokens + a 2048-slot text bucket
-  with 1080 valid tokens (S = 6176); per-block outputs against the oracle
+  with 1080 valid tokens (S = 6176); one denoise step through the input head, all
+  36 blocks and the output head, every stage against the oracle
   (probes/block_sequence_runner.cpp:194-244 compares every block the same way).
 * Max-area BF16 run at 2048x1024: 128x64 image tokens + 2048 text slots with
   300 valid (S = 10240, 1748 masked keys); one block against the oracle.
@@ -22,7 +23,7 @@ import ernie_amd as E
 import kat
 import oracle as O
 from gpu_util import NAMES, dev, empty, host
-from test_oracle import small_block
+from test_oracle import small_block, small_heads
 
 pytestmark = pytest.mark.gpu
 
@@ -44,33 +45,89 @@ def run_block(ctx, index, x, mods, cos, sin, mask, valid):
     return host(out)
 
 
-def test_long_text_fp32_per_block(ctx):
-    # 1376x768: latent 48 rows x 86 columns, 4128 image tokens + 2048 text slots, 1080 valid.
-    S, image, valid_text = 6176, (86, 48), 1080
-    valid = 4128 + valid_text
-    x, mods, cos, sin, mask = block_inputs(S, image, valid_text, seed=5)
-    assert int(np.sum(mask == 0)) == valid
-    nblocks = 2
-    for b in range(nblocks):
-        ctx.block_upload(60 + b, small_block(DIM, FFN, seed=4, block=b), DIM, FFN, E.FP32)
-    cur = x
-    for b in range(nblocks):
-        got = run_block(ctx, 60 + b, cur, mods, cos, sin, mask, valid)
+# 1376x768: latent 48 rows x 86 columns, 4128 image tokens + 2048 text slots, 1080
+# valid; one denoise step at t = 1000: input head, 36 FP32 blocks, output head. Every
+# stage is graded against the oracle on the device's own input, as
+# probes/block_sequence_runner.cpp:194-244 grades each block of the stack. The step
+# runs as a chain of tests (the input head, four groups of nine blocks, the output
+# head) sharing the device's activations, so that none runs for minutes on its own.
+LONG = {"H": 48, "W": 86, "text": 2048, "valid_text": 1080}
+
+
+@pytest.fixture(scope="module")
+def long_step(ctx):
+    H, W, slots, vt = LONG["H"], LONG["W"], LONG["text"], LONG["valid_text"]
+    st = {"S": H * W + slots, "valid": H * W + vt, "heads": small_heads(dim=DIM, latent_ch=LATENT_CH,
+                                                                           text_dim=TEXT_DIM, seed=40)}
+    st["latent"] = O.normal((LATENT_CH, H, W), 5)
+    text = O.normal((slots, TEXT_DIM), 5, offset=1 << 40)
+    text[vt:] = 0.0  # pad_text
+    st["text"] = text
+    st["cos"], st["sin"], st["mask"] = O.dit_constants(O.rope_frequencies(), W, H, vt, slots)
+    yield st
+    for b in range(36):
+        if b in st.get("loaded", ()):
+            ctx.call("block_release", 100 + b)
+
+
+@pytest.mark.slow
+def test_long_text_fp32_step_input_head(ctx, long_step):
+    st = long_step
+    S = st["S"]
+    assert int(np.sum(st["mask"] == 0)) == st["valid"]
+    ctx.heads_upload(st["heads"], DIM, LATENT_CH, TEXT_DIM, E.FP32)
+    feat = O.timestep_features(1000.0)
+    x0, c, mods = empty((S, DIM)), empty((DIM,)), empty((6, DIM))
+    ctx.input_head(dev(st["latent"]), LONG["H"] * LONG["W"], dev(st["text"]), LONG["text"], dev(feat), x0, c, mods)
+    xr, cr, mr = O.input_head({k: st["heads"][k] for k in O.INPUT_HEAD_FIELDS}, st["latent"], st["text"], feat)
+    for got, ref in ((x0, xr), (c, cr), (mods, mr)):
+        g = kat.gate(host(got), ref, *kat.HEAD_GATES["fp32"])
+        assert g["passed"], g
+    st.update(x0=host(x0), cur=host(x0), c=host(c), mods=host(mods), loaded=set())
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("first", [0, 9, 18, 27], ids=lambda b: f"blocks{b}-{b + 8}")
+def test_long_text_fp32_step_blocks(ctx, long_step, first):
+    st = long_step
+    assert "cur" in st, "the input head test did not run"
+    S, valid = st["S"], st["valid"]
+    cd, sd, md, mods_d = dev(st["cos"]), dev(st["sin"]), dev(st["mask"]), dev(st["mods"])
+    for b in range(first, first + 9):
         t0 = time.perf_counter()
-        ref = O.block_forward(small_block(DIM, FFN, seed=4, block=b), cur, mods, cos, sin, mask)
-        print(f"block {b}: oracle {time.perf_counter() - t0:.1f} s", flush=True)
+        w = small_block(DIM, FFN, seed=4, block=b)
+        ctx.block_upload(100 + b, w, DIM, FFN, E.FP32)
+        st["loaded"].add(b)
+        out = empty((S, DIM))
+        ctx.block_forward(100 + b, dev(st["cur"]), out, mods_d, cd, sd, S, mask=md, valid_keys=valid)
+        got = host(out)
+        ref = O.block_forward(w, st["cur"], st["mods"], st["cos"], st["sin"], st["mask"])
+        del w
         m = kat.fp32_block_rule(got, ref)
+        print(f"block {b}: max|d|/max|ref| {m['max_abs_error'] / m['reference_max_abs']:.3g}, "
+              f"{time.perf_counter() - t0:.1f} s", flush=True)
         assert m["passed"], (b, m)
         g = kat.gate(got, ref, *kat.BLOCK_GATES["fp32"])
         assert g["passed"], (b, g)
-        cur = got  # each block is graded on the device's own input
-    # The sequence entry point chains the same blocks bitwise.
+        st["cur"] = got
+
+
+@pytest.mark.slow
+def test_long_text_fp32_step_output_head(ctx, long_step):
+    st = long_step
+    assert len(st.get("loaded", ())) == 36, "the block tests did not all run"
+    S, hw = st["S"], LONG["H"] * LONG["W"]
+    pred = empty((LATENT_CH, hw))
+    ctx.output_head(dev(st["cur"]), S, hw, dev(st["c"]), pred)
+    h = st["heads"]
+    out_w = {"mod_w": h["out_mod_w"], "mod_b": h["out_mod_b"], "proj_w": h["proj_w"], "proj_b": h["proj_b"]}
+    g = kat.gate(host(pred), O.output_head(out_w, st["cur"], st["c"], hw), *kat.HEAD_GATES["fp32"])
+    assert g["passed"], g
+    # The sequence entry point chains the same 36 blocks bitwise.
     out = empty((S, DIM))
-    ctx.block_sequence([60 + b for b in range(nblocks)], dev(x), out, dev(mods), dev(cos), dev(sin), S,
-                       mask=dev(mask), valid_keys=valid)
-    np.testing.assert_array_equal(host(out), cur)
-    for b in range(nblocks):
-        ctx.call("block_release", 60 + b)
+    ctx.block_sequence([100 + b for b in range(36)], dev(st["x0"]), out, dev(st["mods"]), dev(st["cos"]),
+                       dev(st["sin"]), S, mask=dev(st["mask"]), valid_keys=st["valid"])
+    np.testing.assert_array_equal(host(out), st["cur"])
 
 
 def test_max_area_bf16_block(ctx):

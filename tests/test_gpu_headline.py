@@ -1,0 +1,124 @@
+"""Parity at the headline workload itself: the 1024x1024 DiT at full width (dim 4096,
+32 heads, FFN 12288), S = 4096 image + 64 text slots with 40 valid, checked directly
+against the oracle.
+
+* One block, its input and modulations produced by the input head from the first
+  turbo step's time features (t = 1000), in FP32, FP16 and BF16, under the block gates
+  (tools/export_dit_block.py:163-165, tools/validate_dit_block.py:108-120); FP32 also
+  under max|d| <= 1e-4 max|ref|.
+* A 2-block, 2-step turbo denoise with heads at 4096 through the facade: every step's
+  prediction against the oracle DiT under the DiT gates (tools/validate_dit.py:58-60)
+  and the final latent under the denoiser gates (tools/validate_denoiser.py:53-55).
+"""
+import ctypes
+import time
+
+import numpy as np
+import pytest
+
+import ernie_amd as E
+import kat
+import oracle as O
+from gpu_util import NAMES, dev, empty, host
+from test_oracle import small_block, small_heads
+
+pytestmark = [pytest.mark.gpu, pytest.mark.slow]
+
+DIM, FFN, GRID, TEXT, VALID = 4096, 12288, 64, 64, 40
+S = GRID * GRID + TEXT
+
+
+def conditioning(seed):
+    heads = small_heads(dim=DIM, latent_ch=128, text_dim=3072, seed=seed)
+    latent = O.normal((128, GRID, GRID), seed + 3)
+    text = O.normal((TEXT, 3072), seed + 4)
+    text[VALID:] = 0.0  # pad_text
+    cos, sin, mask = O.dit_constants(O.rope_frequencies(), GRID, GRID, VALID, TEXT)
+    return heads, latent, text, cos, sin, mask
+
+
+def test_headline_block_against_oracle(ctx):
+    heads, latent, text, cos, sin, mask = conditioning(0)
+    feat = O.timestep_features(1000.0)
+    x, _, mods = O.input_head({k: heads[k] for k in O.INPUT_HEAD_FIELDS}, latent, text, feat)
+    w = small_block(DIM, FFN, seed=0)
+    t0 = time.perf_counter()
+    ref = O.block_forward(w, x, mods, cos, sin, mask)
+    print(f"oracle block at S={S}: {time.perf_counter() - t0:.1f} s", flush=True)
+    valid = GRID * GRID + VALID
+    assert int(np.sum(mask == 0)) == valid
+    for dt in (E.FP32, E.FP16, E.BF16):
+        ctx.block_upload(80, w, DIM, FFN, dt)
+        out = empty((S, DIM))
+        ctx.block_forward(80, dev(x), out, dev(mods), dev(cos), dev(sin), S, mask=dev(mask), valid_keys=valid)
+        got = host(out)
+        g = kat.gate(got, ref, *kat.BLOCK_GATES[NAMES[dt]])
+        print(f"{NAMES[dt]} block: max|d| {g['max_abs_error']:.3g} (limit {g['max_abs_limit']:.3g}), "
+              f"nrmse {g['nrmse']:.3g} (limit {g['nrmse_limit']:.3g})", flush=True)
+        assert g["passed"], (NAMES[dt], g)
+        if dt == E.FP32:
+            m = kat.fp32_block_rule(got, ref)
+            print(f"fp32 block: max|d| / max|ref| = {m['max_abs_error'] / m['reference_max_abs']:.3g}", flush=True)
+            assert m["passed"], m
+    ctx.call("block_release", 80)
+
+
+def oracle_prediction(heads, blocks, latent, text, feat, cos, sin, mask):
+    x, c, mods = O.input_head({k: heads[k] for k in O.INPUT_HEAD_FIELDS}, latent, text, feat)
+    for w in blocks:
+        x = O.block_forward(w, x, mods, cos, sin, mask)
+    out_w = {"mod_w": heads["out_mod_w"], "mod_b": heads["out_mod_b"], "proj_w": heads["proj_w"],
+             "proj_b": heads["proj_b"]}
+    return O.output_head(out_w, x, c, GRID * GRID).reshape(latent.shape)
+
+
+@pytest.fixture(scope="module")
+def two_step_oracle():
+    heads, latent, text, cos, sin, mask = conditioning(10)
+    blocks = [small_block(DIM, FFN, seed=11, block=b) for b in range(2)]
+    sig, ts = O.flow_schedule_turbo(2)
+    preds, samples = [], []
+    z = latent.copy()
+    t0 = time.perf_counter()
+    for i in range(2):
+        p = oracle_prediction(heads, blocks, z, text, O.timestep_features(float(ts[i])), cos, sin, mask)
+        z = O.euler_step(z, p, sig[i + 1] - sig[i])
+        preds.append(p)
+        samples.append(z)
+    print(f"oracle 2-step denoise: {time.perf_counter() - t0:.1f} s", flush=True)
+    return heads, blocks, latent, text, cos, sin, mask, preds, samples
+
+
+@pytest.mark.parametrize("dt", [E.FP32, E.FP16], ids=lambda d: NAMES[d])
+def test_headline_two_step_denoise_against_oracle(two_step_oracle, dt):
+    import torch
+    heads, blocks, latent, text, cos, sin, mask, preds, samples = two_step_oracle
+    fac = E.Facade(0)
+    try:
+        fac.hip.heads_upload(heads, DIM, 128, 3072, dt)
+        for b, w in enumerate(blocks):
+            fac.hip.block_upload(b, w, DIM, FFN, dt)
+        seen = []
+
+        def observer(step, pred_ptr, sample_ptr, count):
+            p = np.empty(count, np.float32)
+            fac.hip.call("memcpy_d2h", p.ctypes.data, ctypes.c_void_p(pred_ptr), count * 4)
+            seen.append((step, p.reshape(latent.shape)))
+
+        lat = dev(latent)
+        secs, _ = fac.denoise_observed([0, 1], lat, GRID, GRID, dev(text), TEXT, dev(cos), dev(sin), dev(mask),
+                                       GRID * GRID + VALID, 2, dtype=dt, observer=observer)
+        assert [s for s, _ in seen] == [0, 1] and np.all(secs > 0)
+        for (step, p), ref in zip(seen, preds):
+            g = kat.gate(p, ref, *kat.SEQUENCE_GATES[NAMES[dt]])
+            print(f"{NAMES[dt]} step {step} prediction: max|d| {g['max_abs_error']:.3g} "
+                  f"(limit {g['max_abs_limit']:.3g}), nrmse {g['nrmse']:.3g}", flush=True)
+            assert g["passed"], (step, g)
+        nrmse, rtol, atol = kat.DENOISER_GATES[NAMES[dt]]
+        g = kat.gate(host(lat), samples[-1], atol, rtol, nrmse)
+        print(f"{NAMES[dt]} final latent: max|d| {g['max_abs_error']:.3g}, nrmse {g['nrmse']:.3g}", flush=True)
+        assert g["passed"], g
+    finally:
+        torch.cuda.synchronize()
+        fac.close()
+        torch.cuda.empty_cache()
