@@ -109,6 +109,10 @@ struct ernie_hip_ctx {
     hipEvent_t marker[ERNIE_MARKERS] = {};
     bool marker_recorded[ERNIE_MARKERS] = {};
     std::vector<hipEvent_t> seq_events;
+    // Pinned staging blocks of ernie_hip_upload_async, each with the event of its last
+    // copy: a block is reused once that copy has finished.
+    struct Staging { void* host; size_t bytes; hipEvent_t done; };
+    std::vector<Staging> upload_staging;
     size_t event_next = 0;
     std::vector<Launch> pending;
     long launches[ERNIE_PROFILE_CLASSES] = {};
@@ -558,33 +562,81 @@ int ones_buffer(ernie_hip_ctx* ctx, int n, const float** out)
     return ERNIE_OK;
 }
 
+// Device buffers one text block forward works in: activations, the unit gate of the
+// residual epilogues, and the GEMM split-K partials.
+struct TextWs {
+    void *h, *qkv, *attn, *p;
+    float* x1;
+    const float* ones;
+    void* split_ws;
+    size_t split_ws_bytes;
+};
+
+// Activation bytes of one text block forward: h, qkv, attention output, x1 and p, each
+// 256-byte aligned; `at` (nullable) receives their offsets in that order.
+size_t text_activation_bytes(const TextBlockWeights& w, int S, size_t* at = nullptr)
+{
+    const size_t e = esize(w.dtype), QD = (size_t)w.heads * 128, QKV = QD + 2 * (size_t)w.kv_heads * 128;
+    auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+    const size_t sizes[5] = {up((size_t)S * w.hidden * e), up((size_t)S * QKV * e), up((size_t)S * QD * e),
+                             up((size_t)S * w.hidden * 4), up((size_t)S * w.ffn * e)};
+    size_t total = 0;
+    for (int i = 0; i < 5; ++i) {
+        if (at) at[i] = total;
+        total += sizes[i];
+    }
+    return total;
+}
+
+TextWs text_ws_at(const TextBlockWeights& w, int S, void* activations)
+{
+    size_t at[5];
+    text_activation_bytes(w, S, at);
+    char* b = static_cast<char*>(activations);
+    TextWs ws{};
+    ws.h = b + at[0];
+    ws.qkv = b + at[1];
+    ws.attn = b + at[2];
+    ws.x1 = reinterpret_cast<float*>(b + at[3]);
+    ws.p = b + at[4];
+    return ws;
+}
+
+int text_block_run(ernie_hip_ctx* ctx, const TextBlockWeights& w, const float* x, float* out, const float* cos_t,
+                   const float* sin_t, const float* mask, int causal, int S, const TextWs& ws);
+
 // rmsn_8 -> gemm_0/1/2 -> rotary (lines 18-44) -> sdpa_20 (GQA, additive mask in3) ->
 // gemm_3 + add_12 -> rmsn_9 -> gemm_4 (gate) silu_7, gemm_5 (up), mul_13 -> gemm_6 + add_14.
 // The residual adds are the GEMM epilogues with a unit gate; the gated MLP is one GEMM
-// over the interleaved up/gate rows with a SiLU epilogue. out may alias x.
+// over the interleaved up/gate rows with a SiLU epilogue. out may alias x. The
+// workspace comes from the context (grown on demand).
 int text_block_forward(ernie_hip_ctx* ctx, const TextBlockWeights& w, const float* x, float* out, const float* cos_t,
                        const float* sin_t, const float* mask, int causal, int S)
+{
+    int rc = dev_alloc(ctx, ctx->text_ws, text_activation_bytes(w, S), "text workspace");
+    if (rc) return rc;
+    TextWs ws = text_ws_at(w, S, ctx->text_ws.ptr);
+    rc = ones_buffer(ctx, w.hidden, &ws.ones);
+    if (rc) return rc;
+    rc = split_workspace(ctx, S, w.heads, &ws.split_ws, &ws.split_ws_bytes);
+    if (rc) return rc;
+    return text_block_run(ctx, w, x, out, cos_t, sin_t, mask, causal, S, ws);
+}
+
+int text_block_run(ernie_hip_ctx* ctx, const TextBlockWeights& w, const float* x, float* out, const float* cos_t,
+                   const float* sin_t, const float* mask, int causal, int S, const TextWs& ws)
 {
     const int H = w.hidden, F = w.ffn, nq = w.heads, nk = w.kv_heads, dt = w.dtype;
     const int QD = nq * 128, KVD = nk * 128, QKV = QD + 2 * KVD;
     const size_t e = esize(dt);
     const double dS = S;
-    auto up = [](size_t b) { return (b + 255) / 256 * 256; };
-    const size_t bh = up((size_t)S * H * e), bqkv = up((size_t)S * QKV * e), battn = up((size_t)S * QD * e),
-                 bx1 = up((size_t)S * H * 4), bp = up((size_t)S * F * e);
-    int rc = dev_alloc(ctx, ctx->text_ws, bh + bqkv + battn + bx1 + bp, "text workspace");
-    if (rc) return rc;
-    char* base = static_cast<char*>(ctx->text_ws.ptr);
-    void *h = base, *qkv = base + bh, *attn = base + bh + bqkv, *p = base + bh + bqkv + battn + bx1;
-    float* x1 = reinterpret_cast<float*>(base + bh + bqkv + battn);
-    const float* ones = nullptr;
-    rc = ones_buffer(ctx, H, &ones);
-    if (rc) return rc;
+    void *h = ws.h, *qkv = ws.qkv, *attn = ws.attn, *p = ws.p;
+    float* x1 = ws.x1;
+    const float* ones = ws.ones;
+    void* split_ws = ws.split_ws;
+    const size_t split_ws_bytes = ws.split_ws_bytes;
     hipStream_t s = ctx->stream;
-    void* split_ws = nullptr;
-    size_t split_ws_bytes = 0;
-    rc = split_workspace(ctx, S, nq, &split_ws, &split_ws_bytes);
-    if (rc) return rc;
+    int rc = 0;
     {
         Timed t(ctx, P_NORM, 0, dS * H * (4 + e));
         rc = kernel_status(ctx, rmsnorm_modulate(x, ERNIE_DTYPE_FP32, static_cast<const float*>(w.norm1.ptr), nullptr,
@@ -859,6 +911,10 @@ void ernie_hip_destroy(ernie_hip_ctx* ctx)
     dev_free(ctx->split_ws);
     for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
     for (hipEvent_t e : ctx->seq_events) (void)hipEventDestroy(e);
+    for (auto& st : ctx->upload_staging) {
+        (void)hipEventDestroy(st.done);
+        (void)hipHostFree(st.host);
+    }
     for (hipEvent_t e : ctx->marker)
         if (e) (void)hipEventDestroy(e);
     for (hipEvent_t e : ctx->finite_event)
@@ -951,6 +1007,35 @@ int ernie_hip_memcpy_h2d(ernie_hip_ctx* ctx, void* dst, const void* src, size_t 
     if (!ctx) return ERNIE_ERROR;
     int rc = hip_status(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "h2d");
     return rc ? rc : hip_status(ctx, hipStreamSynchronize(ctx->stream), "h2d");
+}
+
+int ernie_hip_upload_async(ernie_hip_ctx* ctx, void* dst, const void* src, size_t bytes)
+{
+    if (!ctx || (!src && bytes) || (!dst && bytes)) return ERNIE_ERROR;
+    if (!bytes) return ERNIE_OK;
+    // A staging block whose previous copy has finished and that is large enough.
+    ernie_hip_ctx::Staging* st = nullptr;
+    for (auto& b : ctx->upload_staging)
+        if (b.bytes >= bytes && hipEventQuery(b.done) == hipSuccess) {
+            st = &b;
+            break;
+        }
+    if (!st) {
+        if (ctx->upload_staging.size() >= 64) return fail(ctx, ERNIE_ERROR, "too many uploads in flight");
+        ernie_hip_ctx::Staging b{nullptr, std::max<size_t>(bytes, size_t(64) << 10), nullptr};
+        int rc = hip_status(ctx, hipHostMalloc(&b.host, b.bytes, 0), "upload staging");
+        if (!rc) rc = hip_status(ctx, hipEventCreateWithFlags(&b.done, hipEventDisableTiming), "upload staging");
+        if (rc) {
+            if (b.host) (void)hipHostFree(b.host);
+            return rc;
+        }
+        ctx->upload_staging.push_back(b);
+        st = &ctx->upload_staging.back();
+    }
+    std::memcpy(st->host, src, bytes);
+    int rc = hip_status(ctx, hipMemcpyAsync(dst, st->host, bytes, hipMemcpyHostToDevice, ctx->stream), "upload");
+    if (!rc) rc = hip_status(ctx, hipEventRecord(st->done, ctx->stream), "upload");
+    return rc;
 }
 
 int ernie_hip_memcpy_d2h(ernie_hip_ctx* ctx, void* dst, const void* src, size_t bytes)

@@ -97,6 +97,7 @@ def hip():
             "ernie_hip_marker_record": (c_int, [c_vp, c_int]),
             "ernie_hip_marker_elapsed": (c_int, [c_vp, c_int, c_int, ctypes.POINTER(c_double)]),
             "ernie_hip_trim": (c_size_t, [c_vp]),
+            "ernie_hip_upload_async": (c_int, [c_vp, c_vp, c_vp, c_size_t]),
             "ernie_hip_transpose": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_vp]),
             "ernie_hip_fill_normal": (c_int, [c_vp, c_vp, c_int, c_size_t, c_u64, c_u64, c_float, c_float]),
             "ernie_hip_convert": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_size_t]),

@@ -52,22 +52,32 @@ DeviceMat denoise(const DenoiseModel& model, const DeviceMat& initial, const std
     DeviceMat sample = DeviceMat::create(device, initial.w, initial.h, initial.c, 3);
     check_status(ernie_hip_convert(ctx, initial.data, ERNIE_DTYPE_FP32, sample.data, ERNIE_DTYPE_FP32, initial.total()),
                  ctx, "copy initial latent");
-    if (!finite_latent(device, sample)) throw std::invalid_argument("Initial latent is not finite");
     const int executed = steps - start_step;
-    if (!executed) return sample;
-
-    // The time features of every executed step (computed on the host in the reference's
-    // FP32 order, src/denoiser.cpp:22-39) go to the device in one copy before the loop,
-    // instead of one blocking upload per step.
-    DeviceMat features = DeviceMat::create(device, 4096, executed, 1, 2);
-    {
-        std::vector<float> host(size_t(executed) * 4096);
-        for (int k = 0; k < executed; ++k) {
-            const auto f = timestep_features(schedule.timesteps[start_step + k]);
-            std::copy(f.begin(), f.end(), host.begin() + size_t(k) * 4096);
-        }
-        features.upload(device, host.data(), host.size());
+    if (!executed) {
+        if (!finite_latent(device, sample)) throw std::invalid_argument("Initial latent is not finite");
+        return sample;
     }
+
+    // Time features (computed on the host in the reference's FP32 order,
+    // src/denoiser.cpp:22-39) go to the device through pinned staging without a wait:
+    // step 0's before its DiT, every later step's while the previous step runs.
+    DeviceMat features = DeviceMat::create(device, 4096, executed, 1, 2);
+    auto upload_features = [&](int k) {
+        const auto f = timestep_features(schedule.timesteps[start_step + k]);
+        check_status(ernie_hip_upload_async(ctx, features.data + size_t(k) * 4096, f.data(), f.size() * sizeof(float)),
+                     ctx, "Upload time features");
+    };
+    upload_features(0);
+    // The initial latent's check is read once step 0's DiT is queued (the reference
+    // rejects a non-finite initial latent before any step, src/denoiser.cpp:56-57; here
+    // the queued work of that step is simply dropped).
+    constexpr int kInitialSlot = 2;
+    check_status(ernie_hip_finite_begin(ctx, sample.data, sample.total(), kInitialSlot), ctx, "Latent finite check");
+    auto check_initial = [&]() {
+        int finite = 0;
+        check_status(ernie_hip_finite_end(ctx, kInitialSlot, &finite), ctx, "Latent finite check");
+        if (!finite) throw std::invalid_argument("Initial latent is not finite");
+    };
 
     // Each step is queued without a wait. Its finiteness flag is read one step behind:
     // step i's check is awaited after step i + 1's DiT has been queued, so the device
@@ -111,12 +121,14 @@ DeviceMat denoise(const DenoiseModel& model, const DeviceMat& initial, const std
                                                 constants[1], constants[2], constants[3]};
             prediction = run_dit(dit, inputs, option, step.dit);
         } catch (...) {
-            // An earlier step's failure comes first (resolve throws it); else this one's.
+            // An earlier failure comes first (check_initial / resolve throw it); else this one's.
+            if (k == 0) check_initial();
             if (!pending.empty()) resolve();
             step.elapsed_seconds = std::chrono::duration<double>(Clock::now() - start).count();
             stats.push_back(step);
             throw;
         }
+        if (k == 0) check_initial();
         if (!pending.empty()) resolve();
         euler_step(device, sample, prediction, step.delta, sample);
         const int slot = k % 2;
@@ -124,6 +136,7 @@ DeviceMat denoise(const DenoiseModel& model, const DeviceMat& initial, const std
         check_status(ernie_hip_marker_record(ctx, (k + 1) % 3), ctx, "Step timing");
         stats.push_back(step);
         pending.push_back({stats.size() - 1, i, slot, k % 3, (k + 1) % 3, prediction});
+        if (k + 1 < executed) upload_features(k + 1);
     }
     resolve();
     return sample;

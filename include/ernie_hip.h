@@ -62,6 +62,11 @@ int ernie_hip_free(ernie_hip_ctx* ctx, void* ptr);
 size_t ernie_hip_trim(ernie_hip_ctx* ctx);
 int ernie_hip_memcpy_h2d(ernie_hip_ctx* ctx, void* dst, const void* src, size_t bytes);
 int ernie_hip_memcpy_d2h(ernie_hip_ctx* ctx, void* dst, const void* src, size_t bytes);
+/* Queues a host-to-device copy without waiting: src is first copied into pinned
+ * staging memory owned by the context, so the caller may reuse it on return. The
+ * reference records such uploads into the step's command buffer
+ * (command.record_upload, src/denoiser.cpp:120-125). */
+int ernie_hip_upload_async(ernie_hip_ctx* ctx, void* dst, const void* src, size_t bytes);
 
 /* ---- operators: the custom layers the reference registers --------------------
  * register_layers (src/ernie_gelu.cpp:108-116) maps op names to these. */

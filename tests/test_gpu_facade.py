@@ -54,6 +54,16 @@ def test_finite_check_in_flight_on_two_slots(ctx):
 E_SLOTS = 4
 
 
+def test_upload_async_copies_before_the_source_is_reused(ctx):
+    import torch
+    dst = torch.empty(3 * 4096, dtype=torch.float32, device="cuda")
+    src = np.arange(4096, dtype=np.float32)
+    for k in range(3):
+        ctx.call("upload_async", ctypes.c_void_p(dst.data_ptr() + k * 4096 * 4), src.ctypes.data, 4096 * 4)
+        src += 4096  # the caller's buffer changes right away
+    np.testing.assert_array_equal(host(dst), np.arange(3 * 4096, dtype=np.float32))
+
+
 def test_trim_releases_freed_blocks():
     import torch
     fac = E.Facade(0)
@@ -195,6 +205,13 @@ def test_denoise_names_the_non_finite_step(start):
             fac.denoise_observed([0], dev(O.normal((128, H, W), 98)), H, W, dev(tx), text, dev(cos), dev(sin),
                                  dev(mask), H * W + valid, 4, start_step=start, dtype=E.FP16,
                                  observer=lambda *a: seen.append(a[0]))
+        assert seen == []
+        # A non-finite initial latent is rejected as an invalid request (src/denoiser.cpp:56-57).
+        bad = O.normal((128, H, W), 98)
+        bad[5, 1, 2] = np.inf
+        with pytest.raises(E.ErnieInvalidRequest, match="Initial latent is not finite"):
+            fac.denoise_observed([0], dev(bad), H, W, dev(tx), text, dev(cos), dev(sin), dev(mask), H * W + valid, 4,
+                                 start_step=start, dtype=E.FP16, observer=lambda *a: seen.append(a[0]))
         assert seen == []
     finally:
         torch.cuda.synchronize()
