@@ -21,7 +21,8 @@ LIB = PKG / "lib"
 OBJ = LIB / "obj"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 
-HIP_SOURCES = ["gemm.hip", "gemm16_pp.hip", "sdpa.hip", "sdpa16_dl.hip", "pointwise.hip", "ernie_hip.cpp"]
+HIP_SOURCES = ["gemm.hip", "gemm16_pp.hip", "sdpa.hip", "sdpa16_dl.hip", "pointwise.hip", "noalloc.hip",
+               "ernie_hip.cpp"]
 HOST_SOURCES = ["runtime.cpp", "conditioning.cpp", "latent_ops.cpp", "denoiser.cpp", "block_sequence.cpp", "dit.cpp", "ops.cpp",
                 "sha256.cpp", "block_files.cpp", "text_encoder.cpp", "capi.cpp"]
 

@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "kernels.hpp"
+#include "noalloc.hpp"
 
 using namespace ehip;
 
@@ -70,6 +71,9 @@ struct Launch {
 
 struct ernie_hip_ctx {
     int device = 0;
+    // This device's copy of the fixed scratch (noalloc.hip), looked up at creation;
+    // nullptr when the lookup failed (the no-allocation entry point then refuses).
+    void* scratch = nullptr;
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     std::string error;
@@ -890,6 +894,7 @@ int ernie_hip_create(int device, ernie_hip_ctx** out)
         return ERNIE_ERROR;
     }
     ctx->stream = ctx->own_stream;
+    if (scratch_init(device) == 0) ctx->scratch = scratch_address(device);
     *out = ctx;
     return ERNIE_OK;
 }
@@ -1497,6 +1502,38 @@ int ernie_hip_text_block_forward(ernie_hip_ctx* ctx, int index, const float* x, 
     const int rc = check_text_call(ctx, index, S, x, out, cos_t, sin_t);
     if (rc) return rc;
     return text_block_forward(ctx, ctx->text_blocks[index], x, out, cos_t, sin_t, mask, causal, S);
+}
+
+int ernie_hip_text_block_forward_noalloc(ernie_hip_ctx* ctx, int index, const float* x, float* out,
+                                         const float* cos_t, const float* sin_t, const float* mask, int causal, int S)
+{
+    if (!ctx) return ERNIE_ERROR;
+    int rc = check_text_call(ctx, index, S, x, out, cos_t, sin_t);
+    if (rc) return rc;
+    if (!ctx->scratch) return fail(ctx, ERNIE_ERROR, "fixed scratch unavailable on this device");
+    const TextBlockWeights& w = ctx->text_blocks[index];
+    // With at most 64 tokens every GEMM is one partial row of tiles, whose split-K
+    // partials (at most 256 parts of 64 x 256 FP32) fit the 16 MiB split region, and the
+    // attention has no query tile to split.
+    if (S > ERNIE_NOALLOC_TEXT_TOKENS)
+        return fail(ctx, ERNIE_ERROR, "no-allocation text block: at most " +
+                                          std::to_string(ERNIE_NOALLOC_TEXT_TOKENS) + " tokens");
+    const size_t act = text_activation_bytes(w, S), ones = ((size_t)w.hidden * 4 + 255) / 256 * 256;
+    if (act + ones > kScratchBytes - kScratchSplitBytes)
+        return fail(ctx, ERNIE_ERROR, "no-allocation text block: activations exceed the " +
+                                          std::to_string((kScratchBytes - kScratchSplitBytes) >> 20) +
+                                          " MiB scratch");
+    char* base = static_cast<char*>(ctx->scratch);
+    TextWs ws = text_ws_at(w, S, base + kScratchSplitBytes);
+    float* ones_ptr = reinterpret_cast<float*>(base + kScratchSplitBytes + act);
+    // The scratch keeps the previous call's contents: the unit gate is rewritten (by a
+    // kernel, no memset node) every call; everything else is written before it is read.
+    rc = kernel_status(ctx, fill_int(reinterpret_cast<int*>(ones_ptr), 0x3f800000, w.hidden, ctx->stream), "ones");
+    if (rc) return rc;
+    ws.ones = ones_ptr;
+    ws.split_ws = base;
+    ws.split_ws_bytes = kScratchSplitBytes;
+    return text_block_run(ctx, w, x, out, cos_t, sin_t, mask, causal, S, ws);
 }
 
 int ernie_hip_text_block_sequence(ernie_hip_ctx* ctx, const int* blocks, int count, const float* x, float* out,

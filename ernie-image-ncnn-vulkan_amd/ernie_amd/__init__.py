@@ -113,6 +113,8 @@ def hip():
             "ernie_hip_text_block_init_random": (c_int, [c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_u64,
                                                          c_float]),
             "ernie_hip_text_block_release": (c_int, [c_vp, c_int]),
+            "ernie_hip_text_block_forward_noalloc": (c_int, [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int,
+                                                             c_int]),
             "ernie_hip_text_block_forward": (c_int, [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int]),
             "ernie_hip_text_block_sequence": (c_int, [c_vp, c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int,
                                                       c_vp]),

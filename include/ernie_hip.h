@@ -239,6 +239,16 @@ int ernie_hip_text_block_release(ernie_hip_ctx* ctx, int index);
  * [S][hidden] FP32; out may alias x. */
 int ernie_hip_text_block_forward(ernie_hip_ctx* ctx, int index, const float* x, float* out, const float* cos_t,
                                  const float* sin_t, const float* mask, int causal, int S);
+/* ernie_hip_text_block_forward that allocates nothing, for callers that cannot call
+ * hipMalloc (code under HIP graph capture, tight serving loops). It has no counterpart
+ * in the reference. Its workspace is a fixed 24 MiB device array of the library (one per
+ * GPU, held until the process ends), so it takes at most ERNIE_NOALLOC_TEXT_TOKENS
+ * tokens (the reference's 32- and 64-token text buckets) and rejects larger calls with
+ * an error. Calls that overlap on one GPU share that array and race; calls on one
+ * context stream are ordered. Results are bitwise those of ernie_hip_text_block_forward. */
+#define ERNIE_NOALLOC_TEXT_TOKENS 64
+int ernie_hip_text_block_forward_noalloc(ernie_hip_ctx* ctx, int index, const float* x, float* out,
+                                         const float* cos_t, const float* sin_t, const float* mask, int causal, int S);
 /* run_text_blocks core (src/text_encoder.cpp:124-180): blocks[0..count), 1..25.
  * seconds (nullable) receives per-block device time. */
 int ernie_hip_text_block_sequence(ernie_hip_ctx* ctx, const int* blocks, int count, const float* x, float* out,
