@@ -92,9 +92,10 @@ def parse():
     ap.add_argument("--valid-text", type=int, default=40)
     ap.add_argument("--cpu-baseline", choices=("on", "off"), default="on")
     ap.add_argument("--cpu-tokens", type=int, default=4160, help="tokens of the single-block CPU sample")
-    ap.add_argument("--event-stride", type=int, default=4,
-                    help="with --events dominant, bracket every n-th launch of the dominant class: each event "
-                         "record leaves a ~5.7 us hole in the queue, which sampling keeps out of the timed steps")
+    ap.add_argument("--event-stride", type=int, default=9,
+                    help="with --events dominant, bracket every n-th launch of the dominant class (9: four of the "
+                         "36 per step): each event record leaves a ~5.6 us hole in the queue, so the timed steps "
+                         "sample the class's launches instead of bracketing every one")
     ap.add_argument("--events", choices=("dominant", "all"), default="dominant",
                     help="HIP events in the timed steps: around the dominant kernel class only (its roofline), or "
                          "around every launch; the per-class table always comes from one extra profiled step")

@@ -15,6 +15,16 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+// Q/K projection rows of a 16-bit block are stored permuted within each 128-row head,
+// so that the GEMM wave holding head dimension d also holds its rotary partner d + 64,
+// in the same lane, 32 columns further on: stored column c (wave half c / 64, position
+// l = c % 64) holds head dimension 32 (c / 64) + l % 32 + 64 (l / 32).
+__host__ __device__ constexpr int qk_dim_of_column(int c) { return (c >> 6) * 32 + (c & 31) + ((c >> 5) & 1) * 64; }
+__host__ __device__ constexpr int qk_stored_column(int d) { return ((d & 63) >> 5) * 64 + (d >> 6) * 32 + (d & 31); }
+static_assert(qk_stored_column(qk_dim_of_column(38)) == 38 && qk_dim_of_column(72) == 40 &&
+                  qk_dim_of_column(38) == 70 && qk_stored_column(100) == 100,
+              "Q/K head permutation");
+
 // Storage dtypes; values match ERNIE_DTYPE_* in the public header.
 enum DType : int { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
 

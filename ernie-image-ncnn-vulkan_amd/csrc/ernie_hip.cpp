@@ -41,6 +41,9 @@ struct BlockWeights {
     // 16-bit projections whose output count is a multiple of 256 are stored K-tiled,
     // [K/32][N][32] (GemmArgs::w_k32); flags for wqkv, wo, w_ug, w_down.
     bool k32[4] = {false, false, false, false};
+    // K-tiled wqkv whose Q and K rows are stored permuted within each head
+    // (qk_stored_column), so the QKV GEMM finishes Q/K norm and rotary in its epilogue.
+    bool qk_fused = false;
 };
 
 // One Mistral text decoder block (tests/fixtures/text-s64.ncnn.param), head_dim 128.
@@ -334,7 +337,8 @@ int alloc_block(ernie_hip_ctx* ctx, BlockWeights& w, int dim, int ffn, int dtype
 
 // Rewrites the 16-bit projection matrices of a freshly written block K-tiled,
 // through the staging buffer, and records which ones were.
-struct TiledMat { DeviceBuffer* b; int rows, cols; };
+// head_rows: leading rows stored permuted within 128-row heads (tile_k32).
+struct TiledMat { DeviceBuffer* b; int rows, cols, head_rows; };
 
 int tile_matrices(ernie_hip_ctx* ctx, int dtype, const TiledMat (&mats)[4], bool (&k32)[4])
 {
@@ -348,7 +352,9 @@ int tile_matrices(ernie_hip_ctx* ctx, int dtype, const TiledMat (&mats)[4], bool
         if (m.rows % 256 || m.cols % 32 || bytes >= (1ull << 31)) continue;
         rc = hip_status(ctx, hipMemcpyAsync(ctx->staging.ptr, m.b->ptr, bytes, hipMemcpyDeviceToDevice, ctx->stream),
                         "tile weights");
-        if (!rc) rc = kernel_status(ctx, tile_k32(ctx->staging.ptr, m.b->ptr, m.rows, m.cols, ctx->stream), "tile weights");
+        if (!rc)
+            rc = kernel_status(ctx, tile_k32(ctx->staging.ptr, m.b->ptr, m.rows, m.cols, ctx->stream, m.head_rows),
+                               "tile weights");
         if (!rc) k32[i] = true;
     }
     if (!rc) rc = hip_status(ctx, hipStreamSynchronize(ctx->stream), "tile weights");
@@ -358,14 +364,16 @@ int tile_matrices(ernie_hip_ctx* ctx, int dtype, const TiledMat (&mats)[4], bool
 int tile_block_weights(ernie_hip_ctx* ctx, BlockWeights& w)
 {
     const int D = w.dim, F = w.ffn;
-    const TiledMat mats[4] = {{&w.wqkv, 3 * D, D}, {&w.wo, D, D}, {&w.w_ug, 2 * F, D}, {&w.w_down, D, F}};
-    return tile_matrices(ctx, w.dtype, mats, w.k32);
+    const TiledMat mats[4] = {{&w.wqkv, 3 * D, D, 2 * D}, {&w.wo, D, D, 0}, {&w.w_ug, 2 * F, D, 0}, {&w.w_down, D, F, 0}};
+    const int rc = tile_matrices(ctx, w.dtype, mats, w.k32);
+    w.qk_fused = !rc && w.k32[0];
+    return rc;
 }
 
 int tile_text_weights(ernie_hip_ctx* ctx, TextBlockWeights& w)
 {
     const int H = w.hidden, F = w.ffn, QD = w.heads * 128, QKV = (w.heads + 2 * w.kv_heads) * 128;
-    const TiledMat mats[4] = {{&w.wqkv, QKV, H}, {&w.wo, H, QD}, {&w.w_ug, 2 * F, H}, {&w.w_down, H, F}};
+    const TiledMat mats[4] = {{&w.wqkv, QKV, H, 0}, {&w.wo, H, QD, 0}, {&w.w_ug, 2 * F, H, 0}, {&w.w_down, H, F, 0}};
     return tile_matrices(ctx, w.dtype, mats, w.k32);
 }
 
@@ -459,13 +467,20 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
                                                  S, D, 1e-6f, ws.h, dt, s, ws.rows), "rmsnorm_modulate");
         if (rc) return rc;
     }
-    // gemm_0/1/2 as one [3D][D] projection
+    // gemm_0/1/2 as one [3D][D] projection; with permuted Q/K weight rows, rmsn_9 /
+    // rmsn_10 and the rotary BinaryOps run in its epilogue.
     {
         GemmArgs g;
         g.A = ws.h; g.lda = D; g.W = w.wqkv.ptr; g.ldw = D; g.M = S; g.N = 3 * D; g.K = D; g.dtype = dt;
         g.w_k32 = w.k32[0];
         g.a_k32_rows = ws.rows;
         g.epilogue = EPI_STORE; g.C = ws.qkv; g.ldc = 3 * D; g.c_dtype = dt;
+        if (w.qk_fused) {
+            g.epilogue = EPI_QKROPE;
+            g.qk_cols = 2 * D; g.k_col = D;
+            g.gq = static_cast<const float*>(w.norm_q.ptr); g.gk = static_cast<const float*>(w.norm_k.ptr);
+            g.cos_t = cos_t; g.sin_t = sin_t; g.qk_eps = 1e-6f;
+        }
         rc = split_workspace(ctx, S, H, &g.split_ws, &g.split_ws_bytes);
         if (rc) return rc;
         Timed t(ctx, P_QKV, 2.0 * dS * 3 * D * D, gemm_bytes(dS, 3.0 * D, D, e, e));
@@ -473,7 +488,7 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
         if (rc) return rc;
     }
     // rmsn_9 / rmsn_10 + rotary, in place on the Q and K column blocks
-    {
+    if (!w.qk_fused) {
         Timed t(ctx, P_ROPE, 0, dS * 2 * D * e * 2 + dS * 128 * 8);
         rc = kernel_status(ctx, qk_norm_rope_qk(ws.qkv, dt, S, H, H, 3L * D, D, static_cast<const float*>(w.norm_q.ptr),
                                                 static_cast<const float*>(w.norm_k.ptr), cos_t, sin_t, s),

@@ -363,7 +363,8 @@ int gemm(const GemmArgs& a, hipStream_t s)
     if (a.epilogue == EPI_GATE_RESID && (!a.resid || !a.gate || a.c_dtype != DT_F32)) return -1;
     if (epi_glu(a.epilogue) && (a.N % 64 || a.ldc < a.N / 2)) return -1;
     if (!epi_glu(a.epilogue) && a.ldc < a.N) return -1;
-    if (a.epilogue < 0 || (a.epilogue > EPI_GEGLU && a.epilogue != EPI_SWIGLU)) return -1;
+    if (a.epilogue < 0 || (a.epilogue > EPI_GEGLU && a.epilogue != EPI_SWIGLU && a.epilogue != EPI_QKROPE)) return -1;
+    if (a.epilogue == EPI_QKROPE && a.dtype == DT_F32) return -1;  // the fused Q/K path is the 16-bit kernel's
     // Only the 16-bit kernel reads or writes K-tiled operands.
     if ((a.w_k32 || a.a_k32_rows || a.c_k32_rows) && a.dtype == DT_F32) return -1;
     GemmParams p{};

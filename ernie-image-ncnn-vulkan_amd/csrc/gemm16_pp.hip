@@ -79,6 +79,14 @@ struct Params {
     // columns move as one vector; else element by element.
     int vec;
     int items;  // work items (tiles and tile parts); workgroup b takes items b, b + grid, ...
+    // EPI_QKROPE (GemmArgs fields of the same names).
+    int qk_cols;
+    long k_col;
+    const float* gq;
+    const float* gk;
+    const float* cos_t;
+    const float* sin_t;
+    float qk_eps;
 };
 
 // Full tile f of the tile order -> (mt, nt): GM M tiles per N sweep, so the
@@ -281,12 +289,100 @@ __device__ __forceinline__ int item_parts(const Params& p, int mt, int li)
     return (p.split_all || mt == p.m_full) ? p.split : (li >= 0 ? p.late_split : 1);
 }
 
+// EPI_QKROPE epilogue of a Q or K tile (n0 < qk_cols). The wave pair (wm, wn) and
+// (wm, wn ^ 1) holds one head's 128 columns for the same rows, each lane four rows of 16
+// and, through the permuted W rows, head dimensions d_j = 32 (wn & 1) + 4 q16 + 16 j
+// (+0..3) in acc[][j] and their rotary partners d_j + 64 in acc[][j + 2]. Each row's sum
+// of squares is taken over the lane's 16 values, the four lanes of the row and, through
+// `red` in LDS, the partner wave; then each pair is normalised, rotated and stored in
+// natural column order. The FP32 accumulators are normalised directly: the only rounding
+// is that of the rotated result, where a separate pass would first read back the
+// projection rounded to the storage precision.
+template <typename OutT, int MSUB>
+__device__ __forceinline__ void qk_rope_epilogue(const Params& p, const f32x4 (&acc)[2 * MSUB][4], int n0, int row_w,
+                                                 int wave, int wn, int q16, int r16, float* red)
+{
+    typedef OutT out4 __attribute__((ext_vector_type(4)));
+    const int hf = wn & 1;
+    const int head_col = n0 + 128 * (wn >> 1);
+    const float* g = head_col >= p.k_col ? p.gk : p.gq;
+    float ss[2 * MSUB];
+#pragma unroll
+    for (int i = 0; i < 2 * MSUB; ++i) {
+        float t = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float a = acc[i][j][r];
+                t += a * a;
+            }
+        t += __shfl_xor(t, 16, 64);
+        t += __shfl_xor(t, 32, 64);
+        ss[i] = t;
+    }
+    // Gammas for the whole tile and the first row's cos / sin are requested before the
+    // partner exchange; each later row's are requested while the previous row is rotated.
+    const int d0 = 32 * hf + 4 * q16;
+    f32x4 ga[2], gb[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        ga[j] = *reinterpret_cast<const f32x4*>(g + d0 + 16 * j);
+        gb[j] = *reinterpret_cast<const f32x4*>(g + d0 + 16 * j + 64);
+    }
+    // cs[b][j]: cos lo, cos hi, sin lo, sin hi of buffer b's row (clamped into [0, M)).
+    f32x4 cs[2][2][4];
+    auto load_row = [&](int i, f32x4 (&dst)[2][4]) {
+        const size_t m = (size_t)min(row_w + 16 * i, p.M - 1) * 128;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int d = d0 + 16 * j;
+            dst[j][0] = *reinterpret_cast<const f32x4*>(p.cos_t + m + d);
+            dst[j][1] = *reinterpret_cast<const f32x4*>(p.cos_t + m + d + 64);
+            dst[j][2] = *reinterpret_cast<const f32x4*>(p.sin_t + m + d);
+            dst[j][3] = *reinterpret_cast<const f32x4*>(p.sin_t + m + d + 64);
+        }
+    };
+    load_row(0, cs[0]);
+    if (q16 == 0)
+#pragma unroll
+        for (int i = 0; i < 2 * MSUB; ++i) red[(wave * 2 * MSUB + i) * 16 + r16] = ss[i];
+    phase_barrier();
+#pragma unroll
+    for (int i = 0; i < 2 * MSUB; ++i) {
+        if (i + 1 < 2 * MSUB) load_row(i + 1, cs[(i + 1) & 1]);
+        const int m = row_w + 16 * i;
+        const float inv = 1.0f / sqrtf((ss[i] + red[((wave ^ 2) * 2 * MSUB + i) * 16 + r16]) / 128.f + p.qk_eps);
+        OutT* crow = static_cast<OutT*>(p.C) + (size_t)m * p.ldc + head_col;
+        const f32x4(&c)[2][4] = cs[i & 1];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int d = d0 + 16 * j;
+            out4 lo, hi;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float na = acc[i][j][r] * inv * ga[j][r];
+                const float nb = acc[i][j + 2][r] * inv * gb[j][r];
+                lo[r] = OutT(na * c[j][0][r] - nb * c[j][2][r]);
+                hi[r] = OutT(nb * c[j][1][r] + na * c[j][3][r]);
+            }
+            if (m < p.M) {
+                *reinterpret_cast<out4*>(crow + d) = lo;
+                *reinterpret_cast<out4*>(crow + d + 64) = hi;
+            }
+        }
+        // Two rows' loads in flight at most: hoisting every row's would raise the
+        // register peak.
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 // One work item. `pre`: its first NS stages were requested by the previous item of this
 // workgroup. nmt >= 0 names the next item (nmt, nnt, npart, nli), whose first NS stages
 // this one requests once its own ring is drained, before its epilogue.
 template <typename T, typename OutT, int EPI, int MSUB>
 __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, int li, uint8_t* smem, bool pre,
-                                     int nmt, int nnt, int npart, int nli)
+                                     int nmt, int nnt, int npart, int nli, float* red)
 {
     typedef typename Mfma<T>::vec vec8;
     const int m0 = mt * BM, n0 = nt * BN;
@@ -438,6 +534,13 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
         return;
     }
 
+    if constexpr (EPI == EPI_QKROPE) {
+        if (n0 < p.qk_cols) {
+            qk_rope_epilogue<OutT, MSUB>(p, acc, n0, row_w, wave, wn, q16, r16, red);
+            return;
+        }
+        // V columns: stored as they are, below.
+    }
     if constexpr (EPI == EPI_GATE_RESID) {
         // C = resid + gate * acc, C possibly aliasing resid. Each element is read and
         // written by this lane only, so the gate values and a 32-row block's residuals
@@ -538,6 +641,8 @@ template <typename T, typename OutT, int EPI>
 __global__ void __launch_bounds__(512, 1) kernel(Params p)
 {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
+    // Per-row partial sums of squares of the EPI_QKROPE epilogue: [wave][row group][16].
+    __shared__ float red[EPI == EPI_QKROPE ? 8 * 8 * 16 : 1];
     // Items blockIdx.x, + gridDim.x, ...: with gridDim.x a multiple of 8 every item of
     // a workgroup maps to the XCD its blockIdx.x runs on.
     int bid = blockIdx.x, mt, nt, part, li;
@@ -547,10 +652,10 @@ __global__ void __launch_bounds__(512, 1) kernel(Params p)
         const int nb = bid + (int)gridDim.x;
         int nmt = -1, nnt = 0, npart = 0, nli = -1;
         if (nb < p.items) tile_of(p, nb, nmt, nnt, npart, nli);
-        if (mt < p.m_full) tile<T, OutT, EPI, 4>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli);
-        else if (p.tail_sub == 1) tile<T, OutT, EPI, 1>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli);
-        else if (p.tail_sub == 2) tile<T, OutT, EPI, 2>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli);
-        else tile<T, OutT, EPI, 3>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli);
+        if (mt < p.m_full) tile<T, OutT, EPI, 4>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
+        else if (p.tail_sub == 1) tile<T, OutT, EPI, 1>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
+        else if (p.tail_sub == 2) tile<T, OutT, EPI, 2>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
+        else tile<T, OutT, EPI, 3>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
         if (nb >= p.items) break;
         bid = nb; mt = nmt; nt = nnt; part = npart; li = nli;
         pre = true;
@@ -573,10 +678,19 @@ static int cu_count()
     return cached[dev];
 }
 
+// Q / K heads must not straddle a 256-column tile.
+constexpr int BN_QK = 256;
+
 int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
 {
-    // No other kernel takes K-tiled operands: shapes this one rejects are errors then.
-    const int other = a.w_k32 || a.a_k32_rows || a.c_k32_rows ? -1 : 1;
+    // No other kernel takes K-tiled operands or fuses the Q/K epilogue: shapes this one
+    // rejects are errors then.
+    const bool qk = a.epilogue == EPI_QKROPE;
+    const int other = a.w_k32 || a.a_k32_rows || a.c_k32_rows || qk ? -1 : 1;
+    if (qk && (a.c_dtype != a.dtype || !a.w_k32 || a.qk_cols <= 0 || a.qk_cols % BN_QK || a.qk_cols > a.N ||
+               a.k_col <= 0 || a.k_col % 128 || a.k_col >= a.qk_cols || !a.gq || !a.gk || !a.cos_t || !a.sin_t ||
+               a.ldc % 4 || (uintptr_t)a.C % 8))
+        return -1;
     if (a.dtype == DT_F32 || a.K % pingpong::BK) return other;
     if (a.epilogue == EPI_STORE && a.c_dtype != DT_F32 && a.c_dtype != a.dtype) return -1;
     if (epi_glu(a.epilogue) && a.c_dtype != a.dtype) return -1;
@@ -608,6 +722,8 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
         if (a.epilogue == EPI_GATE_RESID) v = v && aligned(a.resid, 16) && aligned(a.gate, 16) && a.ld_resid % 4 == 0;
         p.vec = v;
     }
+    p.qk_cols = a.qk_cols; p.k_col = a.k_col; p.gq = a.gq; p.gk = a.gk; p.cos_t = a.cos_t; p.sin_t = a.sin_t;
+    p.qk_eps = a.qk_eps;
     p.w_bytes = (uint32_t)((long)a.N * a.ldw * 2);
     p.w_row_bytes = a.w_k32 ? pingpong::ROWB : (int)(a.ldw * 2);
     p.w_kstep = a.w_k32 ? a.N * pingpong::ROWB : pingpong::ROWB;
@@ -649,7 +765,9 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     p.late_part = nullptr;
     const int full = p.m_full * p.n_tiles;
     const int last_round = full % kSplitTargetItems;
-    if (!p.split_all && a.split_ws && full > kSplitTargetItems && last_round <= kSplitTargetItems / 2 && last_round > 0) {
+    // (Not for the fused Q/K epilogue, whose rows are finished per tile.)
+    if (!qk && !p.split_all && a.split_ws && full > kSplitTargetItems && last_round <= kSplitTargetItems / 2 &&
+        last_round > 0) {
         const size_t tail_bytes =
             p.tail_sub ? ((size_t)p.split * p.n_tiles * 64 * p.tail_sub * pingpong::BN * sizeof(float) + 255) / 256 * 256 : 0;
         const size_t per_part = (size_t)last_round * pingpong::BM * pingpong::BN * sizeof(float);
@@ -667,9 +785,15 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     // One workgroup per CU (the LDS ring allows no second), each walking its items.
     p.items = tiles;
     const dim3 grid(std::min(tiles, cu_count())), block(512);
+    // Fused Q/K epilogue: tiles whose every part is split (split_all) are stored as they
+    // are and the whole GEMM is normalised and rotated afterwards; otherwise the full
+    // tiles are finished in the epilogue and only a split tail row needs that pass.
+    const int epi = qk && p.split_all ? EPI_STORE : a.epilogue;
 #define EHIP_PINGPONG(T)                                                                                            \
     do {                                                                                                      \
-        if (a.epilogue == EPI_STORE) {                                                                        \
+        if (epi == EPI_QKROPE) {                                                                              \
+            hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_QKROPE>), grid, block, 0, s, p);                         \
+        } else if (epi == EPI_STORE) {                                                                        \
             if (a.c_dtype == DT_F32) hipLaunchKernelGGL((pingpong::kernel<T, float, EPI_STORE>), grid, block, 0, s, p); \
             else hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_STORE>), grid, block, 0, s, p);                     \
         } else if (a.epilogue == EPI_GATE_RESID) {                                                            \
@@ -689,7 +813,11 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
                            (long)p.late * pingpong::BM * (epi_glu(a.epilogue) ? pingpong::BN / 2 : pingpong::BN);
         const dim3 rgrid((unsigned)((items + 255) / 256)), rblock(256);
 #define EHIP_REDUCE(OUT, EPI) hipLaunchKernelGGL((pingpong::split_reduce_kernel<OUT, EPI>), rgrid, rblock, 0, s, p)
-        if (a.epilogue == EPI_STORE) {
+        if (qk) {
+            // Split rows are summed as they are (permuted Q / K columns) ...
+            if (a.dtype == DT_F16) EHIP_REDUCE(f16, EPI_STORE);
+            else EHIP_REDUCE(bf16, EPI_STORE);
+        } else if (a.epilogue == EPI_STORE) {
             if (a.c_dtype == DT_F32) EHIP_REDUCE(float, EPI_STORE);
             else if (a.dtype == DT_F16) EHIP_REDUCE(f16, EPI_STORE);
             else EHIP_REDUCE(bf16, EPI_STORE);
@@ -703,6 +831,15 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
             else EHIP_REDUCE(bf16, EPI_GEGLU);
         }
 #undef EHIP_REDUCE
+    }
+    if (qk && p.split > 1) {
+        // ... and then normalised, rotated and put in natural order: every row when all
+        // tiles were split, else the tail rows.
+        const int r0 = p.split_all ? 0 : p.m_full * pingpong::BM;
+        const int rc = qk_norm_rope_permuted(a.C, a.dtype, r0, a.M, (int)(a.k_col / 128),
+                                             (int)((a.qk_cols - a.k_col) / 128), a.ldc, a.k_col, a.gq, a.gk, a.cos_t,
+                                             a.sin_t, a.qk_eps, s);
+        if (rc) return rc;
     }
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : -int(e);

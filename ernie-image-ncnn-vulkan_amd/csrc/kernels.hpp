@@ -15,6 +15,12 @@ enum Epilogue : int {
     EPI_GATE_RESID = 1,  // C(f32) = resid(f32) + gate[n] * acc
     EPI_GEGLU = 2,       // W rows interleaved in 32-row [up | gate] pairs; C[m][n/2] = up * gelu(gate)
     EPI_SWIGLU = 4,      // as EPI_GEGLU with SiLU on the gate: C[m][n/2] = up * silu(gate) (the text MLP)
+    // C = acc in the output precision; the columns below qk_cols are 128-column Q / K heads
+    // whose W rows are stored permuted (tile_k32 head_rows): each head is RMS-normalised
+    // (gamma gq, or gk from column k_col on, eps qk_eps) and rotated with the cos / sin
+    // rows of its token, and written in natural order (rmsn_9 / rmsn_10 and the rotary
+    // BinaryOps of block.ncnn.param lines 28-57, fused). 16-bit operands only.
+    EPI_QKROPE = 5,
 };
 // Gated epilogues: W rows interleaved in 32-row [up | gate] pairs, N/2 outputs.
 constexpr bool epi_glu(int e) { return e == EPI_GEGLU || e == EPI_SWIGLU; }
@@ -49,6 +55,15 @@ struct GemmArgs {
     // share it; calls that run concurrently must not.
     void* split_ws = nullptr;
     size_t split_ws_bytes = 0;
+    // EPI_QKROPE: Q / K columns [0, qk_cols) (K heads from k_col), their gammas [128],
+    // cos / sin [M][128] FP32.
+    int qk_cols = 0;
+    long k_col = 0;
+    const float* gq = nullptr;
+    const float* gk = nullptr;
+    const float* cos_t = nullptr;
+    const float* sin_t = nullptr;
+    float qk_eps = 1e-6f;
 };
 int gemm(const GemmArgs& a, hipStream_t stream);
 // The ping-pong 16-bit kernel (gemm16_pp.hip); returns 1 without launching when
@@ -101,6 +116,12 @@ int qk_norm_rope(void* x, int dtype, int rows, int nheads, long row_stride, cons
 // gamma gk, at k_offset) of each row in one launch.
 int qk_norm_rope_qk(void* x, int dtype, int rows, int nq, int nk, long row_stride, long k_offset, const float* gq,
                     const float* gk, const float* cos_t, const float* sin_t, hipStream_t s);
+// The same in place on rows [r0, r1) whose Q / K head values are stored permuted
+// (qk_stored_column order, as a QKV GEMM over permuted weights writes them): each head
+// is normalised and rotated and written back in natural order.
+int qk_norm_rope_permuted(void* x, int dtype, int r0, int r1, int nq, int nk, long row_stride, long k_offset,
+                          const float* gq, const float* gk, const float* cos_t, const float* sin_t, float eps,
+                          hipStream_t s);
 int gelu_inplace(void* x, int dtype, size_t n, hipStream_t s);
 int residual_add(const void* a, int a_dtype, const void* b, int b_dtype, float* out, size_t n, hipStream_t s);
 int euler_step(const float* x, const float* v, float delta, size_t n, float* out, hipStream_t s);
@@ -121,8 +142,10 @@ int transpose_to_tokens(const float* latent, int ch, int hw, void* out, int dtyp
 int tokens_to_latent(const float* proj, int hw, int ch, float* pred, hipStream_t s);
 
 // Row-major [rows][cols] 16-bit matrix -> K-tiled [cols/32][rows][32] (the
-// layout GemmArgs::w_k32 reads); in and out must not overlap.
-int tile_k32(const void* in, void* out, int rows, int cols, hipStream_t s);
+// layout GemmArgs::w_k32 reads); in and out must not overlap. The first head_rows rows
+// (a multiple of 128: the Q and K projections) are stored permuted within each 128-row
+// head, row d at qk_stored_column(d) (common.hpp), the layout EPI_QKROPE reads.
+int tile_k32(const void* in, void* out, int rows, int cols, hipStream_t s, int head_rows = 0);
 
 // Up or gate matrix [rows][cols] (dtype in_dt) -> its rows of the interleaved W_ug (parity 0 = up).
 int interleave_up_gate(const void* in, int in_dt, void* out, int dt, int rows, int cols, int parity, hipStream_t s);

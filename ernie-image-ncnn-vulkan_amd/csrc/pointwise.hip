@@ -390,6 +390,38 @@ __global__ void __launch_bounds__(256) transpose_kernel(const E* __restrict__ in
     }
 }
 
+// One wave per (row, head) of rows [r0, r1): lane l takes head dimensions l and l + 64
+// from their permuted columns, and writes the normalised, rotated pair back to columns
+// l and l + 64. Every load of a head precedes its stores (the stores depend on the
+// wave-wide sum), so rewriting the head in place is safe.
+template <typename T>
+__global__ void __launch_bounds__(256) qk_rope_permuted_kernel(T* __restrict__ x, int r0, int r1, int nq, int nk,
+                                                               long row_stride, long k_offset,
+                                                               const float* __restrict__ gq,
+                                                               const float* __restrict__ gk,
+                                                               const float* __restrict__ cos_t,
+                                                               const float* __restrict__ sin_t, float eps)
+{
+    const int lane = threadIdx.x & 63;
+    const long w = (long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int heads = nq + nk;
+    if (w >= (long)(r1 - r0) * heads) return;
+    const int m = r0 + (int)(w / heads), h = (int)(w % heads);
+    const bool is_k = h >= nq;
+    T* v = x + (size_t)m * row_stride + (is_k ? k_offset + (long)(h - nq) * 128 : (long)h * 128);
+    const float* g = is_k ? gk : gq;
+    const int d0 = lane, d1 = lane + 64;
+    const float a = float(v[qk_stored_column(d0)]), b = float(v[qk_stored_column(d1)]);
+    const float ss = wave_sum(a * a + b * b);
+    const float inv = 1.0f / sqrtf(ss / 128.f + eps);
+    const float na = a * inv * g[d0], nb = b * inv * g[d1];
+    const float* c = cos_t + (size_t)m * 128;
+    const float* sn = sin_t + (size_t)m * 128;
+    const float lo = na * c[d0] - nb * sn[d0], hi = nb * c[d1] + na * sn[d1];
+    v[d0] = T(lo);
+    v[d1] = T(hi);
+}
+
 __global__ void fill_int_kernel(int* __restrict__ p, int value, size_t n)
 {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = value;
@@ -517,13 +549,15 @@ __global__ void interleave_kernel(const void* __restrict__ in, int idt, void* __
 
 // Row-major [rows][cols] -> K-tiled [cols/32][rows][32], 16 bytes (8 values) per
 // thread: chunk q = (r, c8) of the source lands at ((c8/4)*rows + r)*32 + (c8%4)*8.
-__global__ void tile_k32_kernel(const uint4* __restrict__ in, uint4* __restrict__ out, int rows, int cols)
+__global__ void tile_k32_kernel(const uint4* __restrict__ in, uint4* __restrict__ out, int rows, int cols,
+                                int head_rows)
 {
     const int c8n = cols / 8;
     const size_t n = (size_t)rows * c8n;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
         const int r = (int)(i / c8n), c8 = (int)(i % c8n);
-        out[((size_t)(c8 / 4) * rows + r) * 4 + (c8 % 4)] = in[i];
+        const int o = r < head_rows ? (r & ~127) + qk_stored_column(r & 127) : r;
+        out[((size_t)(c8 / 4) * rows + o) * 4 + (c8 % 4)] = in[i];
     }
 }
 
@@ -721,6 +755,25 @@ int transpose2d(const void* in, int dt, int rows, int cols, void* out, hipStream
     return launch_status();
 }
 
+int qk_norm_rope_permuted(void* x, int dt, int r0, int r1, int nq, int nk, long row_stride, long k_offset,
+                          const float* gq, const float* gk, const float* cos_t, const float* sin_t, float eps,
+                          hipStream_t s)
+{
+    if (!x || !gq || !gk || !cos_t || !sin_t || r0 < 0 || r1 < r0 || nq < 0 || nk < 0 || dt == DT_F32 ||
+        !valid_dt(dt))
+        return -1;
+    const long waves = (long)(r1 - r0) * (nq + nk);
+    if (!waves) return 0;
+    const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+    if (dt == DT_F16)
+        hipLaunchKernelGGL(qk_rope_permuted_kernel<f16>, grid, block, 0, s, static_cast<f16*>(x), r0, r1, nq, nk,
+                           row_stride, k_offset, gq, gk, cos_t, sin_t, eps);
+    else
+        hipLaunchKernelGGL(qk_rope_permuted_kernel<bf16>, grid, block, 0, s, static_cast<bf16*>(x), r0, r1, nq, nk,
+                           row_stride, k_offset, gq, gk, cos_t, sin_t, eps);
+    return launch_status();
+}
+
 int fill_int(int* p, int value, size_t n, hipStream_t s)
 {
     if (!p) return -1;
@@ -799,13 +852,14 @@ int interleave_up_gate(const void* in, int idt, void* out, int dt, int rows, int
     return launch_status();
 }
 
-int tile_k32(const void* in, void* out, int rows, int cols, hipStream_t s)
+int tile_k32(const void* in, void* out, int rows, int cols, hipStream_t s, int head_rows)
 {
+    if (head_rows < 0 || head_rows % 128 || head_rows > rows) return -1;
     if (!in || !out || rows < 1 || cols < 32 || cols % 32) return -1;
     if ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) return -1;
     const size_t n = (size_t)rows * (cols / 8);
     hipLaunchKernelGGL(tile_k32_kernel, dim3(grid_for(n)), dim3(256), 0, s, static_cast<const uint4*>(in),
-                       static_cast<uint4*>(out), rows, cols);
+                       static_cast<uint4*>(out), rows, cols, head_rows);
     return launch_status();
 }
 
