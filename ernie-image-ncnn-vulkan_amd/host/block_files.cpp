@@ -17,8 +17,8 @@
 #include <set>
 #include <stdexcept>
 
-#include "ernie/runtime.h"
 #include "ernie/sha256.h"
+#include "ernie_hip.h"
 
 namespace ernie {
 namespace {
@@ -162,61 +162,6 @@ std::string runtime_hash(const std::string& text, int tokens)
     }
     if (seen != rules.size()) return "";
     return sha256_hex(canon.data(), canon.size());
-}
-
-// Read-only mapping of a weight file.
-class Mapping {
-public:
-    explicit Mapping(const std::string& path)
-    {
-        const int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
-        if (fd < 0) throw std::runtime_error("cannot open weight file " + path + ": " + std::strerror(errno));
-        struct stat st;
-        if (::fstat(fd, &st) != 0 || !S_ISREG(st.st_mode)) {
-            ::close(fd);
-            throw std::runtime_error("weight file is not a regular file: " + path);
-        }
-        size_ = (size_t)st.st_size;
-        if (!size_) {
-            ::close(fd);
-            bad("empty weight file: " + path);
-        }
-        void* p = ::mmap(nullptr, size_, PROT_READ, MAP_PRIVATE, fd, 0);
-        ::close(fd);
-        if (p == MAP_FAILED) throw std::runtime_error("cannot map weight file " + path + ": " + std::strerror(errno));
-        (void)::madvise(p, size_, MADV_SEQUENTIAL);
-        data_ = static_cast<const unsigned char*>(p);
-    }
-    ~Mapping()
-    {
-        if (data_) ::munmap(const_cast<unsigned char*>(data_), size_);
-    }
-    Mapping(const Mapping&) = delete;
-    Mapping& operator=(const Mapping&) = delete;
-    const unsigned char* data() const { return data_; }
-    size_t size() const { return size_; }
-
-private:
-    const unsigned char* data_ = nullptr;
-    size_t size_ = 0;
-};
-
-BlockFile inspect_mapped(const std::string& param_path, const Mapping* bin, bool allow_unreviewed,
-                         const std::string& expected_bin_sha256)
-{
-    BlockFile f;
-    f.graph = inspect_block_graph(read_graph_text(param_path), allow_unreviewed);
-    if (!bin) {
-        if (!expected_bin_sha256.empty()) bad("a weight checksum was given without a weight file");
-        return f;
-    }
-    f.bin_bytes = bin->size();
-    if (!expected_bin_sha256.empty()) {
-        f.bin_sha256 = sha256_hex(bin->data(), bin->size());
-        if (f.bin_sha256 != lower(expected_bin_sha256)) bad("weight file checksum mismatch: " + f.bin_sha256);
-    }
-    f.sections = block_sections(f.graph, bin->data(), bin->size());
-    return f;
 }
 
 }  // namespace
@@ -407,30 +352,56 @@ std::string read_graph_text(const std::string& param_path)
     return text;
 }
 
+MappedFile::MappedFile(const std::string& path)
+{
+    const int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
+    if (fd < 0) throw std::runtime_error("cannot open weight file " + path + ": " + std::strerror(errno));
+    struct stat st;
+    if (::fstat(fd, &st) != 0 || !S_ISREG(st.st_mode)) {
+        ::close(fd);
+        throw std::runtime_error("weight file is not a regular file: " + path);
+    }
+    size_ = (size_t)st.st_size;
+    if (!size_) {
+        ::close(fd);
+        bad("empty weight file: " + path);
+    }
+    void* p = ::mmap(nullptr, size_, PROT_READ, MAP_PRIVATE, fd, 0);
+    ::close(fd);
+    if (p == MAP_FAILED) throw std::runtime_error("cannot map weight file " + path + ": " + std::strerror(errno));
+    (void)::madvise(p, size_, MADV_SEQUENTIAL);
+    data_ = static_cast<const unsigned char*>(p);
+}
+
+MappedFile::~MappedFile()
+{
+    if (data_) ::munmap(const_cast<unsigned char*>(data_), size_);
+}
+
+BlockFile inspect_block_bytes(const std::string& param_path, const unsigned char* bin, size_t size,
+                              bool allow_unreviewed, const std::string& expected_bin_sha256)
+{
+    BlockFile f;
+    f.graph = inspect_block_graph(read_graph_text(param_path), allow_unreviewed);
+    if (!bin) {
+        if (!expected_bin_sha256.empty()) bad("a weight checksum was given without a weight file");
+        return f;
+    }
+    f.bin_bytes = size;
+    if (!expected_bin_sha256.empty()) {
+        f.bin_sha256 = sha256_hex(bin, size);
+        if (f.bin_sha256 != lower(expected_bin_sha256)) bad("weight file checksum mismatch: " + f.bin_sha256);
+    }
+    f.sections = block_sections(f.graph, bin, size);
+    return f;
+}
+
 BlockFile inspect_block_files(const std::string& param_path, const std::string& bin_path, bool allow_unreviewed,
                               const std::string& expected_bin_sha256)
 {
-    if (bin_path.empty()) return inspect_mapped(param_path, nullptr, allow_unreviewed, expected_bin_sha256);
-    const Mapping bin(bin_path);
-    return inspect_mapped(param_path, &bin, allow_unreviewed, expected_bin_sha256);
-}
-
-BlockFile load_block_files(const Device& device, int index, const std::string& param_path,
-                           const std::string& bin_path, int storage_dtype, bool allow_unreviewed,
-                           const std::string& expected_bin_sha256)
-{
-    if (storage_dtype != ERNIE_DTYPE_FP32 && storage_dtype != ERNIE_DTYPE_FP16 && storage_dtype != ERNIE_DTYPE_BF16)
-        bad("invalid storage dtype");
-    if (bin_path.empty()) bad("a weight file is required to load a block");
-    const Mapping bin(bin_path);
-    BlockFile f = inspect_mapped(param_path, &bin, allow_unreviewed, expected_bin_sha256);
-    ernie_host_tensor t[11];
-    for (int i = 0; i < 11; ++i) t[i] = {bin.data() + f.sections[i].data, f.sections[i].dtype};
-    // Section order is the field order of ernie_block_host_tensors.
-    const ernie_block_host_tensors w = {t[0], t[1], t[2], t[3], t[4], t[5], t[6], t[7], t[8], t[9], t[10]};
-    check_status(ernie_hip_block_upload_tensors(device.ctx(), index, &w, f.graph.dim, f.graph.ffn, storage_dtype),
-                 device.ctx(), "block upload");
-    return f;
+    if (bin_path.empty()) return inspect_block_bytes(param_path, nullptr, 0, allow_unreviewed, expected_bin_sha256);
+    const MappedFile bin(bin_path);
+    return inspect_block_bytes(param_path, bin.data(), bin.size(), allow_unreviewed, expected_bin_sha256);
 }
 
 }  // namespace ernie

@@ -75,12 +75,31 @@ struct BlockFile {
     std::string bin_sha256;               // set when a checksum was requested
 };
 
+// Read-only memory mapping of a weight file (a regular, non-empty file).
+class MappedFile {
+public:
+    explicit MappedFile(const std::string& path);
+    ~MappedFile();
+    MappedFile(const MappedFile&) = delete;
+    MappedFile& operator=(const MappedFile&) = delete;
+    const unsigned char* data() const { return data_; }
+    size_t size() const { return size_; }
+
+private:
+    const unsigned char* data_ = nullptr;
+    size_t size_ = 0;
+};
+
 // Graph text of at most 1 MiB without NUL bytes (src/component_files.cpp:14-23).
 std::string read_graph_text(const std::string& param_path);
 
 // Reads and checks the files without a device; an empty bin_path checks the graph only.
 BlockFile inspect_block_files(const std::string& param_path, const std::string& bin_path, bool allow_unreviewed,
                               const std::string& expected_bin_sha256 = "");
+
+// inspect_block_files over weight bytes already in memory; a null `bin` checks the graph only.
+BlockFile inspect_block_bytes(const std::string& param_path, const unsigned char* bin, size_t size,
+                              bool allow_unreviewed, const std::string& expected_bin_sha256 = "");
 
 // inspect_block_files, then uploads the weights into resident block slot
 // `index` at `storage_dtype` (gammas stay FP32). The weight file is memory
