@@ -196,6 +196,9 @@ def facade():
             "ernie_flow_schedule_turbo": (c_int, [c_int, c_vp, c_vp, cp, c_size_t]),
             "ernie_rope_frequencies": (c_int, [c_vp]),
             "ernie_dit_constants": (c_int, [c_vp, c_int, c_int, c_int, c_int, c_vp, c_vp, c_vp, cp, c_size_t]),
+            "ernie_dit_constants_file": (c_int, [ctypes.c_char_p, c_int, c_int, c_int, c_int, c_vp, c_vp, c_vp, cp,
+                                                 c_size_t]),
+            "ernie_pad_text": (c_int, [c_vp, c_int, c_int, c_vp, cp, c_size_t]),
             "ernie_run_block_sequence": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_int,
                                                  c_int, c_vp, c_vp, cp, c_size_t]),
             "ernie_denoise": (c_int, [c_vp, c_vp, c_int, c_vp, c_int, c_int, c_vp, c_int, c_vp, c_vp, c_vp, c_int,
@@ -290,6 +293,35 @@ def dit_constants(freqs, w, h, valid, text):
     if rc < 0:
         _raise(rc, e.value)
     return cos, sin, mask, rc
+
+
+def dit_constants_file(path, w, h, valid, text):
+    """Facade dit_constants from the reference's 256-byte frequency file (token limit 6144)."""
+    import numpy as np
+    S = max(w * h + text, 1)
+    cos = np.empty((S, 128), np.float32)
+    sin = np.empty((S, 128), np.float32)
+    mask = np.empty(S, np.float32)
+    e = _err()
+    rc = facade().ernie_dit_constants_file(str(path).encode(), w, h, valid, text, cos.ctypes.data, sin.ctypes.data,
+                                           mask.ctypes.data, e, 512)
+    if rc < 0:
+        _raise(rc, e.value)
+    return cos, sin, mask, rc
+
+
+def pad_text(embeddings, bucket):
+    """Facade pad_text: [tokens][3072] FP32 embeddings zero-padded to [bucket][3072]."""
+    import numpy as np
+    emb = np.ascontiguousarray(embeddings, np.float32)
+    if emb.ndim != 2 or emb.shape[1] != 3072:
+        raise ValueError("embeddings must be [tokens][3072]")
+    out = np.empty((max(bucket, 1), 3072), np.float32)
+    e = _err()
+    rc = facade().ernie_pad_text(emb.ctypes.data, emb.shape[0], bucket, out.ctypes.data, e, 512)
+    if rc < 0:
+        _raise(rc, e.value)
+    return out
 
 
 def text_constants(freqs, bucket):

@@ -147,6 +147,31 @@ int ernie_dit_constants(const float* frequencies, int width, int height, int val
     });
 }
 
+int ernie_dit_constants_file(const char* frequency_path, int width, int height, int valid_text, int text_bucket,
+                             float* cos_out, float* sin_out, float* mask_out, char* err, size_t errlen)
+{
+    return guarded(err, errlen, [&] {
+        if (!frequency_path || !cos_out || !sin_out || !mask_out) throw std::invalid_argument("null argument");
+        const auto k = ernie::dit_constants(std::string(frequency_path), width, height, valid_text, text_bucket);
+        std::memcpy(cos_out, k.cos.data(), k.cos.size() * sizeof(float));
+        std::memcpy(sin_out, k.sin.data(), k.sin.size() * sizeof(float));
+        std::memcpy(mask_out, k.mask.data(), k.mask.size() * sizeof(float));
+        return k.valid_keys;
+    });
+}
+
+int ernie_pad_text(const float* embeddings, int tokens, int bucket, float* out, char* err, size_t errlen)
+{
+    return guarded(err, errlen, [&] {
+        if (!embeddings || !out) throw std::invalid_argument("null argument");
+        if (tokens < 1 || tokens > 2048) throw std::invalid_argument("Invalid text embeddings or padding bucket");
+        const std::vector<float> in(embeddings, embeddings + size_t(tokens) * 3072);
+        const auto padded = ernie::pad_text(in, tokens, bucket);
+        std::memcpy(out, padded.data(), padded.size() * sizeof(float));
+        return ERNIE_OK;
+    });
+}
+
 int ernie_run_block_sequence(ernie_device* device, const int* blocks, int count, const float* x, int S, int dim,
                              const float* const* mods, const float* cos_t, const float* sin_t, const float* mask,
                              int valid_prefix, int storage_dtype, float* out, double* compute_seconds, char* err,

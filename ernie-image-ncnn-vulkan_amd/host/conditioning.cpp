@@ -4,6 +4,8 @@
 
 #include <cmath>
 #include <cstring>
+#include <filesystem>
+#include <fstream>
 #include <stdexcept>
 
 namespace ernie {
@@ -47,6 +49,21 @@ DitConstantsHost dit_constants(const std::vector<float>& frequencies, int w, int
     }
     for (int k = 0; k < length; ++k) out.mask[k] = k >= image + valid ? -1e30f : 0.f;
     return out;
+}
+
+DitConstantsHost dit_constants(const std::string& frequency_path, int w, int h, int valid, int text)
+{
+    constexpr int kPathTokenLimit = 6144;  // src/conditioning.cpp:46-49
+    std::error_code ec;
+    const auto bytes = std::filesystem::file_size(std::filesystem::u8path(frequency_path), ec);
+    if (w < 1 || w > 256 || h < 1 || h > 256 || valid < 1 || text < valid || text > 2048 ||
+        w * h + text > kPathTokenLimit || ec || bytes != 64 * sizeof(float))
+        throw std::invalid_argument("Invalid DiT position dimensions or frequency file");
+    std::vector<float> frequencies(64);
+    std::ifstream file(std::filesystem::u8path(frequency_path), std::ios::binary);
+    if (!file.read(reinterpret_cast<char*>(frequencies.data()), 64 * sizeof(float)))
+        throw std::runtime_error("Cannot read DiT frequencies");
+    return dit_constants(frequencies, w, h, valid, text, kPathTokenLimit);
 }
 
 std::vector<DeviceMat> upload_constants(const Device& device, const DitConstantsHost& k)

@@ -2,6 +2,7 @@
 // Shared DiT constants: RoPE tables and the one-row attention mask
 // (src/conditioning.h; src/conditioning.cpp:10-67).
 #pragma once
+#include <string>
 #include <vector>
 
 #include "ernie/runtime.h"
@@ -20,6 +21,12 @@ std::vector<float> rope_frequencies();
 // Throws std::invalid_argument for invalid dimensions or frequencies.
 DitConstantsHost dit_constants(const std::vector<float>& frequencies, int width, int height, int valid_text,
                                int text_bucket, int token_limit = 10240);
+// src/conditioning.cpp:10-23,46-49: the same from the frequency file the reference
+// ships (exactly 64 FP32 values, 256 bytes), read and checked, with that overload's
+// token limit of 6144. Dimension or file-size errors throw std::invalid_argument; an
+// unreadable file or a non-finite / non-positive frequency std::runtime_error.
+DitConstantsHost dit_constants(const std::string& frequency_path, int width, int height, int valid_text,
+                               int text_bucket);
 // Uploads: cosine, sine, attention mask (mask carries valid_prefix).
 std::vector<DeviceMat> upload_constants(const Device& device, const DitConstantsHost& constants);
 // src/conditioning.cpp:56-67: zero-pad [tokens][3072] text embeddings to `bucket` rows.

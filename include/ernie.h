@@ -41,6 +41,14 @@ int ernie_rope_frequencies(float* out);
 int ernie_dit_constants(const float* frequencies, int width, int height, int valid_text, int text_bucket,
                         float* cos_out, float* sin_out, float* mask_out, char* err, size_t errlen);
 
+/* dit_constants(path, ...) (src/conditioning.cpp:10-23,46-49): the frequency file of
+ * exactly 64 FP32 values is read and checked, token limit 6144; outputs as above. */
+int ernie_dit_constants_file(const char* frequency_path, int width, int height, int valid_text, int text_bucket,
+                             float* cos_out, float* sin_out, float* mask_out, char* err, size_t errlen);
+/* pad_text (src/conditioning.cpp:56-67): [tokens][3072] host embeddings zero-padded
+ * to out [bucket][3072]; tokens <= bucket <= 2048. */
+int ernie_pad_text(const float* embeddings, int tokens, int bucket, float* out, char* err, size_t errlen);
+
 /* run_block_sequence (src/block_sequence.h:38-41): x [S][dim] device FP32,
  * mods = six [dim] device vectors, cos/sin [S][128], mask [S]. valid_prefix > 0
  * declares the mask canonical (0 below it, -1e30 from it, as dit_constants

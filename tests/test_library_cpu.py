@@ -71,3 +71,48 @@ def test_context_creation_fails_loudly_without_device():
         pytest.skip("a device is present")
     with pytest.raises(E.ErnieError):
         E.Context(0, use_torch_stream=False)
+
+
+def test_dit_constants_from_the_frequency_file(tmp_path):
+    # src/conditioning.cpp:10-23: the 256-byte file is size-checked and read; the
+    # path overload's token limit is 6144 (src/conditioning.cpp:46-49).
+    path = GOLDEN / "rope_inv_freq.f32"
+    freqs = np.fromfile(path, dtype="<f4")
+    for (w, h, valid, text) in ((64, 64, 40, 64), (3, 5, 1, 1), (48, 86, 1000, 1088)):
+        c1, s1, m1, vk = E.dit_constants_file(path, w, h, valid, text)
+        c2, s2, m2, vk2 = E.dit_constants(freqs, w, h, valid, text)
+        np.testing.assert_array_equal(c1, c2)
+        np.testing.assert_array_equal(s1, s2)
+        np.testing.assert_array_equal(m1, m2)
+        assert vk == vk2 == w * h + valid
+    with pytest.raises(E.ErnieInvalidRequest):
+        E.dit_constants_file(path, 48, 86, 1080, 2048)  # 6176 tokens > 6144 for this overload
+    short = tmp_path / "short.f32"
+    short.write_bytes(path.read_bytes()[:252])
+    with pytest.raises(E.ErnieInvalidRequest, match="frequency file"):
+        E.dit_constants_file(short, 8, 8, 4, 8)
+    with pytest.raises(E.ErnieInvalidRequest, match="frequency file"):
+        E.dit_constants_file(tmp_path / "missing.f32", 8, 8, 4, 8)
+    bad = tmp_path / "bad.f32"
+    neg = freqs.copy()
+    neg[17] = -1.0
+    neg.astype("<f4").tofile(bad)
+    with pytest.raises(E.ErnieError, match="Invalid DiT frequency"):
+        E.dit_constants_file(bad, 8, 8, 4, 8)
+    neg[17] = np.nan
+    neg.astype("<f4").tofile(bad)
+    with pytest.raises(E.ErnieError, match="Invalid DiT frequency"):
+        E.dit_constants_file(bad, 8, 8, 4, 8)
+
+
+def test_pad_text_zero_pads_to_the_bucket():
+    # src/conditioning.cpp:56-67: rows copied, the rest of the bucket zero.
+    emb = O.normal((40, 3072), 9)
+    out = E.pad_text(emb, 64)
+    assert out.shape == (64, 3072)
+    np.testing.assert_array_equal(out[:40], emb)
+    assert not out[40:].any()
+    np.testing.assert_array_equal(E.pad_text(emb, 40), emb)
+    for bucket in (39, 2049):
+        with pytest.raises(E.ErnieInvalidRequest, match="padding bucket"):
+            E.pad_text(emb, bucket)
