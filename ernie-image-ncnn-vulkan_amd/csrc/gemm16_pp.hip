@@ -119,22 +119,47 @@ __device__ __forceinline__ void reduce_store(const Params& p, int m, int c, int 
     }
 }
 
+// The epilogue of four reduced elements: row m, output columns c .. c + 3 (tile-grid
+// columns n .. n + 3), every row, residual and vector 16-byte aligned (Params::vec).
+template <typename OutT, int EPI>
+__device__ __forceinline__ void reduce_store4(const Params& p, int m, int c, int n, f32x4 v, f32x4 g)
+{
+    typedef OutT out4 __attribute__((ext_vector_type(4)));
+    if (epi_glu(EPI)) {
+        out4 o;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = OutT(v[r] * glu_act<EPI == EPI_SWIGLU>(g[r]));
+        *reinterpret_cast<out4*>(static_cast<OutT*>(p.C) + (size_t)m * p.c_rs + (size_t)(c >> 5) * p.c_ss + (c & 31)) = o;
+    } else if (EPI == EPI_STORE) {
+        if (p.bias) v += *reinterpret_cast<const f32x4*>(p.bias + n);
+        *reinterpret_cast<out4*>(static_cast<OutT*>(p.C) + (size_t)m * p.ldc + n) =
+            out4{OutT(v[0]), OutT(v[1]), OutT(v[2]), OutT(v[3])};
+    } else {
+        const f32x4 rv = *reinterpret_cast<const f32x4*>(p.resid + (size_t)m * p.ld_resid + n);
+        const f32x4 gv = *reinterpret_cast<const f32x4*>(p.gate + n);
+        f32x4 o;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = rv[r] + gv[r] * v[r];
+        *reinterpret_cast<f32x4*>(static_cast<float*>(p.C) + (size_t)m * p.ldc + n) = o;
+    }
+}
+
 // Sum of `parts` partials `stride` floats apart, in part order, every load issued
 // before the first add (at most kMaxSplit parts), so the sum does not wait out one
-// load latency per part.
-template <int EPI>
-__device__ __forceinline__ void sum_parts(const float* base, size_t stride, int parts, float& v, float& g)
+// load latency per part. V = 4: four consecutive columns per thread, 16-byte loads.
+template <int EPI, int V, typename Vec>
+__device__ __forceinline__ void sum_parts(const float* base, size_t stride, int parts, Vec& v, Vec& g)
 {
-    float pv[kMaxSplit], pg[kMaxSplit];
+    Vec pv[kMaxSplit], pg[kMaxSplit];
 #pragma unroll
     for (int q = 0; q < kMaxSplit; ++q) {
         if (q < parts) {
-            pv[q] = base[(size_t)q * stride];
-            if (epi_glu(EPI)) pg[q] = base[(size_t)q * stride + 32];
+            pv[q] = *reinterpret_cast<const Vec*>(base + (size_t)q * stride);
+            if (epi_glu(EPI)) pg[q] = *reinterpret_cast<const Vec*>(base + (size_t)q * stride + 32);
         }
     }
-    v = 0.f;
-    g = 0.f;
+    v = Vec(0.f);
+    g = Vec(0.f);
 #pragma unroll
     for (int q = 0; q < kMaxSplit; ++q) {
         if (q < parts) {
@@ -145,34 +170,40 @@ __device__ __forceinline__ void sum_parts(const float* base, size_t stride, int 
 }
 
 // Sums the K parts of the split tiles and applies the epilogue: one thread per
-// output column (GEGLU: per up/gate column pair) and row, first over the tail row
-// (or every row when split_all), then over the late-split tiles.
-template <typename OutT, int EPI>
+// V consecutive output columns (GEGLU: up/gate column pairs) of a row, first over the
+// tail row (or every row when split_all), then over the late-split tiles. V = 4 needs
+// Params::vec; each element is summed in the same part order either way.
+template <typename OutT, int EPI, int V>
 __global__ void __launch_bounds__(256) split_reduce_kernel(Params p)
 {
+    typedef typename std::conditional<V == 4, f32x4, float>::type Vec;
     const int rows = p.split <= 1 ? 0 : (p.split_all ? p.M : 64 * p.tail_sub);
-    const int cols = epi_glu(EPI) ? p.N / 2 : p.N;
+    const int cols = (epi_glu(EPI) ? p.N / 2 : p.N) / V;
     const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    auto store = [&](int m, int c, int n, const Vec& v, const Vec& g) {
+        if constexpr (V == 4) reduce_store4<OutT, EPI>(p, m, c, n, v, g);
+        else reduce_store<OutT, EPI>(p, m, c, n, v, g);
+    };
     if (idx >= (long)rows * cols) {
         // Late-split tile li: BM rows x BN grid columns (BN / 2 output columns for GLU).
-        const int cols_t = epi_glu(EPI) ? BN / 2 : BN;
+        const int cols_t = (epi_glu(EPI) ? BN / 2 : BN) / V;
         const long j = idx - (long)rows * cols;
         if (j >= (long)p.late * BM * cols_t) return;
         const int li = (int)(j / (BM * cols_t));
         const int rem = (int)(j - (long)li * BM * cols_t);
-        const int rl = rem / cols_t, cc = rem - rl * cols_t;
+        const int rl = rem / cols_t, cc = (rem - rl * cols_t) * V;
         int mt, nt;
         full_order(p, p.m_full * p.n_tiles - p.late + li, mt, nt);
         const int m = mt * BM + rl;
         const int c = (epi_glu(EPI) ? nt * (BN / 2) : nt * BN) + cc;
         const int n = epi_glu(EPI) ? (c / 32) * 64 + (c % 32) : c;
-        float v, g;
-        sum_parts<EPI>(p.late_part + ((size_t)li * p.late_split * BM + rl) * BN + (n - nt * BN), (size_t)BM * BN,
-                       p.late_split, v, g);
-        reduce_store<OutT, EPI>(p, m, c, n, v, g);
+        Vec v, g;
+        sum_parts<EPI, V>(p.late_part + ((size_t)li * p.late_split * BM + rl) * BN + (n - nt * BN), (size_t)BM * BN,
+                          p.late_split, v, g);
+        store(m, c, n, v, g);
         return;
     }
-    const int rl = (int)(idx / cols), c = (int)(idx - (long)rl * cols);
+    const int rl = (int)(idx / cols), c = (int)(idx - (long)rl * cols) * V;
     const int m = p.split_all ? rl : p.m_full * BM + rl;
     if (m >= p.M) return;
     // Column n of the tile grid; GEGLU output column c holds up column (c / 32) * 64 + c % 32
@@ -183,9 +214,9 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(Params p)
     const float* base = p.split_all
                             ? p.part + ((size_t)((m / BM) * p.n_tiles + nt) * p.split * BM + m % BM) * BN + cl
                             : p.part + (size_t)nt * p.split * rows * BN + (size_t)rl * BN + cl;
-    float v, g;
-    sum_parts<EPI>(base, (size_t)slot_rows * BN, p.split, v, g);
-    reduce_store<OutT, EPI>(p, m, c, n, v, g);
+    Vec v, g;
+    sum_parts<EPI, V>(base, (size_t)slot_rows * BN, p.split, v, g);
+    store(m, c, n, v, g);
 }
 
 template <typename T> struct Mfma;
@@ -809,10 +840,17 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
 #undef EHIP_PINGPONG
     if (p.split > 1 || p.late) {
         const long cols = epi_glu(a.epilogue) ? a.N / 2 : a.N;
-        const long items = (p.split > 1 ? (long)(p.split_all ? a.M : 64 * p.tail_sub) * cols : 0) +
-                           (long)p.late * pingpong::BM * (epi_glu(a.epilogue) ? pingpong::BN / 2 : pingpong::BN);
+        // Four columns per thread when every row and vector is 16-byte aligned.
+        const int V = p.vec && cols % 4 == 0 ? 4 : 1;
+        const long items = ((p.split > 1 ? (long)(p.split_all ? a.M : 64 * p.tail_sub) * cols : 0) +
+                            (long)p.late * pingpong::BM * (epi_glu(a.epilogue) ? pingpong::BN / 2 : pingpong::BN)) /
+                           V;
         const dim3 rgrid((unsigned)((items + 255) / 256)), rblock(256);
-#define EHIP_REDUCE(OUT, EPI) hipLaunchKernelGGL((pingpong::split_reduce_kernel<OUT, EPI>), rgrid, rblock, 0, s, p)
+#define EHIP_REDUCE(OUT, EPI)                                                                                   \
+    do {                                                                                                        \
+        if (V == 4) hipLaunchKernelGGL((pingpong::split_reduce_kernel<OUT, EPI, 4>), rgrid, rblock, 0, s, p);   \
+        else hipLaunchKernelGGL((pingpong::split_reduce_kernel<OUT, EPI, 1>), rgrid, rblock, 0, s, p);          \
+    } while (0)
         if (qk) {
             // Split rows are summed as they are (permuted Q / K columns) ...
             if (a.dtype == DT_F16) EHIP_REDUCE(f16, EPI_STORE);

@@ -76,44 +76,48 @@ struct Params {
 };
 
 // Merges the key-range parts of the split query tile: O = sum_p O_p 2^(m_p - M) /
-// sum_p l_p 2^(m_p - M) with M = max_p m_p (log2 domain). One thread per (head,
-// query, value).
+// sum_p l_p 2^(m_p - M) with M = max_p m_p (log2 domain). One wave per (head, query):
+// the query's (m, l) of every part are wave-uniform loads, and lane l merges values
+// 2l and 2l + 1 with one 8-byte load per part.
 template <typename T>
 __global__ void __launch_bounds__(256) combine_kernel(Params p, int tail_q)
 {
-    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (long)p.heads * tail_q * D) return;
-    const int d = (int)(idx % D);
-    const int ql = (int)((idx / D) % tail_q);
-    const int h = (int)(idx / ((long)D * tail_q));
+    const int wq = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
+    if (wq >= p.heads * tail_q) return;
+    const int lane = threadIdx.x & 63;
+    const int h = wq / tail_q, ql = wq - h * tail_q;
     const float* ml = p.part_ml + ((size_t)h * p.tail_parts * BQ + ql) * 2;
-    const float* po = p.part_o + ((size_t)h * p.tail_parts * BQ + ql) * D + d;
+    const float* po = p.part_o + ((size_t)h * p.tail_parts * BQ + ql) * D + 2 * lane;
     // Every part's loads are issued before the first use (at most kMaxParts parts);
     // the merge then runs in part order.
-    float mv[kMaxParts], lv[kMaxParts], ov[kMaxParts];
+    float mv[kMaxParts], lv[kMaxParts];
+    f32x2 ov[kMaxParts];
 #pragma unroll
     for (int q = 0; q < kMaxParts; ++q) {
         if (q < p.tail_parts) {
             mv[q] = ml[(size_t)q * BQ * 2];
             lv[q] = ml[(size_t)q * BQ * 2 + 1];
-            ov[q] = po[(size_t)q * BQ * D];
+            ov[q] = *reinterpret_cast<const f32x2*>(po + (size_t)q * BQ * D);
         }
     }
     float M = -INFINITY;
 #pragma unroll
     for (int q = 0; q < kMaxParts; ++q)
         if (q < p.tail_parts) M = fmaxf(M, mv[q]);
-    float L = 0.f, O = 0.f;
+    float L = 0.f, O0 = 0.f, O1 = 0.f;
 #pragma unroll
     for (int q = 0; q < kMaxParts; ++q) {
         if (q < p.tail_parts) {
             const float w = mv[q] == -INFINITY ? 0.f : exp2f(mv[q] - M);
             L += lv[q] * w;
-            O += ov[q] * w;
+            O0 += ov[q][0] * w;
+            O1 += ov[q][1] * w;
         }
     }
-    const int qi = p.full_qt * BQ + ql;
-    static_cast<T*>(p.o)[(size_t)h * p.o_hs + (size_t)qi * p.o_rs + (size_t)(d >> 5) * p.o_ds + (d & 31)] = T(O / L);
+    const int qi = p.full_qt * BQ + ql, d = 2 * lane;
+    typedef T t2 __attribute__((ext_vector_type(2)));
+    *reinterpret_cast<t2*>(static_cast<T*>(p.o) + (size_t)h * p.o_hs + (size_t)qi * p.o_rs + (size_t)(d >> 5) * p.o_ds +
+                           (d & 31)) = t2{T(O0 / L), T(O1 / L)};
 }
 
 template <typename T> struct Mfma;
@@ -634,8 +638,8 @@ int sdpa16_d128(const SdpaArgs& a, hipStream_t s)
         else hipLaunchKernelGGL((sdl::kernel<bf16, sdl::MASK_NONE>), grid, block, 0, s, p);
     }
     if (p.tail_parts) {
-        const long n = (long)a.heads * tail_q * sdl::D;
-        const dim3 cgrid((unsigned)((n + 255) / 256));
+        const long n = (long)a.heads * tail_q;  // one wave per (head, query), four per workgroup
+        const dim3 cgrid((unsigned)((n + 3) / 4));
         if (a.dtype == DT_F16) hipLaunchKernelGGL((sdl::combine_kernel<f16>), cgrid, block, 0, s, p, tail_q);
         else hipLaunchKernelGGL((sdl::combine_kernel<bf16>), cgrid, block, 0, s, p, tail_q);
     }
