@@ -44,8 +44,13 @@ namespace pingpong {
 
 constexpr int BM = 256, BN = 256, BK = 32, NS = 4;
 constexpr int ROWB = BK * 2;                // 64 bytes per staged row
-constexpr int A_BYTES = BM * ROWB;          // 16 KiB
-constexpr int STAGE = A_BYTES + BN * ROWB;  // 32 KiB
+// Stage layout: the A rows of the stage, then the W rows. A launch with heavy tiles
+// (HV, see Params::heavy) keeps room for 320 A rows in every stage.
+template <bool HV> struct Ring {
+    static constexpr int A_ROWS = HV ? BM + 64 : BM;
+    static constexpr int A_REGION = A_ROWS * ROWB;      // 16 or 20 KiB
+    static constexpr int STAGE = A_REGION + BN * ROWB;  // 32 or 36 KiB
+};
 constexpr uint32_t kRsrcFlags = 0x00020000;
 
 struct Params {
@@ -53,6 +58,11 @@ struct Params {
     const void* W; long ldw;
     int M, N, K;
     int m_full, tail_sub, n_tiles;
+    // heavy: the tail rows (M % 256 <= 64) are computed by the last row of full tiles,
+    // as 320-row tiles, instead of as split tail items: no tail phase that streams all
+    // of W for 64 rows, and no reduction launch. m_main: the M tiles walked by the
+    // full-tile order (m_full, or m_full - 1 when the last row is heavy).
+    int heavy, m_main;
     void* C; long ldc;
     const float* bias;
     const float* resid; long ld_resid;
@@ -97,7 +107,7 @@ __device__ __forceinline__ void full_order(const Params& p, int f, int& mt, int&
     const int group_size = GM * p.n_tiles;
     const int group = f / group_size;
     const int first_m = group * GM;
-    const int gm = min(p.m_full - first_m, GM);
+    const int gm = min(p.m_main - first_m, GM);
     const int in_group = f - group * group_size;
     mt = first_m + in_group % gm;
     nt = in_group / gm;
@@ -193,7 +203,7 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(Params p)
         const int rem = (int)(j - (long)li * BM * cols_t);
         const int rl = rem / cols_t, cc = (rem - rl * cols_t) * V;
         int mt, nt;
-        full_order(p, p.m_full * p.n_tiles - p.late + li, mt, nt);
+        full_order(p, p.m_main * p.n_tiles - p.late + li, mt, nt);
         const int m = mt * BM + rl;
         const int c = (epi_glu(EPI) ? nt * (BN / 2) : nt * BN) + cc;
         const int n = epi_glu(EPI) ? (c / 32) * 64 + (c % 32) : c;
@@ -249,7 +259,8 @@ __device__ __forceinline__ int fsw(int r) { return (r >> 1) & 3; }
 // the full-height tiles (walked 4 M tiles per N sweep), then of the late-split
 // items (the last `late` full tiles, each in `late_split` K parts) and then of the
 // tail-row items (a tail tile split into `split` K parts), so the short items run
-// last and spread over all XCDs. li = index of a late-split tile, else -1.
+// last and spread over all XCDs; or, with heavy tiles, of the last row of full
+// tiles, one per workgroup in the last round. li = index of a late-split tile, else -1.
 __device__ __forceinline__ void tile_of(const Params& p, int bid, int& mt, int& nt, int& part, int& li)
 {
     li = -1;
@@ -265,9 +276,9 @@ __device__ __forceinline__ void tile_of(const Params& p, int bid, int& mt, int& 
         mt = t - nt * m_tiles;
         return;
     }
-    const int main_full = p.m_full * p.n_tiles - p.late;
+    const int main_full = p.m_main * p.n_tiles - p.late;
     const int late_items = p.late * p.late_split;
-    const int tail_items = p.tail_sub ? p.n_tiles * p.split : 0;
+    const int tail_items = p.heavy ? p.n_tiles : p.tail_sub ? p.n_tiles * p.split : 0;
     part = 0;
     int region, u;
     if ((main_full & 7) == 0 && (late_items & 7) == 0 && (tail_items & 7) == 0) {
@@ -287,6 +298,9 @@ __device__ __forceinline__ void tile_of(const Params& p, int bid, int& mt, int& 
         li = u / p.late_split;
         part = u - li * p.late_split;
         full_order(p, main_full + li, mt, nt);
+    } else if (p.heavy) {
+        mt = p.m_full - 1;
+        nt = u;
     } else {
         mt = p.m_full;
         nt = u / p.split;
@@ -312,6 +326,16 @@ __device__ __forceinline__ void wait_vm(int n)
 {
     if (n >= 8) __builtin_amdgcn_s_waitcnt(8 | (7 << 4) | (15 << 8));
     else if (n >= 4) __builtin_amdgcn_s_waitcnt(4 | (7 << 4) | (15 << 8));
+    else __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
+}
+
+// Wait until at most `stages` stages of LPS loads each are outstanding (more than two
+// are waited down to two).
+template <int LPS>
+__device__ __forceinline__ void wait_stages(int stages)
+{
+    if (stages >= 2) __builtin_amdgcn_s_waitcnt((2 * LPS) | (7 << 4) | (15 << 8));
+    else if (stages == 1) __builtin_amdgcn_s_waitcnt(LPS | (7 << 4) | (15 << 8));
     else __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
 }
 
@@ -411,11 +435,14 @@ __device__ __forceinline__ void qk_rope_epilogue(const Params& p, const f32x4 (&
 // One work item. `pre`: its first NS stages were requested by the previous item of this
 // workgroup. nmt >= 0 names the next item (nmt, nnt, npart, nli), whose first NS stages
 // this one requests once its own ring is drained, before its epilogue.
-template <typename T, typename OutT, int EPI, int MSUB>
+template <typename T, typename OutT, int EPI, int MSUB, bool HV>
 __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, int li, uint8_t* smem, bool pre,
                                      int nmt, int nnt, int npart, int nli, float* red)
 {
     typedef typename Mfma<T>::vec vec8;
+    typedef Ring<HV> R;
+    // A heavy tile (MSUB 5: 320 rows) loads one more A instruction per stage and wave.
+    constexpr int LPS = MSUB == 5 ? 5 : 4;
     const int m0 = mt * BM, n0 = nt * BN;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -427,8 +454,9 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
 
     // Direct loads: wave w fills rows [32w, 32w+32) of the A and W halves of a stage
     // with two 1-KiB instructions each; lane l lands at bytes [16l, 16l+16), i.e.
-    // row (l >> 2), physical chunk l & 3 = logical chunk (l & 3) ^ fsw(row).
-    uint32_t a_src[2], w_src[2];
+    // row (l >> 2), physical chunk l & 3 = logical chunk (l & 3) ^ fsw(row). A heavy
+    // tile's A rows 256 + 8w .. + 7 come from a third instruction of lanes 0-31.
+    uint32_t a_src[3], w_src[2];
     auto sources = [&](int m_0, int n_0, uint32_t* as, uint32_t* ws) {
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
@@ -436,6 +464,10 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
             const int c = (lane & 3) ^ fsw(row);
             as[q] = (uint32_t)((long)(m_0 + row) * p.a_row_bytes + c * 16);
             ws[q] = (uint32_t)((long)(n_0 + row) * p.w_row_bytes + c * 16);
+        }
+        if constexpr (HV) {
+            const int row = BM + wave * 8 + (lane >> 2);
+            as[2] = (uint32_t)((long)(m_0 + row) * p.a_row_bytes + (((lane & 3) ^ fsw(row)) << 4));
         }
     };
     sources(m0, n0, a_src, w_src);
@@ -445,18 +477,23 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
     const int kt0 = (int)((long)nk_all * part / parts);
     const int nk = (int)((long)nk_all * (part + 1) / parts) - kt0;
     // Stage kt (of the item starting at K step k0) into ring slot kt % NS.
-    auto issue_at = [&](const uint32_t* as, const uint32_t* ws, int k0, int kt) {
-        uint8_t* st = smem + (kt & (NS - 1)) * STAGE;
+    auto issue_at = [&](const uint32_t* as, const uint32_t* ws, int k0, int kt, bool heavy_item) {
+        uint8_t* st = smem + (kt & (NS - 1)) * R::STAGE;
         const int koff = (k0 + kt) * p.a_kstep, koff_w = (k0 + kt) * p.w_kstep;
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(st + (wave * 32 + q * 16) * ROWB), 16, as[q],
                                                      koff, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(st + A_BYTES + (wave * 32 + q * 16) * ROWB), 16,
-                                                     ws[q], koff_w, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(st + R::A_REGION + (wave * 32 + q * 16) * ROWB),
+                                                     16, ws[q], koff_w, 0, 0);
+        }
+        if constexpr (HV) {
+            if (heavy_item && lane < 32)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(st + (BM + wave * 8) * ROWB), 16, as[2], koff,
+                                                         0, 0);
         }
     };
-    auto issue = [&](int kt) { issue_at(a_src, w_src, kt0, kt); };
+    auto issue = [&](int kt) { issue_at(a_src, w_src, kt0, kt, MSUB == 5); };
 
     // Fragment of 16 rows x 32 k: lane l reads row l % 16, logical chunk l / 16.
     const int r16 = lane & 15, q16 = lane >> 4;
@@ -475,10 +512,10 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
     vec8 af[2 * MSUB], bf[4];
     // Memory cluster: this wave's fragments of stage kt into registers.
     auto read_frags = [&](int kt) {
-        const uint8_t* st = smem + (kt & (NS - 1)) * STAGE;
+        const uint8_t* st = smem + (kt & (NS - 1)) * R::STAGE;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            bf[j] = *reinterpret_cast<const vec8*>(st + A_BYTES + (wn * 64 + j * 16) * ROWB + frag);
+            bf[j] = *reinterpret_cast<const vec8*>(st + R::A_REGION + (wn * 64 + j * 16) * ROWB + frag);
 #pragma unroll
         for (int i = 0; i < 2 * MSUB; ++i)
             af[i] = *reinterpret_cast<const vec8*>(st + (wm * 32 * MSUB + i * 16) * ROWB + frag);
@@ -490,8 +527,8 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
 #pragma unroll
             for (int j = 0; j < 4; ++j) acc[i][j] = Mfma<T>::run(bf[j], af[i], acc[i][j]);
     };
-    // Loads requested after stage s, per wave, when s must have landed: 4 x min(NS-2, nk-1-s).
-    auto wait_stage = [&](int s) { wait_vm(4 * min(NS - 2, nk - 1 - s)); };
+    // Loads requested after stage s, per wave, when s must have landed: LPS x min(NS-2, nk-1-s).
+    auto wait_stage = [&](int s) { wait_stages<LPS>(min(NS - 2, nk - 1 - s)); };
 
     // Prologue: request stages 0..NS-1 (unless the previous item did), wait for stage 0
     // everywhere. After a previous item, its epilogue's stores are counted too: wait
@@ -500,7 +537,7 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
 #pragma unroll
         for (int s = 0; s < NS; ++s)
             if (s < nk) issue(s);
-        wait_vm(4 * min(NS - 1, nk - 1));
+        wait_stages<LPS>(min(NS - 1, nk - 1));
     } else {
         wait_vm(0);
     }
@@ -541,11 +578,12 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
         const int nparts = item_parts(p, nmt, nli);
         const int nkt0 = (int)((long)nk_all * npart / nparts);
         const int nnk = (int)((long)nk_all * (npart + 1) / nparts) - nkt0;
-        uint32_t na[2], nw[2];
+        uint32_t na[3], nw[2];
         sources(nmt * BM, nnt * BN, na, nw);
+        const bool nheavy = HV && p.heavy && nmt == p.m_full - 1;
 #pragma unroll
         for (int s = 0; s < NS; ++s)
-            if (s < nnk) issue_at(na, nw, nkt0, s);
+            if (s < nnk) issue_at(na, nw, nkt0, s, nheavy);
     }
 
     const int row_w = m0 + wm * 32 * MSUB + r16;  // + 16 i: output row
@@ -668,10 +706,10 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
     }
 }
 
-template <typename T, typename OutT, int EPI>
+template <typename T, typename OutT, int EPI, bool HV>
 __global__ void __launch_bounds__(512, 1) kernel(Params p)
 {
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * Ring<HV>::STAGE];
     // Per-row partial sums of squares of the EPI_QKROPE epilogue: [wave][row group][16].
     __shared__ float red[EPI == EPI_QKROPE ? 8 * 8 * 16 : 1];
     // Items blockIdx.x, + gridDim.x, ...: with gridDim.x a multiple of 8 every item of
@@ -683,10 +721,15 @@ __global__ void __launch_bounds__(512, 1) kernel(Params p)
         const int nb = bid + (int)gridDim.x;
         int nmt = -1, nnt = 0, npart = 0, nli = -1;
         if (nb < p.items) tile_of(p, nb, nmt, nnt, npart, nli);
-        if (mt < p.m_full) tile<T, OutT, EPI, 4>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
-        else if (p.tail_sub == 1) tile<T, OutT, EPI, 1>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
-        else if (p.tail_sub == 2) tile<T, OutT, EPI, 2>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
-        else tile<T, OutT, EPI, 3>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
+        if constexpr (HV) {
+            if (mt == p.m_full - 1) tile<T, OutT, EPI, 5, HV>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
+            else tile<T, OutT, EPI, 4, HV>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
+        } else {
+            if (mt < p.m_full) tile<T, OutT, EPI, 4, HV>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
+            else if (p.tail_sub == 1) tile<T, OutT, EPI, 1, HV>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
+            else if (p.tail_sub == 2) tile<T, OutT, EPI, 2, HV>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
+            else tile<T, OutT, EPI, 3, HV>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
+        }
         if (nb >= p.items) break;
         bid = nb; mt = nmt; nt = nnt; part = npart; li = nli;
         pre = true;
@@ -766,8 +809,20 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     // With M < 256 the tail row is the whole GEMM (a short prompt's projections).
     p.split = 1;
     p.split_all = 0;
+    p.heavy = 0;
+    p.m_main = p.m_full;
     const int m_tiles = p.m_full + (p.tail_sub ? 1 : 0);
-    if (a.split_ws && p.m_full && m_tiles * p.n_tiles <= kSplitTargetItems / 2) {
+    // A tail of at most 64 rows under at least two rounds of full tiles (the block's
+    // up/gate projection at 4096 image + 64 text tokens): the last row of full tiles
+    // takes the tail rows as 320-row tiles, one per workgroup in the last round, which
+    // then ends a quarter of a tile later instead of being followed by a tail phase and
+    // a reduction launch. (The Q/K epilogue would not fit 320 rows in registers.)
+    if (a.epilogue == EPI_GEGLU && p.tail_sub == 1 && p.m_full >= 1 &&
+        (long)p.m_full * p.n_tiles >= 2L * cu_count()) {
+        p.heavy = 1;
+        p.m_main = p.m_full - 1;
+    }
+    if (!p.heavy && a.split_ws && p.m_full && m_tiles * p.n_tiles <= kSplitTargetItems / 2) {
         // Too few tiles for the CUs (a short sequence's narrow projections): split
         // every tile along K, at least 4 K steps per part.
         const size_t per_part = (size_t)m_tiles * p.n_tiles * pingpong::BM * pingpong::BN * sizeof(float);
@@ -780,7 +835,7 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
             p.part = static_cast<float*>(a.split_ws);
         }
     }
-    if (!p.split_all && p.tail_sub && a.split_ws) {
+    if (!p.heavy && !p.split_all && p.tail_sub && a.split_ws) {
         const size_t per_part = (size_t)p.n_tiles * 64 * p.tail_sub * pingpong::BN * sizeof(float);
         int sp = std::min(kMaxSplit, std::max(1, kSplitTargetItems / p.n_tiles));
         sp = std::min(sp, std::max(1, a.K / pingpong::BK / 4));
@@ -797,8 +852,8 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     const int full = p.m_full * p.n_tiles;
     const int last_round = full % kSplitTargetItems;
     // (Not for the fused Q/K epilogue, whose rows are finished per tile.)
-    if (!qk && !p.split_all && a.split_ws && full > kSplitTargetItems && last_round <= kSplitTargetItems / 2 &&
-        last_round > 0) {
+    if (!qk && !p.heavy && !p.split_all && a.split_ws && full > kSplitTargetItems &&
+        last_round <= kSplitTargetItems / 2 && last_round > 0) {
         const size_t tail_bytes =
             p.tail_sub ? ((size_t)p.split * p.n_tiles * 64 * p.tail_sub * pingpong::BN * sizeof(float) + 255) / 256 * 256 : 0;
         const size_t per_part = (size_t)last_round * pingpong::BM * pingpong::BN * sizeof(float);
@@ -812,6 +867,7 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
         }
     }
     const int tiles = p.split_all ? m_tiles * p.n_tiles * p.split
+                      : p.heavy   ? full
                                   : full - p.late + p.late * p.late_split + (p.tail_sub ? p.n_tiles * p.split : 0);
     // One workgroup per CU (the LDS ring allows no second), each walking its items.
     p.items = tiles;
@@ -822,17 +878,19 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     const int epi = qk && p.split_all ? EPI_STORE : a.epilogue;
 #define EHIP_PINGPONG(T)                                                                                            \
     do {                                                                                                      \
-        if (epi == EPI_QKROPE) {                                                                              \
-            hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_QKROPE>), grid, block, 0, s, p);                         \
+        if (p.heavy) {                                                                                        \
+            hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_GEGLU, true>), grid, block, 0, s, p);                    \
+        } else if (epi == EPI_QKROPE) {                                                                       \
+            hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_QKROPE, false>), grid, block, 0, s, p);                  \
         } else if (epi == EPI_STORE) {                                                                        \
-            if (a.c_dtype == DT_F32) hipLaunchKernelGGL((pingpong::kernel<T, float, EPI_STORE>), grid, block, 0, s, p); \
-            else hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_STORE>), grid, block, 0, s, p);                     \
+            if (a.c_dtype == DT_F32) hipLaunchKernelGGL((pingpong::kernel<T, float, EPI_STORE, false>), grid, block, 0, s, p); \
+            else hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_STORE, false>), grid, block, 0, s, p);              \
         } else if (a.epilogue == EPI_GATE_RESID) {                                                            \
-            hipLaunchKernelGGL((pingpong::kernel<T, float, EPI_GATE_RESID>), grid, block, 0, s, p);                 \
+            hipLaunchKernelGGL((pingpong::kernel<T, float, EPI_GATE_RESID, false>), grid, block, 0, s, p);          \
         } else if (a.epilogue == EPI_SWIGLU) {                                                                \
-            hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_SWIGLU>), grid, block, 0, s, p);                         \
+            hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_SWIGLU, false>), grid, block, 0, s, p);                  \
         } else {                                                                                              \
-            hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_GEGLU>), grid, block, 0, s, p);                          \
+            hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_GEGLU, false>), grid, block, 0, s, p);                   \
         }                                                                                                     \
     } while (0)
     if (a.dtype == DT_F16) EHIP_PINGPONG(f16);
