@@ -30,7 +30,7 @@ from pathlib import Path
 SHORT = [
     ("split_reduce_kernelIDF16_Li2", "reduce(up/gate)"), ("split_reduce_kernelIDF16_Li0", "reduce(qkv)"),
     ("split_reduce_kernelIu6__bf16S", "reduce(bf16)"),
-    ("split_reduce_kernel<float, 1>", "reduce(gate-resid)"), ("split_reduce_kernel<float, 0>", "reduce(f32)"),
+    ("split_reduce_kernel<float, 1", "reduce(gate-resid)"), ("split_reduce_kernel<float, 0", "reduce(f32)"),
     ("pingpong6kernelIDF16_DF16_Li5", "gemm qkv+norm+rope"), ("pingpong6kernelIDF16_DF16_Li2", "gemm up/gate+geglu"),
     ("pingpong6kernelIDF16_fLi1", "gemm gate-resid"), ("pingpong6kernelIDF16_DF16_Li0", "gemm store"),
     ("pingpong6kernelIDF16_fLi0", "gemm f32 out"), ("sdl6kernel", "sdpa"), ("sdl14combine", "sdpa combine"),

@@ -47,6 +47,36 @@ def test_stage_attribution_of_a_block():
         (None, False)
 
 
+# The same block with the launches of the current kernels: GEMM kernels carry the
+# heavy-tile flag, reductions their vector width, and the up/gate GEMM (heavy last row
+# of tiles) has no reduction after it.
+BLOCK_HEAVY = [
+    "_ZN4ehip12_GLOBAL__N_123rmsnorm_pair_k32_kernelIfDF16_Li8EEEvPKT_PKfS6_S6_ifPT0_i",
+    "_ZN4ehip8pingpong6kernelIDF16_DF16_Li5ELb0EEEvNS0_6ParamsE",
+    "_ZN4ehip8pingpong19split_reduce_kernelIDF16_Li0ELi4EEEvNS0_6ParamsE",
+    "_ZN4ehip12_GLOBAL__N_123qk_rope_permuted_kernelIDF16_EEvPT_iiiillPKfS5_S5_S5_f",
+    "_ZN4ehip3sdl6kernelIDF16_Li0EEEvNS0_6ParamsE",
+    "_ZN4ehip3sdl14combine_kernelIDF16_EEvNS0_6ParamsEi",
+    "_ZN4ehip8pingpong6kernelIDF16_fLi1ELb0EEEvNS0_6ParamsE",
+    "void ehip::pingpong::split_reduce_kernel<float, 1, 4>(ehip::pingpong::Params)",
+    "_ZN4ehip12_GLOBAL__N_123rmsnorm_pair_k32_kernelIfDF16_Li8EEEvPKT_PKfS6_S6_ifPT0_i",
+    "_ZN4ehip8pingpong6kernelIDF16_DF16_Li2ELb1EEEvNS0_6ParamsE",
+    "_ZN4ehip8pingpong6kernelIDF16_fLi1ELb0EEEvNS0_6ParamsE",
+    "void ehip::pingpong::split_reduce_kernel<float, 1, 4>(ehip::pingpong::Params)",
+]
+STAGES_HEAVY = ["rmsnorm_modulate", "gemm_qkv", "gemm_qkv", "gemm_qkv", "sdpa", "sdpa", "gemm_out", "gemm_out",
+                "rmsnorm_modulate", "gemm_up_gate", "gemm_down", "gemm_down"]
+
+
+def test_stage_attribution_of_the_current_kernel_names():
+    prev, got = None, []
+    for name in BLOCK_HEAVY * 2:
+        st, _ = R.stage_of(name, prev)
+        got.append(st)
+        prev = st
+    assert got == STAGES_HEAVY * 2
+
+
 def write_counters(path, counter, values):
     path.mkdir(parents=True)
     cols = ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value", "Start_Timestamp", "End_Timestamp"]
