@@ -44,8 +44,11 @@ namespace pingpong {
 
 constexpr int BM = 256, BN = 256, BK = 32, NS = 4;
 constexpr int ROWB = BK * 2;                // 64 bytes per staged row
-// Stage layout: the A rows of the stage, then the W rows. A launch with heavy tiles
-// (HV, see Params::heavy) keeps room for 320 A rows in every stage.
+// Launch modes: plain; heavy (Params::heavy: the last row of full tiles is 320 rows
+// tall); ride (Params::ride: every full tile also computes one K range of the tail
+// rows). Heavy and ride launches keep room for 320 A rows in every stage.
+enum { MODE_PLAIN = 0, MODE_HEAVY = 1, MODE_RIDE = 2 };
+// Stage layout: the A rows of the stage, then the W rows.
 template <bool HV> struct Ring {
     static constexpr int A_ROWS = HV ? BM + 64 : BM;
     static constexpr int A_REGION = A_ROWS * ROWB;      // 16 or 20 KiB
@@ -63,6 +66,12 @@ struct Params {
     // of W for 64 rows, and no reduction launch. m_main: the M tiles walked by the
     // full-tile order (m_full, or m_full - 1 when the last row is heavy).
     int heavy, m_main;
+    // ride: the tail rows (M % 256 <= 64) are computed by the full tiles while they
+    // hold the W rows in LDS: full tile (mt, nt) adds tail part mt of tail column block
+    // nt, K steps [K/32 * mt / m_full, K/32 * (mt + 1) / m_full), and stores it as
+    // partial `mt` of `split` = m_full (the tail-row partial layout below), so there
+    // is no tail phase that streams all of W again for 64 rows.
+    int ride;
     void* C; long ldc;
     const float* bias;
     const float* resid; long ld_resid;
@@ -278,7 +287,7 @@ __device__ __forceinline__ void tile_of(const Params& p, int bid, int& mt, int& 
     }
     const int main_full = p.m_main * p.n_tiles - p.late;
     const int late_items = p.late * p.late_split;
-    const int tail_items = p.heavy ? p.n_tiles : p.tail_sub ? p.n_tiles * p.split : 0;
+    const int tail_items = p.heavy ? p.n_tiles : p.ride ? 0 : p.tail_sub ? p.n_tiles * p.split : 0;
     part = 0;
     int region, u;
     if ((main_full & 7) == 0 && (late_items & 7) == 0 && (tail_items & 7) == 0) {
@@ -435,11 +444,12 @@ __device__ __forceinline__ void qk_rope_epilogue(const Params& p, const f32x4 (&
 // One work item. `pre`: its first NS stages were requested by the previous item of this
 // workgroup. nmt >= 0 names the next item (nmt, nnt, npart, nli), whose first NS stages
 // this one requests once its own ring is drained, before its epilogue.
-template <typename T, typename OutT, int EPI, int MSUB, bool HV>
+template <typename T, typename OutT, int EPI, int MSUB, int MODE>
 __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, int li, uint8_t* smem, bool pre,
                                      int nmt, int nnt, int npart, int nli, float* red)
 {
     typedef typename Mfma<T>::vec vec8;
+    constexpr bool HV = MODE != MODE_PLAIN;
     typedef Ring<HV> R;
     // A heavy tile (MSUB 5: 320 rows) loads one more A instruction per stage and wave.
     constexpr int LPS = MSUB == 5 ? 5 : 4;
@@ -454,8 +464,9 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
 
     // Direct loads: wave w fills rows [32w, 32w+32) of the A and W halves of a stage
     // with two 1-KiB instructions each; lane l lands at bytes [16l, 16l+16), i.e.
-    // row (l >> 2), physical chunk l & 3 = logical chunk (l & 3) ^ fsw(row). A heavy
-    // tile's A rows 256 + 8w .. + 7 come from a third instruction of lanes 0-31.
+    // row (l >> 2), physical chunk l & 3 = logical chunk (l & 3) ^ fsw(row). The tail
+    // rows of a heavy or riding tile (stage rows 256 + 8w .. + 7) come from a third
+    // instruction of lanes 0-31.
     uint32_t a_src[3], w_src[2];
     auto sources = [&](int m_0, int n_0, uint32_t* as, uint32_t* ws) {
 #pragma unroll
@@ -467,7 +478,8 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
         }
         if constexpr (HV) {
             const int row = BM + wave * 8 + (lane >> 2);
-            as[2] = (uint32_t)((long)(m_0 + row) * p.a_row_bytes + (((lane & 3) ^ fsw(row)) << 4));
+            const int tail0 = MODE == MODE_HEAVY ? m_0 : (p.m_full - 1) * BM;  // + BM: the first tail row
+            as[2] = (uint32_t)((long)(tail0 + row) * p.a_row_bytes + (((lane & 3) ^ fsw(row)) << 4));
         }
     };
     sources(m0, n0, a_src, w_src);
@@ -493,7 +505,11 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
                                                          0, 0);
         }
     };
-    auto issue = [&](int kt) { issue_at(a_src, w_src, kt0, kt, MSUB == 5); };
+    // Riding: the K steps [rk0, rk1) of this item that also compute its tail part.
+    const int rk0 = MODE == MODE_RIDE ? (int)((long)nk_all * mt / p.m_full) - kt0 : 0;
+    const int rk1 = MODE == MODE_RIDE ? (int)((long)nk_all * (mt + 1) / p.m_full) - kt0 : 0;
+    auto riding = [&](int kt) { return MODE == MODE_RIDE && kt >= rk0 && kt < rk1; };
+    auto issue = [&](int kt) { issue_at(a_src, w_src, kt0, kt, MSUB == 5 || riding(kt)); };
 
     // Fragment of 16 rows x 32 k: lane l reads row l % 16, logical chunk l / 16.
     const int r16 = lane & 15, q16 = lane >> 4;
@@ -510,6 +526,17 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
             for (int r = 0; r < 4; ++r) acc[i][j][r] = 0.f;
 
     vec8 af[2 * MSUB], bf[4];
+    // Riding: the tail part's accumulators (this wave's 32 of the 64 tail rows) and
+    // fragments.
+    constexpr int TR = MODE == MODE_RIDE ? 2 : 0;
+    f32x4 tacc[TR ? TR : 1][4];
+    vec8 tf[TR ? TR : 1];
+#pragma unroll
+    for (int i = 0; i < TR; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) tacc[i][j][r] = 0.f;
     // Memory cluster: this wave's fragments of stage kt into registers.
     auto read_frags = [&](int kt) {
         const uint8_t* st = smem + (kt & (NS - 1)) * R::STAGE;
@@ -519,13 +546,22 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
 #pragma unroll
         for (int i = 0; i < 2 * MSUB; ++i)
             af[i] = *reinterpret_cast<const vec8*>(st + (wm * 32 * MSUB + i * 16) * ROWB + frag);
+        if (riding(kt))
+#pragma unroll
+            for (int i = 0; i < TR; ++i)
+                tf[i] = *reinterpret_cast<const vec8*>(st + (BM + wm * 32 + i * 16) * ROWB + frag);
     };
-    // MFMA cluster on the registers.
-    auto mfma_cluster = [&]() {
+    // MFMA cluster on the registers of stage kt.
+    auto mfma_cluster = [&](int kt) {
 #pragma unroll
         for (int i = 0; i < 2 * MSUB; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j) acc[i][j] = Mfma<T>::run(bf[j], af[i], acc[i][j]);
+        if (riding(kt))
+#pragma unroll
+            for (int i = 0; i < TR; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) tacc[i][j] = Mfma<T>::run(bf[j], tf[i], tacc[i][j]);
     };
     // Loads requested after stage s, per wave, when s must have landed: LPS x min(NS-2, nk-1-s).
     auto wait_stage = [&](int s) { wait_stages<LPS>(min(NS - 2, nk - 1 - s)); };
@@ -551,7 +587,7 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
         read_frags(0);
         phase_barrier();  // end of phase 0
         for (int t = 0; t < nk; ++t) {
-            mfma_cluster();
+            mfma_cluster(t);
             if (t + 1 < nk) wait_stage(t + 1);
             phase_barrier();  // end of phase 2t+1
             if (t + 1 < nk) {
@@ -567,7 +603,7 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
             if (t >= 1 && t - 1 + NS < nk) issue(t - 1 + NS);
             if (t + 1 < nk) wait_stage(t + 1);
             phase_barrier();  // end of phase 2t+1
-            mfma_cluster();
+            mfma_cluster(t);
             phase_barrier();  // end of phase 2t+2
         }
     }
@@ -580,10 +616,23 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
         const int nnk = (int)((long)nk_all * (npart + 1) / nparts) - nkt0;
         uint32_t na[3], nw[2];
         sources(nmt * BM, nnt * BN, na, nw);
-        const bool nheavy = HV && p.heavy && nmt == p.m_full - 1;
+        const bool nheavy = MODE == MODE_HEAVY && nmt == p.m_full - 1;
+        // Riding: the next item's tail K steps among its first stages.
+        const int nrk0 = MODE == MODE_RIDE ? (int)((long)nk_all * nmt / p.m_full) - nkt0 : 0;
+        const int nrk1 = MODE == MODE_RIDE ? (int)((long)nk_all * (nmt + 1) / p.m_full) - nkt0 : 0;
 #pragma unroll
         for (int s = 0; s < NS; ++s)
-            if (s < nnk) issue_at(na, nw, nkt0, s, nheavy);
+            if (s < nnk) issue_at(na, nw, nkt0, s, nheavy || (s >= nrk0 && s < nrk1));
+    }
+    if constexpr (MODE == MODE_RIDE) {
+        // The tail part: partial mt of tail column block nt.
+        float* base = p.part + ((size_t)nt * p.split + mt) * 64 * BN;
+#pragma unroll
+        for (int i = 0; i < TR; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                *reinterpret_cast<f32x4*>(base + (size_t)(wm * 32 + 16 * i + r16) * BN + wn * 64 + 4 * q16 + 16 * j) =
+                    tacc[i][j];
     }
 
     const int row_w = m0 + wm * 32 * MSUB + r16;  // + 16 i: output row
@@ -706,10 +755,10 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
     }
 }
 
-template <typename T, typename OutT, int EPI, bool HV>
+template <typename T, typename OutT, int EPI, int MODE>
 __global__ void __launch_bounds__(512, 1) kernel(Params p)
 {
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * Ring<HV>::STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * Ring<MODE != MODE_PLAIN>::STAGE];
     // Per-row partial sums of squares of the EPI_QKROPE epilogue: [wave][row group][16].
     __shared__ float red[EPI == EPI_QKROPE ? 8 * 8 * 16 : 1];
     // Items blockIdx.x, + gridDim.x, ...: with gridDim.x a multiple of 8 every item of
@@ -721,14 +770,16 @@ __global__ void __launch_bounds__(512, 1) kernel(Params p)
         const int nb = bid + (int)gridDim.x;
         int nmt = -1, nnt = 0, npart = 0, nli = -1;
         if (nb < p.items) tile_of(p, nb, nmt, nnt, npart, nli);
-        if constexpr (HV) {
-            if (mt == p.m_full - 1) tile<T, OutT, EPI, 5, HV>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
-            else tile<T, OutT, EPI, 4, HV>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
+        if constexpr (MODE == MODE_HEAVY) {
+            if (mt == p.m_full - 1) tile<T, OutT, EPI, 5, MODE>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
+            else tile<T, OutT, EPI, 4, MODE>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
+        } else if constexpr (MODE == MODE_RIDE) {
+            tile<T, OutT, EPI, 4, MODE>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
         } else {
-            if (mt < p.m_full) tile<T, OutT, EPI, 4, HV>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
-            else if (p.tail_sub == 1) tile<T, OutT, EPI, 1, HV>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
-            else if (p.tail_sub == 2) tile<T, OutT, EPI, 2, HV>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
-            else tile<T, OutT, EPI, 3, HV>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
+            if (mt < p.m_full) tile<T, OutT, EPI, 4, MODE>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
+            else if (p.tail_sub == 1) tile<T, OutT, EPI, 1, MODE>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
+            else if (p.tail_sub == 2) tile<T, OutT, EPI, 2, MODE>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
+            else tile<T, OutT, EPI, 3, MODE>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
         }
         if (nb >= p.items) break;
         bid = nb; mt = nmt; nt = nnt; part = npart; li = nli;
@@ -835,7 +886,21 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
             p.part = static_cast<float*>(a.split_ws);
         }
     }
-    if (!p.heavy && !p.split_all && p.tail_sub && a.split_ws) {
+    // A tail of at most 64 rows under whole rounds of full tiles (the block's output and
+    // down projections): the full tiles compute it while they hold W (Params::ride),
+    // m_full K ranges of it, one per row of full tiles. (The Q/K/V projection keeps its
+    // 5-part split tail: with 16 parts its reduction would read three times as much.)
+    p.ride = 0;
+    const int full = p.m_full * p.n_tiles;
+    if (!p.heavy && !p.split_all && a.split_ws && a.epilogue == EPI_GATE_RESID &&
+        p.tail_sub == 1 && p.m_full >= 2 && p.m_full <= kMaxSplit && a.K / pingpong::BK >= p.m_full &&
+        full >= cu_count() && full % cu_count() == 0 &&
+        (size_t)p.m_full * p.n_tiles * 64 * pingpong::BN * sizeof(float) <= a.split_ws_bytes) {
+        p.ride = 1;
+        p.split = p.m_full;
+        p.part = static_cast<float*>(a.split_ws);
+    }
+    if (!p.heavy && !p.ride && !p.split_all && p.tail_sub && a.split_ws) {
         const size_t per_part = (size_t)p.n_tiles * 64 * p.tail_sub * pingpong::BN * sizeof(float);
         int sp = std::min(kMaxSplit, std::max(1, kSplitTargetItems / p.n_tiles));
         sp = std::min(sp, std::max(1, a.K / pingpong::BK / 4));
@@ -849,10 +914,9 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     p.late = 0;
     p.late_split = 1;
     p.late_part = nullptr;
-    const int full = p.m_full * p.n_tiles;
     const int last_round = full % kSplitTargetItems;
     // (Not for the fused Q/K epilogue, whose rows are finished per tile.)
-    if (!qk && !p.heavy && !p.split_all && a.split_ws && full > kSplitTargetItems &&
+    if (!qk && !p.heavy && !p.ride && !p.split_all && a.split_ws && full > kSplitTargetItems &&
         last_round <= kSplitTargetItems / 2 && last_round > 0) {
         const size_t tail_bytes =
             p.tail_sub ? ((size_t)p.split * p.n_tiles * 64 * p.tail_sub * pingpong::BN * sizeof(float) + 255) / 256 * 256 : 0;
@@ -867,7 +931,7 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
         }
     }
     const int tiles = p.split_all ? m_tiles * p.n_tiles * p.split
-                      : p.heavy   ? full
+                      : p.heavy || p.ride ? full
                                   : full - p.late + p.late * p.late_split + (p.tail_sub ? p.n_tiles * p.split : 0);
     // One workgroup per CU (the LDS ring allows no second), each walking its items.
     p.items = tiles;
@@ -879,7 +943,9 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
 #define EHIP_PINGPONG(T)                                                                                            \
     do {                                                                                                      \
         if (p.heavy) {                                                                                        \
-            hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_GEGLU, true>), grid, block, 0, s, p);                    \
+            hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_GEGLU, pingpong::MODE_HEAVY>), grid, block, 0, s, p);    \
+        } else if (p.ride) {                                                                                  \
+            hipLaunchKernelGGL((pingpong::kernel<T, float, EPI_GATE_RESID, pingpong::MODE_RIDE>), grid, block, 0, s, p); \
         } else if (epi == EPI_QKROPE) {                                                                       \
             hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_QKROPE, false>), grid, block, 0, s, p);                  \
         } else if (epi == EPI_STORE) {                                                                        \

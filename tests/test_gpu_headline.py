@@ -65,6 +65,36 @@ def test_headline_block_against_oracle(ctx):
     ctx.call("block_release", 80)
 
 
+@pytest.mark.parametrize("dt", [E.FP16, E.BF16], ids=lambda d: NAMES[d])
+def test_full_width_block_short_tail_against_oracle(ctx, dt):
+    # Full width at S = 4096 + 24 text slots (16 valid): a 24-row tail. The up/gate GEMM
+    # takes it on its last row of tiles (320-row tiles, 40 rows past S computed and not
+    # stored); the output and down GEMMs compute it inside their full tiles, one K range
+    # per row of tiles (tail rows past S read A rows that are never stored either); the
+    # Q/K/V GEMM splits it into K parts.
+    text_slots, valid_text = 24, 16
+    S24 = GRID * GRID + text_slots
+    w = small_block(DIM, FFN, seed=3)
+    x = O.normal((S24, DIM), 4)
+    mods = O.normal((6, DIM), 5, std=0.5)
+    cos, sin, mask = O.dit_constants(O.rope_frequencies(), GRID, GRID, valid_text, text_slots)
+    valid = GRID * GRID + valid_text
+    assert int(np.sum(mask == 0)) == valid
+    ref = O.block_forward(w, x, mods, cos, sin, mask)
+    ctx.block_upload(81, w, DIM, FFN, dt)
+    out = empty((S24, DIM))
+    ctx.block_forward(81, dev(x), out, dev(mods), dev(cos), dev(sin), S24, mask=dev(mask), valid_keys=valid)
+    got = host(out)
+    g = kat.gate(got, ref, *kat.BLOCK_GATES[NAMES[dt]])
+    print(f"{NAMES[dt]} block at S={S24}: max|d| {g['max_abs_error']:.3g} (limit {g['max_abs_limit']:.3g}), "
+          f"nrmse {g['nrmse']:.3g} (limit {g['nrmse_limit']:.3g})", flush=True)
+    assert g["passed"], (NAMES[dt], g)
+    again = empty((S24, DIM))
+    ctx.block_forward(81, dev(x), again, dev(mods), dev(cos), dev(sin), S24, mask=dev(mask), valid_keys=valid)
+    np.testing.assert_array_equal(host(again), got)  # repeat-deterministic
+    ctx.call("block_release", 81)
+
+
 def oracle_prediction(heads, blocks, latent, text, feat, cos, sin, mask):
     x, c, mods = O.input_head({k: heads[k] for k in O.INPUT_HEAD_FIELDS}, latent, text, feat)
     for w in blocks:
