@@ -33,7 +33,9 @@ SHORT = [
     ("split_reduce_kernel<float, 1", "reduce(gate-resid)"), ("split_reduce_kernel<float, 0", "reduce(f32)"),
     ("pingpong6kernelIDF16_DF16_Li5", "gemm qkv+norm+rope"), ("pingpong6kernelIDF16_DF16_Li2", "gemm up/gate+geglu"),
     ("pingpong6kernelIDF16_fLi1", "gemm gate-resid"), ("pingpong6kernelIDF16_DF16_Li0", "gemm store"),
-    ("pingpong6kernelIDF16_fLi0", "gemm f32 out"), ("sdl6kernel", "sdpa"), ("sdl14combine", "sdpa combine"),
+    ("pingpong6kernelIDF16_fLi0", "gemm f32 out"), ("pingpong6kernelIDF16_DF16_Li4", "gemm up/gate+swiglu"),
+    ("split_reduce_kernelIDF16_Li4", "reduce(up/gate swiglu)"), ("rmsnorm_persist", "rmsnorm (row-major)"),
+    ("sdl6kernel", "sdpa"), ("sdl14combine", "sdpa combine"),
     ("rmsnorm_pair_k32", "rmsnorm+modulate"), ("qk_rope_permuted", "qk norm+rope (split tail)"),
     ("qk_norm_rope", "qk norm+rope"), ("euler", "euler"), ("finite", "finite"), ("fill_int", "fill_int"),
     ("copyBuffer", "copy"), ("gemv", "gemv"), ("layernorm", "layernorm+mod"), ("transpose_tokens", "to tokens"),
@@ -78,6 +80,19 @@ def read_csv(directory, suffix):
     return rows
 
 
+def bench_classes(log):
+    """The HIP-event class table of the last bench.py JSON line in a log."""
+    line = [x for x in Path(log).read_text().splitlines() if x.startswith("{")][-1]
+    d = json.loads(line)
+    out = ["", "HIP-event figures of the same run (per launch of each class, split-K reduction included):", "",
+           "| class | launches | avg us | TFLOP/s |", "|---|---:|---:|---:|"]
+    for name, k in d["kernels"].items():
+        tf = "-" if k.get("tflops") is None else f"{k['tflops']:.1f}"
+        out.append(f"| {name} | {k['launches']} | {k['avg_us']:.1f} | {tf} |")
+    out += ["", f"{d['value']:.2f} {d['unit']}, {d['ms_per_step']:.2f} ms per step under the profiler."]
+    return out
+
+
 def trace(args):
     rows = read_csv(args.dir, "_kernel_trace.csv")
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
@@ -88,6 +103,8 @@ def trace(args):
     out = [f"# {args.title}", ""]
     if args.command:
         out += ["Command (from the repository root, on one MI355X):", "", "```", *args.command, "```", ""]
+    if args.note:
+        out += [args.note, ""]
     out += ["| kernel | calls | avg us | min us | max us | % time |", "|---|---:|---:|---:|---:|---:|"]
     for name, v in sorted(dur.items(), key=lambda kv: -sum(kv[1])):
         if sum(v) / total < 1e-4:
@@ -134,6 +151,8 @@ def trace(args):
                 "| after | before | count | avg us | max us | total us / step |", "|---|---|---:|---:|---:|---:|"]
         for (a, b), v in sorted(gaps.items(), key=lambda kv: -sum(kv[1]))[:args.gaps]:
             out.append(f"| {a} | {b} | {len(v)} | {statistics.mean(v):.2f} | {max(v):.1f} | {sum(v) / K:.1f} |")
+    if args.bench_log:
+        out += bench_classes(args.bench_log)
     print("\n".join(out))
 
 
@@ -233,6 +252,8 @@ def main(argv=None):
     t.add_argument("--gaps", type=int, default=12)
     t.add_argument("--title", default="Kernel trace")
     t.add_argument("--command", action="append", default=[])
+    t.add_argument("--note", default="")
+    t.add_argument("--bench-log", default="", help="bench.py output of the traced run: its HIP-event class table")
     f = sub.add_parser("traffic")
     f.add_argument("fetch_dir")
     f.add_argument("write_dir")
