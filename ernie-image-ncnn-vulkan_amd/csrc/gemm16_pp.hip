@@ -28,6 +28,12 @@
 //     block's GEMMs read (RMSNorm, attention and GEGLU outputs) are stored this way.
 //   * Workgroup b runs on XCD b % 8: each XCD gets a contiguous range of tiles
 //     (4 M tiles per N sweep, sharing its own L2), and the tail row of tiles last.
+//   * A tail row (M % 256 rows) is computed one of three ways. Split: its tiles are
+//     cut along K into parts that fill the CUs and a reduction launch adds them.
+//     Heavy (Params::heavy): the last row of full tiles is 320 rows tall. Riding
+//     (Params::ride): every full tile computes one K range of the tail rows below
+//     it. The last two reuse the W rows already in LDS instead of streaming all of W
+//     again for at most 64 rows.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -564,6 +570,8 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
                 for (int j = 0; j < 4; ++j) tacc[i][j] = Mfma<T>::run(bf[j], tf[i], tacc[i][j]);
     };
     // Loads requested after stage s, per wave, when s must have landed: LPS x min(NS-2, nk-1-s).
+    // A riding item's window stages carry a fifth load; counting four for every stage
+    // can only wait for more loads than stage s needs, never fewer.
     auto wait_stage = [&](int s) { wait_stages<LPS>(min(NS - 2, nk - 1 - s)); };
 
     // Prologue: request stages 0..NS-1 (unless the previous item did), wait for stage 0
