@@ -38,6 +38,7 @@
 #include "kernels.hpp"
 
 #include <algorithm>
+#include <vector>
 
 namespace ehip {
 namespace {
@@ -52,8 +53,9 @@ constexpr int BM = 256, BN = 256, BK = 32, NS = 4;
 constexpr int ROWB = BK * 2;                // 64 bytes per staged row
 // Launch modes: plain; heavy (Params::heavy: the last row of full tiles is 320 rows
 // tall); ride (Params::ride: every full tile also computes one K range of the tail
-// rows). Heavy and ride launches keep room for 320 A rows in every stage.
-enum { MODE_PLAIN = 0, MODE_HEAVY = 1, MODE_RIDE = 2 };
+// rows); light (Params::light: some full tiles also compute 16 of the tail rows over
+// all of K). Heavy, ride and light launches keep room for 320 A rows in every stage.
+enum { MODE_PLAIN = 0, MODE_HEAVY = 1, MODE_RIDE = 2, MODE_LIGHT = 3 };
 // Stage layout: the A rows of the stage, then the W rows.
 template <bool HV> struct Ring {
     static constexpr int A_ROWS = HV ? BM + 64 : BM;
@@ -78,6 +80,12 @@ struct Params {
     // partial `mt` of `split` = m_full (the tail-row partial layout below), so there
     // is no tail phase that streams all of W again for 64 rows.
     int ride;
+    // light: the tail rows (M % 256 <= 64) are cut into light_c chunks of 16 rows; for
+    // each column block nt, chunk e is computed over all of K by one full tile of M
+    // group e (light_chunk), as 16 more rows while it holds W. The host enables it only
+    // when those tiles fall at most ceil(light tiles / grid) to a workgroup, so the
+    // extra sixteenth of a tile is spread over the CUs: no tail phase, no reduction.
+    int light, light_c;
     void* C; long ldc;
     const float* bias;
     const float* resid; long ld_resid;
@@ -116,16 +124,29 @@ struct Params {
 
 // Full tile f of the tile order -> (mt, nt): GM M tiles per N sweep, so the
 // workgroups that run together share A and W panels.
-__device__ __forceinline__ void full_order(const Params& p, int f, int& mt, int& nt)
+constexpr int GM = 4;
+__host__ __device__ __forceinline__ void full_order(const Params& p, int f, int& mt, int& nt)
 {
-    constexpr int GM = 4;
     const int group_size = GM * p.n_tiles;
     const int group = f / group_size;
     const int first_m = group * GM;
-    const int gm = min(p.m_main - first_m, GM);
+    const int gm = p.m_main - first_m < GM ? p.m_main - first_m : GM;
     const int in_group = f - group * group_size;
     mt = first_m + in_group % gm;
     nt = in_group / gm;
+}
+
+// Light tiles: the tail chunk (rows m_full * 256 + 16 e .. + 15) that full tile (mt, nt)
+// also computes, or -1. Chunk e of column block nt belongs to M group e (M tiles
+// 4e .. 4e + 3, all full when m_full >= 4 light_c), at the group offset
+// (nt / 8 + e) mod 4: one tile per (chunk, column block), and along the tile order the
+// offset changes every 8 column blocks, which spreads the light tiles over the
+// workgroups (the host checks the spread for each launch shape).
+__host__ __device__ __forceinline__ int light_chunk(const Params& p, int mt, int nt)
+{
+    const int e = mt / GM;
+    if (!p.light || e >= p.light_c) return -1;
+    return mt - e * GM == (nt / 8 + e) % GM ? e : -1;
 }
 
 // The epilogue of a reduced element: row m, output column c (GEGLU / SwiGLU: of
@@ -275,8 +296,9 @@ __device__ __forceinline__ int fsw(int r) { return (r >> 1) & 3; }
 // items (the last `late` full tiles, each in `late_split` K parts) and then of the
 // tail-row items (a tail tile split into `split` K parts), so the short items run
 // last and spread over all XCDs; or, with heavy tiles, of the last row of full
-// tiles, one per workgroup in the last round. li = index of a late-split tile, else -1.
-__device__ __forceinline__ void tile_of(const Params& p, int bid, int& mt, int& nt, int& part, int& li)
+// tiles, one per workgroup in the last round. Riding and light launches have no
+// tail-row items. li = index of a late-split tile, else -1.
+__host__ __device__ __forceinline__ void tile_of(const Params& p, int bid, int& mt, int& nt, int& part, int& li)
 {
     li = -1;
     if (p.split_all) {
@@ -293,7 +315,7 @@ __device__ __forceinline__ void tile_of(const Params& p, int bid, int& mt, int& 
     }
     const int main_full = p.m_main * p.n_tiles - p.late;
     const int late_items = p.late * p.late_split;
-    const int tail_items = p.heavy ? p.n_tiles : p.ride ? 0 : p.tail_sub ? p.n_tiles * p.split : 0;
+    const int tail_items = p.heavy ? p.n_tiles : p.ride || p.light ? 0 : p.tail_sub ? p.n_tiles * p.split : 0;
     part = 0;
     int region, u;
     if ((main_full & 7) == 0 && (late_items & 7) == 0 && (tail_items & 7) == 0) {
@@ -447,18 +469,111 @@ __device__ __forceinline__ void qk_rope_epilogue(const Params& p, const f32x4 (&
     }
 }
 
+// Epilogue of a light tile's tail chunk e: output row m_full * 256 + 16 e + r16. The
+// wave holds the chunk's columns 16 j + 4 q16 + r of its 64 for j = wm (lacc[0]) and
+// j = wm + 2 (lacc[1]), the pairs that the GLU epilogues (up, gate) and the Q/K
+// epilogue (dimension, rotary partner) combine in one lane. A Q or K head's 128
+// columns then lie in the four waves 4 h .. 4 h + 3; each row's sum of squares is
+// added over them through `red` in one fixed order, so all four use the same value.
+template <typename OutT, int EPI>
+__device__ __forceinline__ void light_epilogue(const Params& p, const f32x4 (&lacc)[2], int chunk, int n0, int wave,
+                                               int wm, int wn, int q16, int r16, float* red)
+{
+    typedef OutT out4 __attribute__((ext_vector_type(4)));
+    const int m = p.m_full * BM + 16 * chunk + r16;
+    if constexpr (EPI == EPI_QKROPE) {
+        if (n0 < p.qk_cols) {
+            const int head_col = n0 + 128 * (wn >> 1);
+            const float* g = head_col >= p.k_col ? p.gk : p.gq;
+            float t = 0.f;
+#pragma unroll
+            for (int x = 0; x < 2; ++x)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) t += lacc[x][r] * lacc[x][r];
+            t += __shfl_xor(t, 16, 64);
+            t += __shfl_xor(t, 32, 64);
+            float* lred = red + 8 * 8 * 16;  // after the full rows' slots
+            if (q16 == 0) lred[wave * 16 + r16] = t;
+            const int d = 32 * (wn & 1) + 4 * q16 + 16 * wm;
+            const f32x4 ga = *reinterpret_cast<const f32x4*>(g + d);
+            const f32x4 gb = *reinterpret_cast<const f32x4*>(g + d + 64);
+            const size_t mc = (size_t)min(m, p.M - 1) * 128;
+            const f32x4 clo = *reinterpret_cast<const f32x4*>(p.cos_t + mc + d);
+            const f32x4 chi = *reinterpret_cast<const f32x4*>(p.cos_t + mc + d + 64);
+            const f32x4 slo = *reinterpret_cast<const f32x4*>(p.sin_t + mc + d);
+            const f32x4 shi = *reinterpret_cast<const f32x4*>(p.sin_t + mc + d + 64);
+            phase_barrier();
+            const int w0 = wave & ~3;
+            const float ss = (lred[w0 * 16 + r16] + lred[(w0 + 1) * 16 + r16]) +
+                             (lred[(w0 + 2) * 16 + r16] + lred[(w0 + 3) * 16 + r16]);
+            const float inv = 1.0f / sqrtf(ss / 128.f + p.qk_eps);
+            out4 lo, hi;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float na = lacc[0][r] * inv * ga[r];
+                const float nb = lacc[1][r] * inv * gb[r];
+                lo[r] = OutT(na * clo[r] - nb * slo[r]);
+                hi[r] = OutT(nb * chi[r] + na * shi[r]);
+            }
+            if (m < p.M) {
+                OutT* crow = static_cast<OutT*>(p.C) + (size_t)m * p.ldc + head_col;
+                *reinterpret_cast<out4*>(crow + d) = lo;
+                *reinterpret_cast<out4*>(crow + d + 64) = hi;
+            }
+            return;
+        }
+        // V columns: stored as they are, below.
+    }
+    if (m >= p.M) return;
+    if constexpr (epi_glu(EPI)) {
+        if (n0 + wn * 64 >= p.N) return;
+        OutT* c = static_cast<OutT*>(p.C) + (size_t)m * p.c_rs + (size_t)((n0 + wn * 64) >> 6) * p.c_ss + 4 * q16 +
+                  16 * wm;
+        out4 o;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = OutT(lacc[0][r] * glu_act<EPI == EPI_SWIGLU>(lacc[1][r]));
+        if (p.vec) *reinterpret_cast<out4*>(c) = o;
+        else
+#pragma unroll
+            for (int r = 0; r < 4; ++r) c[r] = o[r];
+    } else {
+        static_assert(EPI != EPI_GATE_RESID, "light tiles take no gate + residual epilogue");
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+            const int n = n0 + wn * 64 + 4 * q16 + 16 * (wm + 2 * x);
+            if (n >= p.N) continue;
+            OutT* c = static_cast<OutT*>(p.C) + (size_t)m * p.ldc + n;
+            if (p.vec) {
+                f32x4 v = lacc[x];
+                if (p.bias) v += *reinterpret_cast<const f32x4*>(p.bias + n);
+                *reinterpret_cast<out4*>(c) = out4{OutT(v[0]), OutT(v[1]), OutT(v[2]), OutT(v[3])};
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if (n + r >= p.N) continue;
+                    float v = lacc[x][r];
+                    if (p.bias) v += p.bias[n + r];
+                    c[r] = OutT(v);
+                }
+            }
+        }
+    }
+}
+
 // One work item. `pre`: its first NS stages were requested by the previous item of this
 // workgroup. nmt >= 0 names the next item (nmt, nnt, npart, nli), whose first NS stages
-// this one requests once its own ring is drained, before its epilogue.
-template <typename T, typename OutT, int EPI, int MSUB, int MODE>
+// this one requests once its own ring is drained, before its epilogue. XR: this item is
+// a light tile carrying tail chunk xe; nxe: the next item's chunk (or -1).
+template <typename T, typename OutT, int EPI, int MSUB, int MODE, int XR = 0>
 __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, int li, uint8_t* smem, bool pre,
-                                     int nmt, int nnt, int npart, int nli, float* red)
+                                     int nmt, int nnt, int npart, int nli, float* red, int xe = -1, int nxe = -1)
 {
     typedef typename Mfma<T>::vec vec8;
     constexpr bool HV = MODE != MODE_PLAIN;
     typedef Ring<HV> R;
-    // A heavy tile (MSUB 5: 320 rows) loads one more A instruction per stage and wave.
-    constexpr int LPS = MSUB == 5 ? 5 : 4;
+    // A heavy tile (MSUB 5: 320 rows) or a light tile loads one more A instruction per
+    // stage and wave.
+    constexpr int LPS = MSUB == 5 || XR ? 5 : 4;
     const int m0 = mt * BM, n0 = nt * BN;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -472,9 +587,10 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
     // with two 1-KiB instructions each; lane l lands at bytes [16l, 16l+16), i.e.
     // row (l >> 2), physical chunk l & 3 = logical chunk (l & 3) ^ fsw(row). The tail
     // rows of a heavy or riding tile (stage rows 256 + 8w .. + 7) come from a third
-    // instruction of lanes 0-31.
+    // instruction of lanes 0-31; the 16 chunk rows of a light tile (stage rows
+    // 256 + 2w, + 1) from a third instruction of lanes 0-7.
     uint32_t a_src[3], w_src[2];
-    auto sources = [&](int m_0, int n_0, uint32_t* as, uint32_t* ws) {
+    auto sources = [&](int m_0, int n_0, uint32_t* as, uint32_t* ws, int chunk) {
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             const int row = wave * 32 + q * 16 + (lane >> 2);
@@ -482,13 +598,17 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
             as[q] = (uint32_t)((long)(m_0 + row) * p.a_row_bytes + c * 16);
             ws[q] = (uint32_t)((long)(n_0 + row) * p.w_row_bytes + c * 16);
         }
-        if constexpr (HV) {
+        if constexpr (MODE == MODE_LIGHT) {
+            const int row = BM + wave * 2 + (lane >> 2);
+            const int src = p.m_full * BM + 16 * max(chunk, 0) + wave * 2 + (lane >> 2);
+            as[2] = (uint32_t)((long)src * p.a_row_bytes + (((lane & 3) ^ fsw(row)) << 4));
+        } else if constexpr (HV) {
             const int row = BM + wave * 8 + (lane >> 2);
             const int tail0 = MODE == MODE_HEAVY ? m_0 : (p.m_full - 1) * BM;  // + BM: the first tail row
             as[2] = (uint32_t)((long)(tail0 + row) * p.a_row_bytes + (((lane & 3) ^ fsw(row)) << 4));
         }
     };
-    sources(m0, n0, a_src, w_src);
+    sources(m0, n0, a_src, w_src, xe);
     // K steps of this item: all of them, or part `part` of `split` for a tail tile.
     const int nk_all = p.K / BK;
     const int parts = item_parts(p, mt, li);
@@ -505,7 +625,11 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(st + R::A_REGION + (wave * 32 + q * 16) * ROWB),
                                                      16, ws[q], koff_w, 0, 0);
         }
-        if constexpr (HV) {
+        if constexpr (MODE == MODE_LIGHT) {
+            if (heavy_item && lane < 8)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(st + (BM + wave * 2) * ROWB), 16, as[2], koff,
+                                                         0, 0);
+        } else if constexpr (HV) {
             if (heavy_item && lane < 32)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(st + (BM + wave * 8) * ROWB), 16, as[2], koff,
                                                          0, 0);
@@ -515,7 +639,7 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
     const int rk0 = MODE == MODE_RIDE ? (int)((long)nk_all * mt / p.m_full) - kt0 : 0;
     const int rk1 = MODE == MODE_RIDE ? (int)((long)nk_all * (mt + 1) / p.m_full) - kt0 : 0;
     auto riding = [&](int kt) { return MODE == MODE_RIDE && kt >= rk0 && kt < rk1; };
-    auto issue = [&](int kt) { issue_at(a_src, w_src, kt0, kt, MSUB == 5 || riding(kt)); };
+    auto issue = [&](int kt) { issue_at(a_src, w_src, kt0, kt, MSUB == 5 || XR || riding(kt)); };
 
     // Fragment of 16 rows x 32 k: lane l reads row l % 16, logical chunk l / 16.
     const int r16 = lane & 15, q16 = lane >> 4;
@@ -543,6 +667,14 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) tacc[i][j][r] = 0.f;
+    // Light tile: the chunk's fragment (stage rows 256 .. 271) and its accumulators for
+    // this wave's column blocks j = wm and wm + 2.
+    f32x4 lacc[2];
+    vec8 lf;
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) lacc[x][r] = 0.f;
     // Memory cluster: this wave's fragments of stage kt into registers.
     auto read_frags = [&](int kt) {
         const uint8_t* st = smem + (kt & (NS - 1)) * R::STAGE;
@@ -556,6 +688,7 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
 #pragma unroll
             for (int i = 0; i < TR; ++i)
                 tf[i] = *reinterpret_cast<const vec8*>(st + (BM + wm * 32 + i * 16) * ROWB + frag);
+        if constexpr (XR) lf = *reinterpret_cast<const vec8*>(st + BM * ROWB + frag);
     };
     // MFMA cluster on the registers of stage kt.
     auto mfma_cluster = [&](int kt) {
@@ -568,6 +701,12 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
             for (int i = 0; i < TR; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) tacc[i][j] = Mfma<T>::run(bf[j], tf[i], tacc[i][j]);
+        if constexpr (XR) {
+            // Column blocks wm and wm + 2, selected without a branch in the cluster.
+            const vec8 b0 = wm ? bf[1] : bf[0], b1 = wm ? bf[3] : bf[2];
+            lacc[0] = Mfma<T>::run(b0, lf, lacc[0]);
+            lacc[1] = Mfma<T>::run(b1, lf, lacc[1]);
+        }
     };
     // Loads requested after stage s, per wave, when s must have landed: LPS x min(NS-2, nk-1-s).
     // A riding item's window stages carry a fifth load; counting four for every stage
@@ -623,8 +762,8 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
         const int nkt0 = (int)((long)nk_all * npart / nparts);
         const int nnk = (int)((long)nk_all * (npart + 1) / nparts) - nkt0;
         uint32_t na[3], nw[2];
-        sources(nmt * BM, nnt * BN, na, nw);
-        const bool nheavy = MODE == MODE_HEAVY && nmt == p.m_full - 1;
+        sources(nmt * BM, nnt * BN, na, nw, nxe);
+        const bool nheavy = (MODE == MODE_HEAVY && nmt == p.m_full - 1) || nxe >= 0;
         // Riding: the next item's tail K steps among its first stages.
         const int nrk0 = MODE == MODE_RIDE ? (int)((long)nk_all * nmt / p.m_full) - nkt0 : 0;
         const int nrk1 = MODE == MODE_RIDE ? (int)((long)nk_all * (nmt + 1) / p.m_full) - nkt0 : 0;
@@ -632,6 +771,9 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
         for (int s = 0; s < NS; ++s)
             if (s < nnk) issue_at(na, nw, nkt0, s, nheavy || (s >= nrk0 && s < nrk1));
     }
+    // A light tile finishes its chunk first: its accumulators are then free before the
+    // full rows' epilogue, which sets the register peak.
+    if constexpr (XR) light_epilogue<OutT, EPI>(p, lacc, xe, n0, wave, wm, wn, q16, r16, red);
     if constexpr (MODE == MODE_RIDE) {
         // The tail part: partial mt of tail column block nt.
         float* base = p.part + ((size_t)nt * p.split + mt) * 64 * BN;
@@ -767,8 +909,9 @@ template <typename T, typename OutT, int EPI, int MODE>
 __global__ void __launch_bounds__(512, 1) kernel(Params p)
 {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * Ring<MODE != MODE_PLAIN>::STAGE];
-    // Per-row partial sums of squares of the EPI_QKROPE epilogue: [wave][row group][16].
-    __shared__ float red[EPI == EPI_QKROPE ? 8 * 8 * 16 : 1];
+    // Per-row partial sums of squares of the EPI_QKROPE epilogue: [wave][row group][16],
+    // then a light chunk's [wave][16].
+    __shared__ float red[EPI == EPI_QKROPE ? 8 * 8 * 16 + 8 * 16 : 1];
     // Items blockIdx.x, + gridDim.x, ...: with gridDim.x a multiple of 8 every item of
     // a workgroup maps to the XCD its blockIdx.x runs on.
     int bid = blockIdx.x, mt, nt, part, li;
@@ -783,6 +926,11 @@ __global__ void __launch_bounds__(512, 1) kernel(Params p)
             else tile<T, OutT, EPI, 4, MODE>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
         } else if constexpr (MODE == MODE_RIDE) {
             tile<T, OutT, EPI, 4, MODE>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
+        } else if constexpr (MODE == MODE_LIGHT) {
+            const int xe = light_chunk(p, mt, nt);
+            const int nxe = nmt >= 0 ? light_chunk(p, nmt, nnt) : -1;
+            if (xe >= 0) tile<T, OutT, EPI, 4, MODE, 1>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red, xe, nxe);
+            else tile<T, OutT, EPI, 4, MODE, 0>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red, -1, nxe);
         } else {
             if (mt < p.m_full) tile<T, OutT, EPI, 4, MODE>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
             else if (p.tail_sub == 1) tile<T, OutT, EPI, 1, MODE>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
@@ -813,6 +961,37 @@ static int cu_count()
 
 // Q / K heads must not straddle a 256-column tile.
 constexpr int BN_QK = 256;
+
+// Light tiles of a launch with p.light set, walked as the kernel walks its items
+// (workgroup b takes items b, b + grid, ...): true when every (chunk, column block) is
+// carried by exactly one tile and no workgroup carries more than its even share,
+// rounded up. The last few shapes are remembered per thread.
+static bool light_spread_ok(const pingpong::Params& p, int grid)
+{
+    struct Entry { int m_full, n_tiles, light_c, grid; bool ok; };
+    thread_local Entry cache[8];
+    thread_local int next = 0;
+    for (const Entry& e : cache)
+        if (e.grid && e.m_full == p.m_full && e.n_tiles == p.n_tiles && e.light_c == p.light_c && e.grid == grid)
+            return e.ok;
+    std::vector<int> per_wg(grid, 0), seen((size_t)p.light_c * p.n_tiles, 0);
+    int total = 0;
+    bool ok = true;
+    for (int b = 0; b < p.items && ok; ++b) {
+        int mt, nt, part, li;
+        pingpong::tile_of(p, b, mt, nt, part, li);
+        const int e = pingpong::light_chunk(p, mt, nt);
+        if (e < 0) continue;
+        ok = ++seen[(size_t)e * p.n_tiles + nt] == 1;
+        ++per_wg[b % grid];
+        ++total;
+    }
+    ok = ok && total == p.light_c * p.n_tiles &&
+         *std::max_element(per_wg.begin(), per_wg.end()) <= (total + grid - 1) / grid;
+    cache[next] = Entry{p.m_full, p.n_tiles, p.light_c, grid, ok};
+    next = (next + 1) % 8;
+    return ok;
+}
 
 int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
 {
@@ -871,17 +1050,44 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     p.heavy = 0;
     p.m_main = p.m_full;
     const int m_tiles = p.m_full + (p.tail_sub ? 1 : 0);
-    // A tail of at most 64 rows under at least two rounds of full tiles (the block's
-    // up/gate projection at 4096 image + 64 text tokens): the last row of full tiles
-    // takes the tail rows as 320-row tiles, one per workgroup in the last round, which
-    // then ends a quarter of a tile later instead of being followed by a tail phase and
-    // a reduction launch. (The Q/K epilogue would not fit 320 rows in registers.)
-    if (a.epilogue == EPI_GEGLU && p.tail_sub == 1 && p.m_full >= 1 &&
+    const int full = p.m_full * p.n_tiles;
+    // A tail of at most 64 rows under whole rounds of full tiles, with an epilogue that
+    // finishes rows within the tile (the block's Q/K/V projection with the Q/K norm and
+    // rotary at 4096 image + 64 text tokens): light tiles (Params::light). Each adds 16
+    // tail rows, a sixteenth more MFMAs, and no workgroup gets more than its share of
+    // them, so the launch ends about a sixteenth of a tile later per light tile a
+    // workgroup carries, with no tail phase streaming all of W for 64 rows and no
+    // reduction launch. Measured on the block's Q/K/V GEMM: 370 -> 358 us against the
+    // split tail. A GLU epilogue over two or more rounds takes the heavy last row
+    // instead: light tiles, two per workgroup on half of them, measured 636 -> 643 us on
+    // the up/gate GEMM.
+    p.light = 0;
+    p.light_c = 0;
+    {
+        const int tail_rows = a.M % pingpong::BM, chunks = (tail_rows + 15) / 16;
+        const bool heavy_fits = a.epilogue == EPI_GEGLU && full >= 2 * cu_count();
+        if ((qk || (epi_glu(a.epilogue) && !heavy_fits) || a.epilogue == EPI_STORE) && tail_rows > 0 &&
+            tail_rows <= 64 && full >= cu_count() && full % cu_count() == 0 && p.m_full >= pingpong::GM * chunks) {
+            p.light = 1;
+            p.light_c = chunks;
+            p.items = full;
+            if (!light_spread_ok(p, cu_count())) {
+                p.light = 0;
+                p.light_c = 0;
+            }
+        }
+    }
+    // A tail of at most 64 rows under at least two rounds of full tiles, when light
+    // tiles do not apply: the last row of full tiles takes the tail rows as 320-row
+    // tiles, one per workgroup in the last round, which then ends a quarter of a tile
+    // later instead of being followed by a tail phase and a reduction launch. (The Q/K
+    // epilogue would not fit 320 rows in registers.)
+    if (!p.light && a.epilogue == EPI_GEGLU && p.tail_sub == 1 && p.m_full >= 1 &&
         (long)p.m_full * p.n_tiles >= 2L * cu_count()) {
         p.heavy = 1;
         p.m_main = p.m_full - 1;
     }
-    if (!p.heavy && a.split_ws && p.m_full && m_tiles * p.n_tiles <= kSplitTargetItems / 2) {
+    if (!p.heavy && !p.light && a.split_ws && p.m_full && m_tiles * p.n_tiles <= kSplitTargetItems / 2) {
         // Too few tiles for the CUs (a short sequence's narrow projections): split
         // every tile along K, at least 4 K steps per part.
         const size_t per_part = (size_t)m_tiles * p.n_tiles * pingpong::BM * pingpong::BN * sizeof(float);
@@ -899,8 +1105,7 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     // m_full K ranges of it, one per row of full tiles. (The Q/K/V projection keeps its
     // 5-part split tail: with 16 parts its reduction would read three times as much.)
     p.ride = 0;
-    const int full = p.m_full * p.n_tiles;
-    if (!p.heavy && !p.split_all && a.split_ws && a.epilogue == EPI_GATE_RESID &&
+    if (!p.heavy && !p.light && !p.split_all && a.split_ws && a.epilogue == EPI_GATE_RESID &&
         p.tail_sub == 1 && p.m_full >= 2 && p.m_full <= kMaxSplit && a.K / pingpong::BK >= p.m_full &&
         full >= cu_count() && full % cu_count() == 0 &&
         (size_t)p.m_full * p.n_tiles * 64 * pingpong::BN * sizeof(float) <= a.split_ws_bytes) {
@@ -908,7 +1113,7 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
         p.split = p.m_full;
         p.part = static_cast<float*>(a.split_ws);
     }
-    if (!p.heavy && !p.ride && !p.split_all && p.tail_sub && a.split_ws) {
+    if (!p.heavy && !p.ride && !p.light && !p.split_all && p.tail_sub && a.split_ws) {
         const size_t per_part = (size_t)p.n_tiles * 64 * p.tail_sub * pingpong::BN * sizeof(float);
         int sp = std::min(kMaxSplit, std::max(1, kSplitTargetItems / p.n_tiles));
         sp = std::min(sp, std::max(1, a.K / pingpong::BK / 4));
@@ -924,7 +1129,7 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     p.late_part = nullptr;
     const int last_round = full % kSplitTargetItems;
     // (Not for the fused Q/K epilogue, whose rows are finished per tile.)
-    if (!qk && !p.heavy && !p.ride && !p.split_all && a.split_ws && full > kSplitTargetItems &&
+    if (!qk && !p.heavy && !p.ride && !p.light && !p.split_all && a.split_ws && full > kSplitTargetItems &&
         last_round <= kSplitTargetItems / 2 && last_round > 0) {
         const size_t tail_bytes =
             p.tail_sub ? ((size_t)p.split * p.n_tiles * 64 * p.tail_sub * pingpong::BN * sizeof(float) + 255) / 256 * 256 : 0;
@@ -939,7 +1144,7 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
         }
     }
     const int tiles = p.split_all ? m_tiles * p.n_tiles * p.split
-                      : p.heavy || p.ride ? full
+                      : p.heavy || p.ride || p.light ? full
                                   : full - p.late + p.late * p.late_split + (p.tail_sub ? p.n_tiles * p.split : 0);
     // One workgroup per CU (the LDS ring allows no second), each walking its items.
     p.items = tiles;
@@ -950,7 +1155,18 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     const int epi = qk && p.split_all ? EPI_STORE : a.epilogue;
 #define EHIP_PINGPONG(T)                                                                                            \
     do {                                                                                                      \
-        if (p.heavy) {                                                                                        \
+        if (p.light) {                                                                                        \
+            if (epi == EPI_QKROPE)                                                                            \
+                hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_QKROPE, pingpong::MODE_LIGHT>), grid, block, 0, s, p); \
+            else if (epi == EPI_STORE && a.c_dtype == DT_F32)                                                 \
+                hipLaunchKernelGGL((pingpong::kernel<T, float, EPI_STORE, pingpong::MODE_LIGHT>), grid, block, 0, s, p); \
+            else if (epi == EPI_STORE)                                                                        \
+                hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_STORE, pingpong::MODE_LIGHT>), grid, block, 0, s, p); \
+            else if (epi == EPI_SWIGLU)                                                                       \
+                hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_SWIGLU, pingpong::MODE_LIGHT>), grid, block, 0, s, p); \
+            else                                                                                              \
+                hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_GEGLU, pingpong::MODE_LIGHT>), grid, block, 0, s, p); \
+        } else if (p.heavy) {                                                                                 \
             hipLaunchKernelGGL((pingpong::kernel<T, T, EPI_GEGLU, pingpong::MODE_HEAVY>), grid, block, 0, s, p);    \
         } else if (p.ride) {                                                                                  \
             hipLaunchKernelGGL((pingpong::kernel<T, float, EPI_GATE_RESID, pingpong::MODE_RIDE>), grid, block, 0, s, p); \

@@ -64,7 +64,7 @@ def test_block_heavy_tail_tiles_against_oracle(ctx, dt):
     # 40 text slots, 30 valid). The up/gate GEMM has 16 x 32 = 512 full tiles, two
     # rounds of 256 workgroups, so its last row of tiles takes the 40 tail rows as
     # 320-row tiles (rows past S are computed and not stored) instead of a split tail
-    # row; the other GEMMs keep their split tails.
+    # row; the other GEMMs have too few tiles for that and keep their split tails.
     dim, ffn = 1024, 4096
     w = small_block(dim=dim, ffn=ffn, seed=11)
     x, mods, cos, sin, mask = small_inputs(S=4136, dim=dim, image=(64, 64), valid=30, seed=12)
@@ -76,6 +76,25 @@ def test_block_heavy_tail_tiles_against_oracle(ctx, dt):
     assert g["passed"], g
     np.testing.assert_array_equal(run_block(ctx, 6, x, mods, cos, sin, mask, valid), got)  # repeat-deterministic
     ctx.call("block_release", 6)
+
+
+@pytest.mark.parametrize("dt", [E.FP16, E.BF16], ids=lambda d: NAMES[d])
+def test_block_light_tail_tiles_against_oracle(ctx, dt):
+    # Width 1024, FFN 2048, S = 4136 = 16 x 256 + 40. The up/gate GEMM has 16 x 16 = 256
+    # full tiles, one round: the 40 tail rows go as three 16-row chunks (the last one
+    # 8 rows past S) into 48 of those tiles, at most one per workgroup, with the GEGLU
+    # epilogue applied to each chunk in the tile that computed it.
+    dim, ffn = 1024, 2048
+    w = small_block(dim=dim, ffn=ffn, seed=13)
+    x, mods, cos, sin, mask = small_inputs(S=4136, dim=dim, image=(64, 64), valid=30, seed=14)
+    ctx.block_upload(7, w, dim, ffn, dt)
+    valid = int(np.sum(mask == 0))
+    got = run_block(ctx, 7, x, mods, cos, sin, mask, valid)
+    ref = O.block_forward(w, x, mods, cos, sin, mask)
+    g = kat.gate(got, ref, *kat.BLOCK_GATES[NAMES[dt]])
+    assert g["passed"], g
+    np.testing.assert_array_equal(run_block(ctx, 7, x, mods, cos, sin, mask, valid), got)  # repeat-deterministic
+    ctx.call("block_release", 7)
 
 
 _CONFIG0_MODS = []

@@ -71,7 +71,8 @@ def test_full_width_block_short_tail_against_oracle(ctx, dt):
     # takes it on its last row of tiles (320-row tiles, 40 rows past S computed and not
     # stored); the output and down GEMMs compute it inside their full tiles, one K range
     # per row of tiles (tail rows past S read A rows that are never stored either); the
-    # Q/K/V GEMM splits it into K parts.
+    # Q/K/V GEMM computes it as two 16-row chunks inside 96 of its full tiles, with the
+    # Q/K norm and rotary applied there (8 rows past S computed and not stored).
     text_slots, valid_text = 24, 16
     S24 = GRID * GRID + text_slots
     w = small_block(DIM, FFN, seed=3)

@@ -78,8 +78,12 @@ def test_gemm_exact_products_kat(ctx, dt, name, m, n, k, bias):
 
 
 @pytest.mark.parametrize("dt", ALL_DT, ids=lambda d: NAMES[d])
-@pytest.mark.parametrize("m,n,k", [(300, 520, 256), (4160, 256, 512), (33, 4096, 128), (1056, 96, 4096)])
+@pytest.mark.parametrize("m,n,k", [(300, 520, 256), (4160, 256, 512), (33, 4096, 128), (1056, 96, 4096),
+                                   (4160, 4096, 256), (4120, 4096, 256)])
 def test_gemm_random_against_oracle(ctx, dt, m, n, k):
+    # 4160 / 4120 x 4096: 256 full tiles and a 64- or 24-row tail row; the 16-bit kernel
+    # computes the tail in 16-row chunks inside full tiles (light tiles), one per
+    # workgroup at most.
     a = O.normal((m, k), 1)
     w = O.normal((n, k), 2, std=0.02)
     a_s, w_s = stored(a, dt), stored(w, dt)
