@@ -28,16 +28,18 @@
 //     block's GEMMs read (RMSNorm, attention and GEGLU outputs) are stored this way.
 //   * Workgroup b runs on XCD b % 8: each XCD gets a contiguous range of tiles
 //     (4 M tiles per N sweep, sharing its own L2), and the tail row of tiles last.
-//   * A tail row (M % 256 rows) is computed one of three ways. Split: its tiles are
+//   * A tail row (M % 256 rows) is computed one of four ways. Split: its tiles are
 //     cut along K into parts that fill the CUs and a reduction launch adds them.
 //     Heavy (Params::heavy): the last row of full tiles is 320 rows tall. Riding
 //     (Params::ride): every full tile computes one K range of the tail rows below
-//     it. The last two reuse the W rows already in LDS instead of streaming all of W
-//     again for at most 64 rows.
+//     it. Light (Params::light): a 16- or 32-row chunk of the tail rows rides along
+//     all of K in some full tiles, at most one per workgroup. The last three reuse the W rows
+//     already in LDS instead of streaming all of W again for at most 64 rows.
 #include "common.hpp"
 #include "kernels.hpp"
 
 #include <algorithm>
+#include <cstring>
 #include <vector>
 
 namespace ehip {
@@ -53,8 +55,8 @@ constexpr int BM = 256, BN = 256, BK = 32, NS = 4;
 constexpr int ROWB = BK * 2;                // 64 bytes per staged row
 // Launch modes: plain; heavy (Params::heavy: the last row of full tiles is 320 rows
 // tall); ride (Params::ride: every full tile also computes one K range of the tail
-// rows); light (Params::light: some full tiles also compute 16 of the tail rows over
-// all of K). Heavy, ride and light launches keep room for 320 A rows in every stage.
+// rows); light (Params::light: some full tiles also compute 16 or 32 of the tail rows
+// over all of K). Heavy, ride and light launches keep room for 320 A rows in every stage.
 enum { MODE_PLAIN = 0, MODE_HEAVY = 1, MODE_RIDE = 2, MODE_LIGHT = 3 };
 // Stage layout: the A rows of the stage, then the W rows.
 template <bool HV> struct Ring {
@@ -80,12 +82,14 @@ struct Params {
     // partial `mt` of `split` = m_full (the tail-row partial layout below), so there
     // is no tail phase that streams all of W again for 64 rows.
     int ride;
-    // light: the tail rows (M % 256 <= 64) are cut into light_c chunks of 16 rows; for
-    // each column block nt, chunk e is computed over all of K by one full tile of M
-    // group e (light_chunk), as 16 more rows while it holds W. The host enables it only
-    // when those tiles fall at most ceil(light tiles / grid) to a workgroup, so the
-    // extra sixteenth of a tile is spread over the CUs: no tail phase, no reduction.
-    int light, light_c;
+    // light: the tail rows (M % 256 <= 64) are cut into light_c chunks of light_h (16 or
+    // 32) rows; for each column block nt, chunk e is computed over all of K by the full
+    // tile (light_mt[e][nt], nt), as light_h more rows while it holds W. The host picks
+    // those tiles so that no workgroup carries more than ceil(light tiles / grid) of
+    // them: the extra MFMAs (a sixteenth or an eighth of a tile each) are spread over
+    // the CUs, with no tail phase and no reduction.
+    int light, light_c, light_h;
+    uint8_t light_mt[4][128];
     void* C; long ldc;
     const float* bias;
     const float* resid; long ld_resid;
@@ -136,17 +140,15 @@ __host__ __device__ __forceinline__ void full_order(const Params& p, int f, int&
     nt = in_group / gm;
 }
 
-// Light tiles: the tail chunk (rows m_full * 256 + 16 e .. + 15) that full tile (mt, nt)
-// also computes, or -1. Chunk e of column block nt belongs to M group e (M tiles
-// 4e .. 4e + 3, all full when m_full >= 4 light_c), at the group offset
-// (nt / 8 + e) mod 4: one tile per (chunk, column block), and along the tile order the
-// offset changes every 8 column blocks, which spreads the light tiles over the
-// workgroups (the host checks the spread for each launch shape).
+// Light tiles: the tail chunk (rows m_full * 256 + light_h e .. + light_h - 1) that full
+// tile (mt, nt) also computes, or -1.
 __host__ __device__ __forceinline__ int light_chunk(const Params& p, int mt, int nt)
 {
-    const int e = mt / GM;
-    if (!p.light || e >= p.light_c) return -1;
-    return mt - e * GM == (nt / 8 + e) % GM ? e : -1;
+    if (!p.light) return -1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        if (e < p.light_c && p.light_mt[e][nt] == mt) return e;
+    return -1;
 }
 
 // The epilogue of a reduced element: row m, output column c (GEGLU / SwiGLU: of
@@ -469,19 +471,23 @@ __device__ __forceinline__ void qk_rope_epilogue(const Params& p, const f32x4 (&
     }
 }
 
-// Epilogue of a light tile's tail chunk e: output row m_full * 256 + 16 e + r16. The
-// wave holds the chunk's columns 16 j + 4 q16 + r of its 64 for j = wm (lacc[0]) and
-// j = wm + 2 (lacc[1]), the pairs that the GLU epilogues (up, gate) and the Q/K
-// epilogue (dimension, rotary partner) combine in one lane. A Q or K head's 128
-// columns then lie in the four waves 4 h .. 4 h + 3; each row's sum of squares is
-// added over them through `red` in one fixed order, so all four use the same value.
-template <typename OutT, int EPI>
-__device__ __forceinline__ void light_epilogue(const Params& p, const f32x4 (&lacc)[2], int chunk, int n0, int wave,
-                                               int wm, int wn, int q16, int r16, float* red)
+// Epilogue of a light tile's tail chunk e. XR = 1 (16-row chunks): output row
+// m_full * 256 + 16 e + r16, and the wave holds the chunk's columns 16 j + 4 q16 + r of
+// its 64 for j = wm (lacc[0]) and j = wm + 2 (lacc[1]), the pairs that the GLU epilogues
+// (up, gate) and the Q/K epilogue (dimension, rotary partner) combine in one lane; a
+// Q or K head's 128 columns then lie in the four waves 4 h .. 4 h + 3, and each row's
+// sum of squares is added over them through `red` in one fixed order, so all four use
+// the same value. XR = 2 (32-row chunks, GLU only): output row
+// m_full * 256 + 32 e + 16 wm + r16 and all four column blocks j in lacc[j], as in a
+// full tile's row group.
+template <typename OutT, int EPI, int XR>
+__device__ __forceinline__ void light_epilogue(const Params& p, const f32x4 (&lacc)[2 * XR], int chunk, int n0,
+                                               int wave, int wm, int wn, int q16, int r16, float* red)
 {
     typedef OutT out4 __attribute__((ext_vector_type(4)));
-    const int m = p.m_full * BM + 16 * chunk + r16;
+    const int m = p.m_full * BM + p.light_h * chunk + (XR == 2 ? 16 * wm : 0) + r16;
     if constexpr (EPI == EPI_QKROPE) {
+        static_assert(XR == 1, "the Q/K epilogue takes 16-row chunks");
         if (n0 < p.qk_cols) {
             const int head_col = n0 + 128 * (wn >> 1);
             const float* g = head_col >= p.k_col ? p.gk : p.gq;
@@ -525,22 +531,26 @@ __device__ __forceinline__ void light_epilogue(const Params& p, const f32x4 (&la
         // V columns: stored as they are, below.
     }
     if (m >= p.M) return;
+    // Column block of lacc[x] (and, for GLU, of its gate partner lacc[x + XR]).
+    auto jb = [&](int x) { return XR == 1 ? wm + 2 * x : x; };
     if constexpr (epi_glu(EPI)) {
         if (n0 + wn * 64 >= p.N) return;
-        OutT* c = static_cast<OutT*>(p.C) + (size_t)m * p.c_rs + (size_t)((n0 + wn * 64) >> 6) * p.c_ss + 4 * q16 +
-                  16 * wm;
-        out4 o;
+        OutT* c = static_cast<OutT*>(p.C) + (size_t)m * p.c_rs + (size_t)((n0 + wn * 64) >> 6) * p.c_ss + 4 * q16;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o[r] = OutT(lacc[0][r] * glu_act<EPI == EPI_SWIGLU>(lacc[1][r]));
-        if (p.vec) *reinterpret_cast<out4*>(c) = o;
-        else
+        for (int x = 0; x < XR; ++x) {
+            out4 o;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) c[r] = o[r];
+            for (int r = 0; r < 4; ++r) o[r] = OutT(lacc[x][r] * glu_act<EPI == EPI_SWIGLU>(lacc[x + XR][r]));
+            if (p.vec) *reinterpret_cast<out4*>(c + 16 * jb(x)) = o;
+            else
+#pragma unroll
+                for (int r = 0; r < 4; ++r) c[16 * jb(x) + r] = o[r];
+        }
     } else {
         static_assert(EPI != EPI_GATE_RESID, "light tiles take no gate + residual epilogue");
 #pragma unroll
-        for (int x = 0; x < 2; ++x) {
-            const int n = n0 + wn * 64 + 4 * q16 + 16 * (wm + 2 * x);
+        for (int x = 0; x < 2 * XR; ++x) {
+            const int n = n0 + wn * 64 + 4 * q16 + 16 * (XR == 1 ? wm + 2 * x : x);
             if (n >= p.N) continue;
             OutT* c = static_cast<OutT*>(p.C) + (size_t)m * p.ldc + n;
             if (p.vec) {
@@ -563,7 +573,8 @@ __device__ __forceinline__ void light_epilogue(const Params& p, const f32x4 (&la
 // One work item. `pre`: its first NS stages were requested by the previous item of this
 // workgroup. nmt >= 0 names the next item (nmt, nnt, npart, nli), whose first NS stages
 // this one requests once its own ring is drained, before its epilogue. XR: this item is
-// a light tile carrying tail chunk xe; nxe: the next item's chunk (or -1).
+// a light tile carrying tail chunk xe of 16 (XR = 1) or 32 (XR = 2) rows; nxe: the next
+// item's chunk (or -1).
 template <typename T, typename OutT, int EPI, int MSUB, int MODE, int XR = 0>
 __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, int li, uint8_t* smem, bool pre,
                                      int nmt, int nnt, int npart, int nli, float* red, int xe = -1, int nxe = -1)
@@ -587,8 +598,8 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
     // with two 1-KiB instructions each; lane l lands at bytes [16l, 16l+16), i.e.
     // row (l >> 2), physical chunk l & 3 = logical chunk (l & 3) ^ fsw(row). The tail
     // rows of a heavy or riding tile (stage rows 256 + 8w .. + 7) come from a third
-    // instruction of lanes 0-31; the 16 chunk rows of a light tile (stage rows
-    // 256 + 2w, + 1) from a third instruction of lanes 0-7.
+    // instruction of lanes 0-31; the chunk rows of a light tile (stage rows
+    // 256 + h w .. + h - 1, h = light_h / 8) from a third instruction of lanes 0 .. 4h - 1.
     uint32_t a_src[3], w_src[2];
     auto sources = [&](int m_0, int n_0, uint32_t* as, uint32_t* ws, int chunk) {
 #pragma unroll
@@ -599,8 +610,9 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
             ws[q] = (uint32_t)((long)(n_0 + row) * p.w_row_bytes + c * 16);
         }
         if constexpr (MODE == MODE_LIGHT) {
-            const int row = BM + wave * 2 + (lane >> 2);
-            const int src = p.m_full * BM + 16 * max(chunk, 0) + wave * 2 + (lane >> 2);
+            const int h = p.light_h >> 3;
+            const int row = BM + wave * h + (lane >> 2);
+            const int src = p.m_full * BM + p.light_h * max(chunk, 0) + wave * h + (lane >> 2);
             as[2] = (uint32_t)((long)src * p.a_row_bytes + (((lane & 3) ^ fsw(row)) << 4));
         } else if constexpr (HV) {
             const int row = BM + wave * 8 + (lane >> 2);
@@ -626,9 +638,9 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
                                                      16, ws[q], koff_w, 0, 0);
         }
         if constexpr (MODE == MODE_LIGHT) {
-            if (heavy_item && lane < 8)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(st + (BM + wave * 2) * ROWB), 16, as[2], koff,
-                                                         0, 0);
+            if (heavy_item && lane < (p.light_h >> 1))
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(st + (BM + wave * (p.light_h >> 3)) * ROWB), 16,
+                                                         as[2], koff, 0, 0);
         } else if constexpr (HV) {
             if (heavy_item && lane < 32)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(st + (BM + wave * 8) * ROWB), 16, as[2], koff,
@@ -667,12 +679,13 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) tacc[i][j][r] = 0.f;
-    // Light tile: the chunk's fragment (stage rows 256 .. 271) and its accumulators for
-    // this wave's column blocks j = wm and wm + 2.
-    f32x4 lacc[2];
+    // Light tile: this wave's chunk fragment (stage rows 256 .. 271, or 256 + 16 wm ..
+    // + 15 for 32-row chunks) and its accumulators: column blocks j = wm and wm + 2, or
+    // all four.
+    f32x4 lacc[XR ? 2 * XR : 1];
     vec8 lf;
 #pragma unroll
-    for (int x = 0; x < 2; ++x)
+    for (int x = 0; x < (XR ? 2 * XR : 1); ++x)
 #pragma unroll
         for (int r = 0; r < 4; ++r) lacc[x][r] = 0.f;
     // Memory cluster: this wave's fragments of stage kt into registers.
@@ -688,7 +701,8 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
 #pragma unroll
             for (int i = 0; i < TR; ++i)
                 tf[i] = *reinterpret_cast<const vec8*>(st + (BM + wm * 32 + i * 16) * ROWB + frag);
-        if constexpr (XR) lf = *reinterpret_cast<const vec8*>(st + BM * ROWB + frag);
+        if constexpr (XR == 1) lf = *reinterpret_cast<const vec8*>(st + BM * ROWB + frag);
+        if constexpr (XR == 2) lf = *reinterpret_cast<const vec8*>(st + (BM + 16 * wm) * ROWB + frag);
     };
     // MFMA cluster on the registers of stage kt.
     auto mfma_cluster = [&](int kt) {
@@ -701,12 +715,15 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
             for (int i = 0; i < TR; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) tacc[i][j] = Mfma<T>::run(bf[j], tf[i], tacc[i][j]);
-        if constexpr (XR) {
+        if constexpr (XR == 1) {
             // Column blocks wm and wm + 2, selected without a branch in the cluster.
             const vec8 b0 = wm ? bf[1] : bf[0], b1 = wm ? bf[3] : bf[2];
             lacc[0] = Mfma<T>::run(b0, lf, lacc[0]);
             lacc[1] = Mfma<T>::run(b1, lf, lacc[1]);
         }
+        if constexpr (XR == 2)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) lacc[j] = Mfma<T>::run(bf[j], lf, lacc[j]);
     };
     // Loads requested after stage s, per wave, when s must have landed: LPS x min(NS-2, nk-1-s).
     // A riding item's window stages carry a fifth load; counting four for every stage
@@ -773,7 +790,7 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
     }
     // A light tile finishes its chunk first: its accumulators are then free before the
     // full rows' epilogue, which sets the register peak.
-    if constexpr (XR) light_epilogue<OutT, EPI>(p, lacc, xe, n0, wave, wm, wn, q16, r16, red);
+    if constexpr (XR) light_epilogue<OutT, EPI, XR>(p, lacc, xe, n0, wave, wm, wn, q16, r16, red);
     if constexpr (MODE == MODE_RIDE) {
         // The tail part: partial mt of tail column block nt.
         float* base = p.part + ((size_t)nt * p.split + mt) * 64 * BN;
@@ -811,9 +828,11 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
     }
     if constexpr (EPI == EPI_GATE_RESID) {
         // C = resid + gate * acc, C possibly aliasing resid. Each element is read and
-        // written by this lane only, so the gate values and a 32-row block's residuals
-        // are loaded before any of the block's stores: 8 loads of 16 bytes in flight
-        // per lane instead of one load-wait-store round trip per element.
+        // written by this lane only, so a 32-row block's residuals (8 loads of 16 bytes
+        // per lane) are requested before the previous block's stores. Stores and loads
+        // share one in-order counter, so a load requested after a store could only be
+        // waited for together with that store's write acknowledgement; requested one
+        // block ahead, each block's wait leaves the previous block's stores in flight.
         float* C = static_cast<float*>(p.C);
         if (p.vec) {
             f32x4 gv[4];
@@ -822,17 +841,23 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
                 const int n = col_w + 16 * j;
                 gv[j] = n < p.N ? *reinterpret_cast<const f32x4*>(p.gate + n) : f32x4{0.f, 0.f, 0.f, 0.f};
             }
-#pragma unroll
-            for (int i2 = 0; i2 < MSUB; ++i2) {
-                f32x4 rv[2][4];
+            f32x4 rv[2][2][4];
+            // Whole tile inside M x N (every tile but the tail row's, N a multiple of 256):
+            // no per-element bounds, so no branches, and the wait before each block's
+            // stores counts only the loads it needs.
+            const bool whole = m0 + 64 * MSUB <= p.M && n0 + BN <= p.N;
+            auto load_block = [&](int i2, f32x4 (&dst)[2][4]) {
 #pragma unroll
                 for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         const int m = row_w + 16 * (2 * i2 + ii), n = col_w + 16 * j;
-                        rv[ii][j] = m < p.M && n < p.N ? *reinterpret_cast<const f32x4*>(p.resid + (size_t)m * p.ld_resid + n)
-                                                       : f32x4{0.f, 0.f, 0.f, 0.f};
+                        dst[ii][j] = whole || (m < p.M && n < p.N)
+                                         ? *reinterpret_cast<const f32x4*>(p.resid + (size_t)m * p.ld_resid + n)
+                                         : f32x4{0.f, 0.f, 0.f, 0.f};
                     }
+            };
+            auto store_block = [&](int i2, const f32x4 (&src)[2][4]) {
 #pragma unroll
                 for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
@@ -840,9 +865,24 @@ __device__ __forceinline__ void tile(const Params& p, int mt, int nt, int part, 
                         const int m = row_w + 16 * (2 * i2 + ii), n = col_w + 16 * j;
                         f32x4 o;
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) o[r] = __builtin_fmaf(gv[j][r], acc[2 * i2 + ii][j][r], rv[ii][j][r]);
-                        if (m < p.M && n < p.N) *reinterpret_cast<f32x4*>(C + (size_t)m * p.ldc + n) = o;
+                        for (int r = 0; r < 4; ++r) o[r] = __builtin_fmaf(gv[j][r], acc[2 * i2 + ii][j][r], src[ii][j][r]);
+                        if (whole || (m < p.M && n < p.N)) *reinterpret_cast<f32x4*>(C + (size_t)m * p.ldc + n) = o;
                     }
+            };
+            if (whole) {
+                load_block(0, rv[0]);
+#pragma unroll
+                for (int i2 = 0; i2 < MSUB; ++i2) {
+                    if (i2 + 1 < MSUB) load_block(i2 + 1, rv[(i2 + 1) & 1]);
+                    store_block(i2, rv[i2 & 1]);
+                }
+            } else {
+                load_block(0, rv[0]);
+#pragma unroll
+                for (int i2 = 0; i2 < MSUB; ++i2) {
+                    if (i2 + 1 < MSUB) load_block(i2 + 1, rv[(i2 + 1) & 1]);
+                    store_block(i2, rv[i2 & 1]);
+                }
             }
         } else {
 #pragma unroll
@@ -929,8 +969,14 @@ __global__ void __launch_bounds__(512, 1) kernel(Params p)
         } else if constexpr (MODE == MODE_LIGHT) {
             const int xe = light_chunk(p, mt, nt);
             const int nxe = nmt >= 0 ? light_chunk(p, nmt, nnt) : -1;
-            if (xe >= 0) tile<T, OutT, EPI, 4, MODE, 1>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red, xe, nxe);
-            else tile<T, OutT, EPI, 4, MODE, 0>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red, -1, nxe);
+            if (xe < 0) {
+                tile<T, OutT, EPI, 4, MODE, 0>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red, -1, nxe);
+            } else if constexpr (epi_glu(EPI)) {
+                if (p.light_h == 32) tile<T, OutT, EPI, 4, MODE, 2>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red, xe, nxe);
+                else tile<T, OutT, EPI, 4, MODE, 1>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red, xe, nxe);
+            } else {
+                tile<T, OutT, EPI, 4, MODE, 1>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red, xe, nxe);
+            }
         } else {
             if (mt < p.m_full) tile<T, OutT, EPI, 4, MODE>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
             else if (p.tail_sub == 1) tile<T, OutT, EPI, 1, MODE>(p, mt, nt, part, li, smem, pre, nmt, nnt, npart, nli, red);
@@ -962,33 +1008,79 @@ static int cu_count()
 // Q / K heads must not straddle a 256-column tile.
 constexpr int BN_QK = 256;
 
-// Light tiles of a launch with p.light set, walked as the kernel walks its items
-// (workgroup b takes items b, b + grid, ...): true when every (chunk, column block) is
-// carried by exactly one tile and no workgroup carries more than its even share,
-// rounded up. The last few shapes are remembered per thread.
-static bool light_spread_ok(const pingpong::Params& p, int grid)
+// Chooses the light tiles of a launch with p.light set (p.light_mt), walking the
+// kernel's items as the kernel walks them (workgroup b takes items b, b + grid, ...).
+// First choice, a fixed pattern: chunk e of column block nt goes to M tile
+// 4 e + (nt / 8 + e) mod 4 (M group e of the tile order, the offset turning every 8
+// column blocks), taken when no workgroup then carries more than its even share,
+// rounded up. Otherwise each (chunk, column block) goes to the tile of that column whose
+// workgroup, then whose XCD (b % 8), carries the fewest light tiles so far, then the
+// lowest M tile, never to a tile that already carries a chunk. (On the Q/K/V GEMM at
+// 4160 tokens the pattern measured 344 us, the greedy choice 348 us, 361 us without
+// its XCD term, which filled six XCDs and left two without light tiles; the up/gate
+// GEMM's two 32-row chunks cannot be spread by the pattern.) True when no workgroup
+// carries more than its share. The last few shapes' tables are remembered per thread.
+static bool light_assign(pingpong::Params& p, int grid)
 {
-    struct Entry { int m_full, n_tiles, light_c, grid; bool ok; };
+    struct Entry { int m_full, n_tiles, light_c, grid; bool ok; uint8_t mt[4][128]; };
     thread_local Entry cache[8];
     thread_local int next = 0;
     for (const Entry& e : cache)
-        if (e.grid && e.m_full == p.m_full && e.n_tiles == p.n_tiles && e.light_c == p.light_c && e.grid == grid)
+        if (e.grid && e.m_full == p.m_full && e.n_tiles == p.n_tiles && e.light_c == p.light_c && e.grid == grid) {
+            std::memcpy(p.light_mt, e.mt, sizeof p.light_mt);
             return e.ok;
-    std::vector<int> per_wg(grid, 0), seen((size_t)p.light_c * p.n_tiles, 0);
-    int total = 0;
-    bool ok = true;
-    for (int b = 0; b < p.items && ok; ++b) {
-        int mt, nt, part, li;
-        pingpong::tile_of(p, b, mt, nt, part, li);
-        const int e = pingpong::light_chunk(p, mt, nt);
-        if (e < 0) continue;
-        ok = ++seen[(size_t)e * p.n_tiles + nt] == 1;
-        ++per_wg[b % grid];
-        ++total;
+        }
+    bool ok = p.m_full <= 255 && p.n_tiles <= 128 && p.light_c <= 4;
+    std::memset(p.light_mt, 0xff, sizeof p.light_mt);
+    const int total = p.light_c * p.n_tiles, share = (total + grid - 1) / grid;
+    if (ok) {
+        std::vector<int> wg_of((size_t)p.m_full * p.n_tiles, -1), load(grid, 0), xcd_load(8, 0);
+        for (int b = 0; b < p.items; ++b) {
+            int mt, nt, part, li;
+            pingpong::tile_of(p, b, mt, nt, part, li);
+            wg_of[(size_t)mt * p.n_tiles + nt] = b % grid;
+        }
+        bool pattern = p.m_full >= pingpong::GM * p.light_c;
+        for (int nt = 0; nt < p.n_tiles && pattern; ++nt)
+            for (int e = 0; e < p.light_c && pattern; ++e) {
+                const int mt = pingpong::GM * e + (nt / 8 + e) % pingpong::GM;
+                const int w = wg_of[(size_t)mt * p.n_tiles + nt];
+                pattern = w >= 0 && ++load[w] <= share;
+                p.light_mt[e][nt] = (uint8_t)mt;
+            }
+        if (!pattern) {
+            std::fill(load.begin(), load.end(), 0);
+            std::memset(p.light_mt, 0xff, sizeof p.light_mt);
+            std::vector<char> taken((size_t)p.m_full * p.n_tiles, 0);
+            for (int nt = 0; nt < p.n_tiles && ok; ++nt)
+                for (int e = 0; e < p.light_c && ok; ++e) {
+                    int best = -1;
+                    for (int mt = 0; mt < p.m_full; ++mt) {
+                        const size_t t = (size_t)mt * p.n_tiles + nt;
+                        if (wg_of[t] < 0 || taken[t]) continue;
+                        if (best < 0) {
+                            best = mt;
+                            continue;
+                        }
+                        const int w = wg_of[t], bw = wg_of[(size_t)best * p.n_tiles + nt];
+                        if (load[w] < load[bw] || (load[w] == load[bw] && xcd_load[w % 8] < xcd_load[bw % 8]))
+                            best = mt;
+                    }
+                    ok = best >= 0;
+                    if (ok) {
+                        const size_t t = (size_t)best * p.n_tiles + nt;
+                        taken[t] = 1;
+                        ++load[wg_of[t]];
+                        ++xcd_load[wg_of[t] % 8];
+                        p.light_mt[e][nt] = (uint8_t)best;
+                    }
+                }
+            ok = ok && *std::max_element(load.begin(), load.end()) <= share;
+        }
     }
-    ok = ok && total == p.light_c * p.n_tiles &&
-         *std::max_element(per_wg.begin(), per_wg.end()) <= (total + grid - 1) / grid;
-    cache[next] = Entry{p.m_full, p.n_tiles, p.light_c, grid, ok};
+    Entry& slot = cache[next];
+    slot = Entry{p.m_full, p.n_tiles, p.light_c, grid, ok, {}};
+    std::memcpy(slot.mt, p.light_mt, sizeof p.light_mt);
     next = (next + 1) % 8;
     return ok;
 }
@@ -1053,27 +1145,32 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     const int full = p.m_full * p.n_tiles;
     // A tail of at most 64 rows under whole rounds of full tiles, with an epilogue that
     // finishes rows within the tile (the block's Q/K/V projection with the Q/K norm and
-    // rotary at 4096 image + 64 text tokens): light tiles (Params::light). Each adds 16
-    // tail rows, a sixteenth more MFMAs, and no workgroup gets more than its share of
-    // them, so the launch ends about a sixteenth of a tile later per light tile a
-    // workgroup carries, with no tail phase streaming all of W for 64 rows and no
-    // reduction launch. Measured on the block's Q/K/V GEMM: 370 -> 358 us against the
-    // split tail. A GLU epilogue over two or more rounds takes the heavy last row
-    // instead: light tiles, two per workgroup on half of them, measured 636 -> 643 us on
-    // the up/gate GEMM.
+    // rotary, and its up/gate projection, at 4096 image + 64 text tokens): light tiles
+    // (Params::light). Each adds a 16- or 32-row chunk of the tail, a sixteenth or an
+    // eighth more MFMAs, and no workgroup gets more than its share of them, so the
+    // launch ends that much later per light tile a workgroup carries, with no tail phase
+    // streaming all of W for 64 rows and no reduction launch. The Q/K/V GEMM takes
+    // 16-row chunks (192 light tiles, at most one per workgroup: 362 -> 347 us against
+    // the split tail). A GLU epilogue over two or more rounds takes 32-row chunks: the
+    // up/gate GEMM then has 192 light tiles, at most one per workgroup, where 16-row
+    // chunks gave 384, two per workgroup on half of them (no faster than the heavy last
+    // row).
     p.light = 0;
     p.light_c = 0;
+    p.light_h = 16;
     {
-        const int tail_rows = a.M % pingpong::BM, chunks = (tail_rows + 15) / 16;
-        const bool heavy_fits = a.epilogue == EPI_GEGLU && full >= 2 * cu_count();
-        if ((qk || (epi_glu(a.epilogue) && !heavy_fits) || a.epilogue == EPI_STORE) && tail_rows > 0 &&
-            tail_rows <= 64 && full >= cu_count() && full % cu_count() == 0 && p.m_full >= pingpong::GM * chunks) {
+        const bool glu_rounds = epi_glu(a.epilogue) && full >= 2 * cu_count();
+        const int tail_rows = a.M % pingpong::BM, h = glu_rounds ? 32 : 16, chunks = (tail_rows + h - 1) / h;
+        if ((qk || epi_glu(a.epilogue) || a.epilogue == EPI_STORE) && tail_rows > 0 && tail_rows <= 64 &&
+            full >= cu_count() && full % cu_count() == 0 && p.m_full >= chunks) {
             p.light = 1;
             p.light_c = chunks;
+            p.light_h = h;
             p.items = full;
-            if (!light_spread_ok(p, cu_count())) {
+            if (!light_assign(p, cu_count())) {
                 p.light = 0;
                 p.light_c = 0;
+                p.light_h = 16;
             }
         }
     }

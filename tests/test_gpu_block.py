@@ -60,14 +60,14 @@ def test_block_last_round_split_against_oracle(ctx, dt):
 
 @pytest.mark.parametrize("dt", [E.FP16, E.BF16], ids=lambda d: NAMES[d])
 def test_block_heavy_tail_tiles_against_oracle(ctx, dt):
-    # Width 1024 (8 heads), FFN 4096, S = 4136 = 16 x 256 + 40 (64 x 64 image tokens,
-    # 40 text slots, 30 valid). The up/gate GEMM has 16 x 32 = 512 full tiles, two
-    # rounds of 256 workgroups, so its last row of tiles takes the 40 tail rows as
+    # Width 1024 (8 heads), FFN 4096, S = 5160 = 20 x 256 + 40 (64 x 80 image tokens,
+    # 40 text slots, 30 valid). The up/gate GEMM has 20 x 32 = 640 full tiles, two and a
+    # half rounds of 256 workgroups, so its last row of tiles takes the 40 tail rows as
     # 320-row tiles (rows past S are computed and not stored) instead of a split tail
     # row; the other GEMMs have too few tiles for that and keep their split tails.
     dim, ffn = 1024, 4096
     w = small_block(dim=dim, ffn=ffn, seed=11)
-    x, mods, cos, sin, mask = small_inputs(S=4136, dim=dim, image=(64, 64), valid=30, seed=12)
+    x, mods, cos, sin, mask = small_inputs(S=5160, dim=dim, image=(64, 80), valid=30, seed=12)
     ctx.block_upload(6, w, dim, ffn, dt)
     valid = int(np.sum(mask == 0))
     got = run_block(ctx, 6, x, mods, cos, sin, mask, valid)
@@ -78,13 +78,16 @@ def test_block_heavy_tail_tiles_against_oracle(ctx, dt):
     ctx.call("block_release", 6)
 
 
+@pytest.mark.parametrize("ffn", [2048, 4096])
 @pytest.mark.parametrize("dt", [E.FP16, E.BF16], ids=lambda d: NAMES[d])
-def test_block_light_tail_tiles_against_oracle(ctx, dt):
-    # Width 1024, FFN 2048, S = 4136 = 16 x 256 + 40. The up/gate GEMM has 16 x 16 = 256
-    # full tiles, one round: the 40 tail rows go as three 16-row chunks (the last one
-    # 8 rows past S) into 48 of those tiles, at most one per workgroup, with the GEGLU
-    # epilogue applied to each chunk in the tile that computed it.
-    dim, ffn = 1024, 2048
+def test_block_light_tail_tiles_against_oracle(ctx, dt, ffn):
+    # Width 1024, S = 4136 = 16 x 256 + 40. FFN 2048: the up/gate GEMM has 16 x 16 = 256
+    # full tiles, one round, and the 40 tail rows go as three 16-row chunks (the last one
+    # 8 rows past S) into 48 of those tiles. FFN 4096: 512 full tiles, two rounds, and
+    # the tail goes as two 32-row chunks (24 rows past S) into 64 tiles. Either way at
+    # most one chunk per workgroup, with the GEGLU epilogue applied to each chunk in the
+    # tile that computed it.
+    dim = 1024
     w = small_block(dim=dim, ffn=ffn, seed=13)
     x, mods, cos, sin, mask = small_inputs(S=4136, dim=dim, image=(64, 64), valid=30, seed=14)
     ctx.block_upload(7, w, dim, ffn, dt)

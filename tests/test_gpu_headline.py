@@ -68,8 +68,8 @@ def test_headline_block_against_oracle(ctx):
 @pytest.mark.parametrize("dt", [E.FP16, E.BF16], ids=lambda d: NAMES[d])
 def test_full_width_block_short_tail_against_oracle(ctx, dt):
     # Full width at S = 4096 + 24 text slots (16 valid): a 24-row tail. The up/gate GEMM
-    # takes it on its last row of tiles (320-row tiles, 40 rows past S computed and not
-    # stored); the output and down GEMMs compute it inside their full tiles, one K range
+    # computes it as one 32-row chunk inside 96 of its full tiles (8 rows past S computed
+    # and not stored); the output and down GEMMs compute it inside their full tiles, one K range
     # per row of tiles (tail rows past S read A rows that are never stored either); the
     # Q/K/V GEMM computes it as two 16-row chunks inside 96 of its full tiles, with the
     # Q/K norm and rotary applied there (8 rows past S computed and not stored).
