@@ -43,8 +43,13 @@
 
 namespace ehip {
 namespace {
-// Workgroup slots of an MI355X for this kernel: 256 CUs x 2.
-constexpr int kSdpaSlots = 512;
+// Key-range parts of a partial last query tile, summed over the heads: 192, i.e. 6
+// parts per head at 32 heads. The parts run in the slots the last full tiles leave
+// free as they finish unevenly; at 4096 image + 64 text tokens, 4, 6 and 8 parts per
+// head measured 290-291 us against 293-294 us for 16 (one per slot of the 256 CUs x 2),
+// whose shorter parts cost more in the merge and in per-part start-up than they save
+// at the end of the launch.
+constexpr int kSdpaSlots = 192;
 }
 namespace sdl {
 
@@ -613,7 +618,7 @@ int sdpa16_d128(const SdpaArgs& a, hipStream_t s)
     const float scale = a.scale > 0.f ? a.scale : 1.f / sqrtf(128.f);
     p.scale_log2 = scale * sdl::kLog2e;
     // A partial last query tile is split along the keys when a workspace is given:
-    // up to 16 parts per head, aiming at one workgroup per CU slot (two per CU).
+    // kSdpaSlots parts over all heads, at most 16 and at least 1 per head.
     p.full_qt = a.sq / sdl::BQ;
     const int tail_q = a.sq - p.full_qt * sdl::BQ;
     if (tail_q && p.full_qt && a.split_ws) {
