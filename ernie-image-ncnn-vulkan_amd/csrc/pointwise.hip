@@ -594,8 +594,14 @@ int rms_dispatch_out(const TIn* x, const float* gamma, const float* shift, const
                      float eps, void* out, int odt, hipStream_t s, int out_rows)
 {
     if (out_rows && width % 512 == 0 && width <= 4096 && odt != DT_F32) {
-        // Four persistent workgroups per CU of an MI355X, never more than the row pairs.
-        const dim3 grid((unsigned)std::min((rows + 1) / 2, 1024)), block(256);
+        // Persistent workgroups of about six row pairs each, at least one per CU of an
+        // MI355X (256) and never more than the row pairs or four per CU. Each workgroup
+        // stages the per-column factors (32 KiB at width 4096) once, so fewer, longer
+        // workgroups move fewer bytes: at 4160 x 4096 after the output projection, 347
+        // workgroups took 26.5 us where 1024 (two pairs each) took 30.6 and 694 / 520 /
+        // 260 took 27.9 / 29.5 / 28.3 (bench A/B, two runs each on one box).
+        const int pairs = (rows + 1) / 2;
+        const dim3 grid((unsigned)std::min(std::max(std::min(pairs, 256), (pairs + 5) / 6), 1024)), block(256);
 #define EHIP_RMS_PAIR(NI)                                                                                        \
         do {                                                                                                     \
             if (odt == DT_F16)                                                                                   \
