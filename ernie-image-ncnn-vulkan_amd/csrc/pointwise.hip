@@ -370,9 +370,14 @@ __global__ void residual_kernel(const void* a, int adt, const void* b, int bdt, 
 // Element-wise read-then-write, so out may alias x (in-place latent update).
 __global__ void euler_kernel(const float* x, const float* v, float delta, size_t n, float* out)
 {
+    // The reference compiles its Euler update without contraction (-ffp-contract=off,
+    // src/CMakeLists.txt:12-13): the product is rounded before the sum. hipcc contracts
+    // by default, and __fmul_rn / __fadd_rn alone do not stop it from fusing the two into
+    // one v_fmac_f32, so contraction is switched off for this function.
+#pragma clang fp contract(off)
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
-        const float change = __fmul_rn(delta, v[i]);
-        out[i] = __fadd_rn(x[i], change);
+        const float change = delta * v[i];
+        out[i] = x[i] + change;
     }
 }
 

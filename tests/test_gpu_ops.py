@@ -211,11 +211,55 @@ def test_qk_norm_rope_against_oracle(ctx, dt):
     np.testing.assert_array_equal(got[:, H * 128:], xs[:, H * 128:])
 
 
+@pytest.mark.slow
+@pytest.mark.parametrize("dt", [E.FP32, E.FP16], ids=lambda d: NAMES[d])
+def test_sdpa_config1_every_row_against_oracle(ctx, dt):
+    # The standalone SDPA workload at full size: 32 heads x 128, S = 4160 (4096 image
+    # tokens + a 64-token text bucket whose last 24 keys are padding), Q/K/V ~ N(0,1), scale
+    # 1/sqrt(128), head-major [32][S][128]. Every query row of every head is compared with
+    # the oracle (FP64 sums), so the full query tiles, both rounds of them and the key-split
+    # partial last tile are all covered.
+    S, H, d, valid = 4160, 32, 128, 4136
+    q = O.normal((H, S, d), 2)
+    k = O.normal((H, S, d), 3)
+    v = O.normal((H, S, d), 4)
+    o = empty((H, S, d), dt)
+    strides = (S * d, d, S * d, d, S * d, d, S * d, d)
+    ctx.sdpa(dev(q, dt), dev(k, dt), dev(v, dt), o, dt, H, H, S, S, d, strides, valid_keys=valid)
+    got = host(o)
+    mask = np.zeros(S, np.float32)
+    mask[valid:] = -1e30
+    ref = O.sdpa(stored(q, dt), stored(k, dt), stored(v, dt), mask=mask)
+    if dt == E.FP32:
+        m = kat.fp32_block_rule(got, ref)
+        assert m["passed"] and m["nrmse"] < 1e-6, m
+    else:
+        g = kat.gate(got, ref, *kat.BLOCK_GATES[NAMES[dt]])
+        assert g["passed"], g
+        # Per-row error bound as well, so that a few wrong rows cannot hide in the norm.
+        row_err = np.abs(got - ref).max(axis=2)
+        assert float(row_err.max()) <= 0.02 + 0.02 * float(np.abs(ref).max()), float(row_err.max())
+
+
 def test_euler_and_finite_contracts(ctx):
     # src/latent_ops.cpp:72-92 and tests/test_latent_contract.cpp.
     x = O.normal((128, 5, 3), 9)
     v = O.normal((128, 5, 3), 10)
     xd, vd, out = dev(x), dev(v), empty(x.shape)
+    # Each delta of the 8-step turbo schedule (none a power of two): x + (delta * v) rounded
+    # twice, bitwise the oracle's -ffp-contract=off product and sum. A fused multiply-add
+    # (one rounding) gives different bits for some elements at these deltas, so the test
+    # sees a contraction.
+    sig, _ = O.flow_schedule_turbo(8)
+    contraction_visible = False
+    for i in range(8):
+        delta = np.float32(sig[i + 1] - sig[i])
+        ctx.euler_step(xd, vd, float(delta), x.size, out)
+        ref = O.euler_step(x, v, delta)
+        np.testing.assert_array_equal(host(out), ref)
+        fused = (x.astype(np.float64) + np.float64(delta) * v.astype(np.float64)).astype(np.float32)
+        contraction_visible |= bool(np.any(fused != ref))
+    assert contraction_visible
     ctx.euler_step(xd, vd, -0.0625, x.size, out)
     np.testing.assert_array_equal(host(out), O.euler_step(x, v, -0.0625))
     for bad in (0.0, 0.5, -1.5, float("nan")):

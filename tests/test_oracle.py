@@ -5,6 +5,8 @@ tests (ported in kat.py), closed forms, library routines in FP64 (PyTorch on
 the CPU), or invariants chosen so that a dropped term, wrong sign or transposed
 operand fails.
 """
+import hashlib
+import json
 import math
 from pathlib import Path
 
@@ -112,6 +114,53 @@ def test_dit_constants_brute_force():
     for bad in ((0, 3, 1, 2), (5, 3, 0, 2), (5, 3, 3, 2), (5, 3, 1, 2049)):
         with pytest.raises(ValueError):
             O.dit_constants(freqs, *bad)
+
+
+def _official_block00():
+    """The reference's block-0 fixture record: layout and SHA-256 of the official inputs
+    (artifacts/2026-09-05/components/blocks/block-00/runtime/fixture.json)."""
+    fx = json.loads((GOLDEN / "block00_runtime_fixture.json").read_text())
+    w, h = fx["grid"]
+    assert fx["tokens"] == w * h + fx["text_tokens"]
+    return fx, w, h
+
+
+def _sha256_f32(a):
+    return hashlib.sha256(np.ascontiguousarray(a, "<f4").tobytes()).hexdigest()
+
+
+def test_dit_mask_reproduces_official_in9():
+    # in9 is the official dense [S][S] additive mask of a 4x4 grid with 272 text slots,
+    # 270 valid; the oracle's one-row mask broadcast over the queries is bitwise that tensor.
+    fx, w, h = _official_block00()
+    S = fx["tokens"]
+    _, _, mask = O.dit_constants(O.rope_frequencies(), w, h, fx["valid_text"], fx["text_tokens"])
+    assert fx["inputs"]["in9"]["shape"] == [S, S]
+    assert _sha256_f32(np.broadcast_to(mask.reshape(1, S), (S, S))) == fx["inputs"]["in9"]["sha256"]
+
+
+def test_dit_rope_layout_reproduces_official_in7_in8():
+    # in7 / in8 are the official model's position embeddings. PyTorch FP32 cos / sin of
+    # position x frequency, with image token i at (valid, i / w, i % w), text token j at
+    # (j, 0, 0), axes of 16 / 24 / 24 frequencies and each value duplicated into columns
+    # 2j and 2j + 1, reproduce both hashes bitwise: that pins the position layout, the axis
+    # split and the column duplication to the official model. The oracle's table (glibc
+    # cosf / sinf of the same FP32 phases) is then within one ulp of it everywhere.
+    torch = pytest.importorskip("torch")
+    fx, w, h = _official_block00()
+    S, valid, image = fx["tokens"], fx["valid_text"], w * h
+    freqs = O.rope_frequencies()
+    pos = np.array([(valid, i // w, i % w) if i < image else (i - image, 0, 0) for i in range(S)], np.float32)
+    axis = np.array([0 if j < 16 else 1 if j < 40 else 2 for j in range(64)])
+    phase = torch.from_numpy(np.ascontiguousarray(pos[:, axis])) * torch.from_numpy(freqs)[None, :]
+    tc = torch.cos(phase).repeat_interleave(2, dim=1).numpy()
+    ts = torch.sin(phase).repeat_interleave(2, dim=1).numpy()
+    assert _sha256_f32(tc) == fx["inputs"]["in7"]["sha256"]
+    assert _sha256_f32(ts) == fx["inputs"]["in8"]["sha256"]
+    cos, sin, _ = O.dit_constants(freqs, w, h, valid, fx["text_tokens"])
+    for ours, official in ((cos, tc), (sin, ts)):
+        assert np.all(np.abs(ours.astype(np.float64) - official) <= np.spacing(np.abs(official)))
+        assert np.mean(ours == official) > 0.95
 
 
 # ---- operators -----------------------------------------------------------------------------
