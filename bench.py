@@ -103,10 +103,26 @@ def parse():
                     help="denoise: the headline DiT denoise (default); text: one Mistral text prefill, 25 blocks "
                          "(hidden 3072, 32 heads over 8 K/V heads, ffn 9216) at --text-bucket tokens, causal")
     ap.add_argument("--text-bucket", type=int, default=2048)
+    ap.add_argument("--mfma-ceiling", choices=("on", "off"), default="on",
+                    help="after the timed steps, measure the device's dense FP16 MFMA issue rate and the clock it "
+                         "holds under that load (ernie_hip_mfma_rate), reported as mfma_ceiling")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="first run a plain FP32 copy kernel of this many MiB three times (the reference "
                          "dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
     return ap.parse_args()
+
+
+def mfma_ceiling(ctx):
+    """The box's own dense FP16 matrix-core ceiling: every wave of one 512-thread workgroup per
+    CU (two per SIMD) issues independent v_mfma_f32_16x16x32_f16 from registers, 50 timed
+    launches; the clock is the median over waves of s_memtime / s_memrealtime."""
+    r = ctx.mfma_rate(iters=8192, launches=50)
+    cus = __import__("torch").cuda.get_device_properties(0).multi_processor_count
+    return {"instr": "v_mfma_f32_16x16x32_f16", "waves_per_simd": 2, "cus": cus,
+            "tflops": r["flop_per_s"] / 1e12, "clock_ghz": r["clock_hz"] / 1e9,
+            "flop_per_clock_per_cu": r["flop_per_s"] / r["clock_hz"] / cus if r["clock_hz"] else None,
+            "published_tflops": PEAK["fp16"] / 1e12, "frac_of_published": r["flop_per_s"] / PEAK["fp16"],
+            "seconds": r["seconds"]}
 
 
 def cpu_baseline(tokens):
@@ -344,6 +360,15 @@ def main():
         "step_seconds": [round(float(s), 5) for s in step_s],
         "latent_finite": finite,
     }
+    if args.mfma_ceiling == "on":
+        ceil = mfma_ceiling(ctx)
+        print(f"bench: mfma ceiling {ceil['tflops']:.0f} TFLOP/s at {ceil['clock_ghz']:.2f} GHz", file=sys.stderr,
+              flush=True)
+        result["mfma_ceiling"] = ceil
+        if args.precision in ("fp16", "bf16") and ceil["tflops"] > 0:
+            result["roofline"]["frac_of_measured_ceiling"] = result["roofline"]["achieved"] / ceil["tflops"]
+            if result["mfma_util_sdpa_gemm"] is not None:
+                result["mfma_util_sdpa_gemm_of_measured_ceiling"] = result["sdpa_gemm_tflops"] / ceil["tflops"]
     if args.cpu_baseline == "on":
         print("bench: cpu baseline ...", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(args.cpu_tokens)

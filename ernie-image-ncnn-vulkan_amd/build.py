@@ -21,10 +21,10 @@ LIB = PKG / "lib"
 OBJ = LIB / "obj"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 
-HIP_SOURCES = ["gemm.hip", "gemm16_pp.hip", "sdpa.hip", "sdpa16_dl.hip", "pointwise.hip", "noalloc.hip",
+HIP_SOURCES = ["gemm.hip", "gemm16_pp.hip", "sdpa.hip", "sdpa16_dl.hip", "pointwise.hip", "noalloc.hip", "mfma_rate.hip",
                "ernie_hip.cpp"]
 HOST_SOURCES = ["runtime.cpp", "conditioning.cpp", "latent_ops.cpp", "denoiser.cpp", "block_sequence.cpp", "dit.cpp", "ops.cpp",
-                "sha256.cpp", "block_files.cpp", "block_upload.cpp", "text_encoder.cpp", "capi.cpp"]
+                "sha256.cpp", "block_files.cpp", "block_upload.cpp", "component_files.cpp", "text_encoder.cpp", "capi.cpp"]
 
 # Packed-FP32 VALU forms are disabled for every HIP translation unit.
 HIPCC_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Xclang", "-target-feature",

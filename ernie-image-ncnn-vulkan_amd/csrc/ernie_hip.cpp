@@ -24,6 +24,9 @@ using namespace ehip;
 namespace {
 
 constexpr int kHeadDim = 128;
+// Callers' finite-check slots and markers, then the ranges the C++ facade reserves.
+constexpr int kFiniteSlots = ERNIE_FINITE_SLOTS + ERNIE_FINITE_SLOTS_RESERVED;
+constexpr int kMarkers = ERNIE_MARKERS + ERNIE_MARKERS_RESERVED;
 
 struct DeviceBuffer {
     void* ptr = nullptr;
@@ -58,10 +61,13 @@ struct TextBlockWeights {
     bool k32[4] = {false, false, false, false};  // K-tiled wqkv, wo, w_ug, w_down (16-bit)
 };
 
+// The two DiT heads (heads/input and heads/output head.ncnn.param); each part is loaded
+// and released on its own, sharing dim, latent_ch and dtype.
 struct HeadWeights {
-    bool loaded = false;
+    int parts = 0;  // ERNIE_HEAD_INPUT | ERNIE_HEAD_OUTPUT
     int dim = 0, latent_ch = 0, text_dim = 0, dtype = 0;
-    DeviceBuffer x_w, x_b, text_w, t1_w, t1_b, t2_w, t2_b, mod_w, mod_b, out_mod_w, out_mod_b, proj_w, proj_b;
+    DeviceBuffer x_w, x_b, text_w, t1_w, t1_b, t2_w, t2_b, mod_w, mod_b;  // input head
+    DeviceBuffer out_mod_w, out_mod_b, proj_w, proj_b;                    // output head
 };
 
 struct Launch {
@@ -81,6 +87,8 @@ struct ernie_hip_ctx {
     hipStream_t stream = nullptr;
     std::string error;
     int query_rows = 128;
+    // ERNIE_QK_ROUND_STORAGE: 16-bit blocks round the Q/K projections before their RMSNorm.
+    bool qk_storage_rounding = false;
     std::vector<BlockWeights> blocks;
     std::vector<TextBlockWeights> text_blocks;
     HeadWeights heads;
@@ -105,16 +113,17 @@ struct ernie_hip_ctx {
     std::unordered_map<void*, size_t> live;
     size_t cached_bytes = 0;
     std::mutex alloc_mu;
-    // Finiteness flags: [ERNIE_FINITE_SLOTS] for the asynchronous check plus one for
-    // ernie_hip_finite, on the device; their pinned host copies and completion events.
+    // Finiteness flags: kFiniteSlots for the asynchronous check (the callers' slots, then
+    // the facade's) plus one for ernie_hip_finite, on the device; their pinned host copies
+    // and completion events.
     int* finite_flag = nullptr;
     int* finite_host = nullptr;
-    hipEvent_t finite_event[ERNIE_FINITE_SLOTS] = {};
-    bool finite_pending[ERNIE_FINITE_SLOTS] = {};
-    // Stream markers (ernie_hip_marker_*) and the per-block events of a timed block
-    // sequence: created once, reused by every call.
-    hipEvent_t marker[ERNIE_MARKERS] = {};
-    bool marker_recorded[ERNIE_MARKERS] = {};
+    hipEvent_t finite_event[kFiniteSlots] = {};
+    bool finite_pending[kFiniteSlots] = {};
+    // Stream markers (ernie_hip_marker_*: the callers', then the facade's) and the
+    // per-block events of a timed block sequence: created once, reused by every call.
+    hipEvent_t marker[kMarkers] = {};
+    bool marker_recorded[kMarkers] = {};
     std::vector<hipEvent_t> seq_events;
     // Pinned staging blocks of ernie_hip_upload_async, each with the event of its last
     // copy: a block is reused once that copy has finished.
@@ -225,12 +234,16 @@ void free_text_block(TextBlockWeights& w)
     w = TextBlockWeights{};
 }
 
-void free_heads(HeadWeights& h)
+// Releases the head parts in `parts`; the dimensions go with the last part.
+void free_heads(HeadWeights& h, int parts = ERNIE_HEAD_INPUT | ERNIE_HEAD_OUTPUT)
 {
-    for (DeviceBuffer* b : {&h.x_w, &h.x_b, &h.text_w, &h.t1_w, &h.t1_b, &h.t2_w, &h.t2_b, &h.mod_w, &h.mod_b,
-                            &h.out_mod_w, &h.out_mod_b, &h.proj_w, &h.proj_b})
-        dev_free(*b);
-    h = HeadWeights{};
+    if (parts & ERNIE_HEAD_INPUT)
+        for (DeviceBuffer* b : {&h.x_w, &h.x_b, &h.text_w, &h.t1_w, &h.t1_b, &h.t2_w, &h.t2_b, &h.mod_w, &h.mod_b})
+            dev_free(*b);
+    if (parts & ERNIE_HEAD_OUTPUT)
+        for (DeviceBuffer* b : {&h.out_mod_w, &h.out_mod_b, &h.proj_w, &h.proj_b}) dev_free(*b);
+    h.parts &= ~parts;
+    if (!h.parts) h = HeadWeights{};
 }
 
 // ---- event timing ------------------------------------------------------------------
@@ -475,7 +488,7 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
         g.w_k32 = w.k32[0];
         g.a_k32_rows = ws.rows;
         g.epilogue = EPI_STORE; g.C = ws.qkv; g.ldc = 3 * D; g.c_dtype = dt;
-        if (w.qk_fused) {
+        if (w.qk_fused && !ctx->qk_storage_rounding) {
             g.epilogue = EPI_QKROPE;
             g.qk_cols = 2 * D; g.k_col = D;
             g.gq = static_cast<const float*>(w.norm_q.ptr); g.gk = static_cast<const float*>(w.norm_k.ptr);
@@ -487,8 +500,16 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
         rc = kernel_status(ctx, gemm(g, s), "gemm qkv");
         if (rc) return rc;
     }
-    // rmsn_9 / rmsn_10 + rotary, in place on the Q and K column blocks
-    if (!w.qk_fused) {
+    // rmsn_9 / rmsn_10 + rotary on the Q and K columns the GEMM rounded to the storage
+    // dtype: in place and in natural order, or from the permuted order of fused-layout weights.
+    if (w.qk_fused && ctx->qk_storage_rounding) {
+        Timed t(ctx, P_ROPE, 0, dS * 2 * D * e * 2 + dS * 128 * 8);
+        rc = kernel_status(ctx, qk_norm_rope_permuted(ws.qkv, dt, 0, S, H, H, 3L * D, D,
+                                                      static_cast<const float*>(w.norm_q.ptr),
+                                                      static_cast<const float*>(w.norm_k.ptr), cos_t, sin_t, 1e-6f, s),
+                           "qk_norm_rope");
+        if (rc) return rc;
+    } else if (!w.qk_fused) {
         Timed t(ctx, P_ROPE, 0, dS * 2 * D * e * 2 + dS * 128 * 8);
         rc = kernel_status(ctx, qk_norm_rope_qk(ws.qkv, dt, S, H, H, 3L * D, D, static_cast<const float*>(w.norm_q.ptr),
                                                 static_cast<const float*>(w.norm_k.ptr), cos_t, sin_t, s),
@@ -889,6 +910,33 @@ int check_block_call(ernie_hip_ctx* ctx, int index, int S, const void* x, const 
     return ERNIE_OK;
 }
 
+// Makes a context's device current for the duration of one entry point and gives the
+// calling thread its own selection back afterwards. Allocations (hipMalloc), device
+// queries (the GEMM launcher's CU count) and launches then all refer to the context's
+// device, whichever device the calling thread had selected before the call.
+struct DeviceGuard {
+    int prev = -1;
+    bool ok = true;
+    explicit DeviceGuard(int device)
+    {
+        if (device < 0) return;
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev == device) {
+            prev = -1;
+            return;
+        }
+        ok = hipSetDevice(device) == hipSuccess;
+        if (!ok) (void)hipGetLastError();
+    }
+    explicit DeviceGuard(const ernie_hip_ctx* ctx) : DeviceGuard(ctx ? ctx->device : -1) {}
+    ~DeviceGuard()
+    {
+        if (prev >= 0) (void)hipSetDevice(prev);
+    }
+    DeviceGuard(const DeviceGuard&) = delete;
+    DeviceGuard& operator=(const DeviceGuard&) = delete;
+};
+
 }  // namespace
 
 // =====================================================================================
@@ -900,7 +948,8 @@ int ernie_hip_create(int device, ernie_hip_ctx** out)
     *out = nullptr;
     int count = 0;
     if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) return ERNIE_ERROR;
-    if (hipSetDevice(device) != hipSuccess) return ERNIE_ERROR;
+    DeviceGuard guard(device);
+    if (!guard.ok) return ERNIE_ERROR;
     auto* ctx = new (std::nothrow) ernie_hip_ctx();
     if (!ctx) return ERNIE_ALLOCATION_FAILED;
     ctx->device = device;
@@ -916,8 +965,8 @@ int ernie_hip_create(int device, ernie_hip_ctx** out)
 
 void ernie_hip_destroy(ernie_hip_ctx* ctx)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return;
-    (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     for (auto& b : ctx->blocks) free_block(b);
     for (auto& b : ctx->text_blocks) free_text_block(b);
@@ -951,6 +1000,7 @@ const char* ernie_hip_last_error(const ernie_hip_ctx* ctx) { return ctx ? ctx->e
 
 int ernie_hip_set_stream(ernie_hip_ctx* ctx, void* stream)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     // Cached blocks may still be in use by work on the old stream: let it finish first.
     if (ctx->stream != static_cast<hipStream_t>(stream) && ctx->stream) (void)hipStreamSynchronize(ctx->stream);
@@ -964,6 +1014,7 @@ void* ernie_hip_get_stream(ernie_hip_ctx* ctx) { return ctx ? ctx->stream : null
 
 int ernie_hip_synchronize(ernie_hip_ctx* ctx)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     return hip_status(ctx, hipStreamSynchronize(ctx->stream), "synchronize");
 }
@@ -973,6 +1024,7 @@ constexpr size_t kCacheCapBytes = size_t(8) << 30;
 
 int ernie_hip_malloc(ernie_hip_ctx* ctx, size_t bytes, void** out)
 {
+    DeviceGuard guard(ctx);
     if (!ctx || !out) return ERNIE_ERROR;
     *out = nullptr;
     const size_t b = ((bytes ? bytes : 1) + 255) / 256 * 256;
@@ -997,6 +1049,7 @@ int ernie_hip_malloc(ernie_hip_ctx* ctx, size_t bytes, void** out)
 
 int ernie_hip_free(ernie_hip_ctx* ctx, void* ptr)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     if (!ptr) return ERNIE_OK;
     {
@@ -1017,6 +1070,7 @@ int ernie_hip_free(ernie_hip_ctx* ctx, void* ptr)
 
 size_t ernie_hip_trim(ernie_hip_ctx* ctx)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return 0;
     (void)hipStreamSynchronize(ctx->stream);
     return release_cache(ctx);
@@ -1024,6 +1078,7 @@ size_t ernie_hip_trim(ernie_hip_ctx* ctx)
 
 int ernie_hip_memcpy_h2d(ernie_hip_ctx* ctx, void* dst, const void* src, size_t bytes)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     int rc = hip_status(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "h2d");
     return rc ? rc : hip_status(ctx, hipStreamSynchronize(ctx->stream), "h2d");
@@ -1031,6 +1086,7 @@ int ernie_hip_memcpy_h2d(ernie_hip_ctx* ctx, void* dst, const void* src, size_t 
 
 int ernie_hip_upload_async(ernie_hip_ctx* ctx, void* dst, const void* src, size_t bytes)
 {
+    DeviceGuard guard(ctx);
     if (!ctx || (!src && bytes) || (!dst && bytes)) return ERNIE_ERROR;
     if (!bytes) return ERNIE_OK;
     // A staging block whose previous copy has finished and that is large enough.
@@ -1060,6 +1116,7 @@ int ernie_hip_upload_async(ernie_hip_ctx* ctx, void* dst, const void* src, size_
 
 int ernie_hip_memcpy_d2h(ernie_hip_ctx* ctx, void* dst, const void* src, size_t bytes)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     int rc = hip_status(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "d2h");
     return rc ? rc : hip_status(ctx, hipStreamSynchronize(ctx->stream), "d2h");
@@ -1069,6 +1126,7 @@ int ernie_hip_memcpy_d2h(ernie_hip_ctx* ctx, void* dst, const void* src, size_t 
 int ernie_hip_rmsnorm(ernie_hip_ctx* ctx, const void* x, int x_dtype, const float* gamma, const float* shift,
                       const float* scale, int rows, int width, float eps, void* out, int out_dtype)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     return kernel_status(ctx, rmsnorm_modulate(x, x_dtype, gamma, shift, scale, rows, width, eps, out, out_dtype,
                                                ctx->stream), "rmsnorm");
@@ -1077,6 +1135,7 @@ int ernie_hip_rmsnorm(ernie_hip_ctx* ctx, const void* x, int x_dtype, const floa
 int ernie_hip_layernorm_modulate(ernie_hip_ctx* ctx, const float* x, const float* shift, const float* scale, int rows,
                                  int width, float eps, void* out, int out_dtype)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     return kernel_status(ctx, layernorm_modulate(x, shift, scale, rows, width, eps, out, out_dtype, ctx->stream),
                          "layernorm");
@@ -1084,6 +1143,7 @@ int ernie_hip_layernorm_modulate(ernie_hip_ctx* ctx, const float* x, const float
 
 int ernie_hip_gelu(ernie_hip_ctx* ctx, void* data, int dtype, size_t count)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     return kernel_status(ctx, gelu_inplace(data, dtype, count, ctx->stream), "gelu");
 }
@@ -1091,6 +1151,7 @@ int ernie_hip_gelu(ernie_hip_ctx* ctx, void* data, int dtype, size_t count)
 int ernie_hip_residual_add(ernie_hip_ctx* ctx, const void* a, int a_dtype, const void* b, int b_dtype, float* out,
                            size_t count)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     return kernel_status(ctx, residual_add(a, a_dtype, b, b_dtype, out, count, ctx->stream), "residual_add");
 }
@@ -1098,6 +1159,7 @@ int ernie_hip_residual_add(ernie_hip_ctx* ctx, const void* a, int a_dtype, const
 int ernie_hip_gemm(ernie_hip_ctx* ctx, const void* a, long lda, const void* w, long ldw, const float* bias, void* c,
                    long ldc, int m, int n, int k, int dtype, int out_dtype)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     GemmArgs g;
     g.A = a; g.lda = lda; g.W = w; g.ldw = ldw; g.M = m; g.N = n; g.K = k; g.dtype = dtype;
@@ -1110,6 +1172,7 @@ int ernie_hip_sdpa(ernie_hip_ctx* ctx, const void* q, const void* k, const void*
                    long v_rs, long o_hs, long o_rs, const float* mask, int mask_heads, int mask_rows, int valid_keys,
                    float scale)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     SdpaArgs a;
     a.q = q; a.k = k; a.v = v; a.o = out; a.dtype = dtype; a.heads = heads; a.kv_heads = kv_heads;
@@ -1123,6 +1186,7 @@ int ernie_hip_sdpa_causal(ernie_hip_ctx* ctx, const void* q, const void* k, cons
                           int heads, int kv_heads, int sq, int sk, int d, long q_hs, long q_rs, long k_hs, long k_rs,
                           long v_hs, long v_rs, long o_hs, long o_rs, float scale)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     SdpaArgs a;
     a.q = q; a.k = k; a.v = v; a.o = out; a.dtype = dtype; a.heads = heads; a.kv_heads = kv_heads;
@@ -1133,6 +1197,7 @@ int ernie_hip_sdpa_causal(ernie_hip_ctx* ctx, const void* q, const void* k, cons
 
 int ernie_hip_set_attention_query_rows(ernie_hip_ctx* ctx, int rows)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     if (rows != 128 && rows != 64 && rows != 32 && rows != 16)
         return fail(ctx, ERNIE_ERROR, "Attention query rows must be 128, 64, 32 or 16");
@@ -1142,9 +1207,19 @@ int ernie_hip_set_attention_query_rows(ernie_hip_ctx* ctx, int rows)
 
 uint64_t ernie_hip_attention_internal_submissions(const ernie_hip_ctx*) { return 0; }
 
+int ernie_hip_set_qk_rounding(ernie_hip_ctx* ctx, int mode)
+{
+    if (!ctx) return ERNIE_ERROR;
+    if (mode != ERNIE_QK_ROUND_FUSED && mode != ERNIE_QK_ROUND_STORAGE)
+        return fail(ctx, ERNIE_ERROR, "Q/K rounding mode must be ERNIE_QK_ROUND_FUSED or ERNIE_QK_ROUND_STORAGE");
+    ctx->qk_storage_rounding = mode == ERNIE_QK_ROUND_STORAGE;
+    return ERNIE_OK;
+}
+
 int ernie_hip_qk_norm_rope(ernie_hip_ctx* ctx, void* x, int dtype, int rows, int heads, long row_stride,
                            const float* gamma, const float* cos_t, const float* sin_t)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     return kernel_status(ctx, qk_norm_rope(x, dtype, rows, heads, row_stride, gamma, cos_t, sin_t, ctx->stream),
                          "qk_norm_rope");
@@ -1152,6 +1227,7 @@ int ernie_hip_qk_norm_rope(ernie_hip_ctx* ctx, void* x, int dtype, int rows, int
 
 int ernie_hip_euler_step(ernie_hip_ctx* ctx, const float* x, const float* v, float delta, size_t count, float* out)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     if (!std::isfinite(delta) || delta >= 0.f || delta < -1.f)
         return fail(ctx, ERNIE_ERROR, "Incompatible Euler shapes or delta outside [-1,0)");
@@ -1162,12 +1238,12 @@ int ernie_hip_euler_step(ernie_hip_ctx* ctx, const float* x, const float* v, flo
 static int finite_setup(ernie_hip_ctx* ctx)
 {
     if (ctx->finite_flag) return ERNIE_OK;
-    constexpr int n = ERNIE_FINITE_SLOTS + 1;
+    constexpr int n = kFiniteSlots + 1;
     int rc = hip_status(ctx, device_malloc(ctx, reinterpret_cast<void**>(&ctx->finite_flag), n * sizeof(int)),
                         "finite flags");
     if (!rc) rc = hip_status(ctx, hipHostMalloc(reinterpret_cast<void**>(&ctx->finite_host), n * sizeof(int), 0),
                              "finite flags");
-    for (int i = 0; i < ERNIE_FINITE_SLOTS && !rc; ++i)
+    for (int i = 0; i < kFiniteSlots && !rc; ++i)
         rc = hip_status(ctx, hipEventCreateWithFlags(&ctx->finite_event[i], hipEventDisableTiming), "finite event");
     if (rc) {
         for (hipEvent_t& e : ctx->finite_event)
@@ -1194,17 +1270,19 @@ static int finite_enqueue(ernie_hip_ctx* ctx, const float* x, size_t count, int 
 
 int ernie_hip_finite(ernie_hip_ctx* ctx, const float* x, size_t count, int* finite)
 {
+    DeviceGuard guard(ctx);
     if (!ctx || !finite || (!x && count)) return ERNIE_ERROR;
-    int rc = finite_enqueue(ctx, x, count, ERNIE_FINITE_SLOTS);
+    int rc = finite_enqueue(ctx, x, count, kFiniteSlots);
     if (!rc) rc = hip_status(ctx, hipStreamSynchronize(ctx->stream), "finite");
-    if (!rc) *finite = ctx->finite_host[ERNIE_FINITE_SLOTS] ? 0 : 1;
+    if (!rc) *finite = ctx->finite_host[kFiniteSlots] ? 0 : 1;
     return rc;
 }
 
 int ernie_hip_finite_begin(ernie_hip_ctx* ctx, const float* x, size_t count, int slot)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
-    if (slot < 0 || slot >= ERNIE_FINITE_SLOTS) return fail(ctx, ERNIE_ERROR, "finite slot out of range");
+    if (slot < 0 || slot >= kFiniteSlots) return fail(ctx, ERNIE_ERROR, "finite slot out of range");
     if (!x && count) return fail(ctx, ERNIE_ERROR, "null finite input");
     int rc = finite_enqueue(ctx, x, count, slot);
     if (!rc) rc = hip_status(ctx, hipEventRecord(ctx->finite_event[slot], ctx->stream), "finite event");
@@ -1214,8 +1292,9 @@ int ernie_hip_finite_begin(ernie_hip_ctx* ctx, const float* x, size_t count, int
 
 int ernie_hip_finite_end(ernie_hip_ctx* ctx, int slot, int* finite)
 {
+    DeviceGuard guard(ctx);
     if (!ctx || !finite) return ERNIE_ERROR;
-    if (slot < 0 || slot >= ERNIE_FINITE_SLOTS || !ctx->finite_pending[slot])
+    if (slot < 0 || slot >= kFiniteSlots || !ctx->finite_pending[slot])
         return fail(ctx, ERNIE_ERROR, "no finite check pending in this slot");
     ctx->finite_pending[slot] = false;
     const int rc = hip_status(ctx, hipEventSynchronize(ctx->finite_event[slot]), "finite wait");
@@ -1225,8 +1304,9 @@ int ernie_hip_finite_end(ernie_hip_ctx* ctx, int slot, int* finite)
 
 int ernie_hip_marker_record(ernie_hip_ctx* ctx, int marker)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
-    if (marker < 0 || marker >= ERNIE_MARKERS) return fail(ctx, ERNIE_ERROR, "marker out of range");
+    if (marker < 0 || marker >= kMarkers) return fail(ctx, ERNIE_ERROR, "marker out of range");
     if (!ctx->marker[marker]) {
         const int rc = hip_status(ctx, hipEventCreate(&ctx->marker[marker]), "marker");
         if (rc) return rc;
@@ -1238,8 +1318,9 @@ int ernie_hip_marker_record(ernie_hip_ctx* ctx, int marker)
 
 int ernie_hip_marker_elapsed(ernie_hip_ctx* ctx, int from, int to, double* seconds)
 {
+    DeviceGuard guard(ctx);
     if (!ctx || !seconds) return ERNIE_ERROR;
-    if (from < 0 || to < 0 || from >= ERNIE_MARKERS || to >= ERNIE_MARKERS || !ctx->marker_recorded[from] ||
+    if (from < 0 || to < 0 || from >= kMarkers || to >= kMarkers || !ctx->marker_recorded[from] ||
         !ctx->marker_recorded[to])
         return fail(ctx, ERNIE_ERROR, "marker not recorded");
     int rc = hip_status(ctx, hipEventSynchronize(ctx->marker[to]), "marker wait");
@@ -1251,6 +1332,7 @@ int ernie_hip_marker_elapsed(ernie_hip_ctx* ctx, int from, int to, double* secon
 
 int ernie_hip_transpose(ernie_hip_ctx* ctx, const void* in, int dtype, int rows, int cols, void* out)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     if (in == out && rows > 1 && cols > 1) return fail(ctx, ERNIE_ERROR, "transpose cannot run in place");
     return kernel_status(ctx, transpose2d(in, dtype, rows, cols, out, ctx->stream), "transpose");
@@ -1259,12 +1341,14 @@ int ernie_hip_transpose(ernie_hip_ctx* ctx, const void* in, int dtype, int rows,
 int ernie_hip_fill_normal(ernie_hip_ctx* ctx, void* out, int dtype, size_t count, uint64_t seed, uint64_t offset,
                           float mean, float std_dev)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     return kernel_status(ctx, fill_normal(out, dtype, count, seed, offset, mean, std_dev, ctx->stream), "fill_normal");
 }
 
 int ernie_hip_convert(ernie_hip_ctx* ctx, const void* in, int in_dtype, void* out, int out_dtype, size_t count)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     return kernel_status(ctx, convert(in, in_dtype, out, out_dtype, count, ctx->stream), "convert");
 }
@@ -1273,6 +1357,7 @@ int ernie_hip_convert(ernie_hip_ctx* ctx, const void* in, int in_dtype, void* ou
 int ernie_hip_block_upload_tensors(ernie_hip_ctx* ctx, int index, const ernie_block_host_tensors* w, int dim, int ffn,
                                    int dtype)
 {
+    DeviceGuard guard(ctx);
     if (!ctx || !w) return ERNIE_ERROR;
     int rc = check_block_dims(ctx, dim, ffn, dtype);
     if (rc) return rc;
@@ -1324,6 +1409,7 @@ int ernie_hip_block_upload_tensors(ernie_hip_ctx* ctx, int index, const ernie_bl
 int ernie_hip_block_upload(ernie_hip_ctx* ctx, int index, const ernie_block_host_weights* w, int dim, int ffn,
                            int dtype)
 {
+    DeviceGuard guard(ctx);
     if (!ctx || !w) return ERNIE_ERROR;
     auto f32 = [](const float* p) { return ernie_host_tensor{p, ERNIE_DTYPE_FP32}; };
     const ernie_block_host_tensors t = {f32(w->norm1), f32(w->wq),     f32(w->wk),     f32(w->wv),
@@ -1335,6 +1421,7 @@ int ernie_hip_block_upload(ernie_hip_ctx* ctx, int index, const ernie_block_host
 int ernie_hip_block_init_random(ernie_hip_ctx* ctx, int index, int dim, int ffn, int dtype, uint64_t seed,
                                 float std_dev)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     int rc = check_block_dims(ctx, dim, ffn, dtype);
     if (rc) return rc;
@@ -1370,6 +1457,7 @@ int ernie_hip_block_init_random(ernie_hip_ctx* ctx, int index, int dim, int ffn,
 
 int ernie_hip_block_release(ernie_hip_ctx* ctx, int index)
 {
+    DeviceGuard guard(ctx);
     if (!ctx || index < 0 || (size_t)index >= ctx->blocks.size()) return ERNIE_ERROR;
     (void)hipStreamSynchronize(ctx->stream);
     free_block(ctx->blocks[index]);
@@ -1387,6 +1475,7 @@ int ernie_hip_block_count(const ernie_hip_ctx* ctx)
 int ernie_hip_block_forward(ernie_hip_ctx* ctx, int index, const float* x, float* out, const float* mods,
                             const float* cos_t, const float* sin_t, const float* mask, int valid_keys, int S)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     int rc = check_block_call(ctx, index, S, x, out, mods, cos_t, sin_t, valid_keys);
     if (rc) return rc;
@@ -1397,6 +1486,7 @@ int ernie_hip_block_sequence(ernie_hip_ctx* ctx, const int* blocks, int count, c
                              const float* mods, const float* cos_t, const float* sin_t, const float* mask,
                              int valid_keys, int S, double* seconds)
 {
+    DeviceGuard guard(ctx);
     if (!ctx || !blocks) return ERNIE_ERROR;
     if (count < 1 || count > 36) return fail(ctx, ERNIE_ERROR, "Expected 1..36 blocks");
     for (int i = 0; i < count; ++i) {
@@ -1419,6 +1509,7 @@ int ernie_hip_block_sequence(ernie_hip_ctx* ctx, const int* blocks, int count, c
 int ernie_hip_text_block_upload_tensors(ernie_hip_ctx* ctx, int index, const ernie_text_block_host_tensors* w,
                                         int hidden, int heads, int kv_heads, int ffn, int dtype)
 {
+    DeviceGuard guard(ctx);
     if (!ctx || !w) return ERNIE_ERROR;
     int rc = check_text_dims(ctx, hidden, heads, kv_heads, ffn, dtype);
     if (rc) return rc;
@@ -1467,6 +1558,7 @@ int ernie_hip_text_block_upload_tensors(ernie_hip_ctx* ctx, int index, const ern
 int ernie_hip_text_block_init_random(ernie_hip_ctx* ctx, int index, int hidden, int heads, int kv_heads, int ffn,
                                      int dtype, uint64_t seed, float std_dev)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     int rc = check_text_dims(ctx, hidden, heads, kv_heads, ffn, dtype);
     if (rc) return rc;
@@ -1504,6 +1596,7 @@ int ernie_hip_text_block_init_random(ernie_hip_ctx* ctx, int index, int hidden, 
 
 int ernie_hip_text_block_release(ernie_hip_ctx* ctx, int index)
 {
+    DeviceGuard guard(ctx);
     if (!ctx || index < 0 || (size_t)index >= ctx->text_blocks.size()) return ERNIE_ERROR;
     (void)hipStreamSynchronize(ctx->stream);
     free_text_block(ctx->text_blocks[index]);
@@ -1513,6 +1606,7 @@ int ernie_hip_text_block_release(ernie_hip_ctx* ctx, int index)
 int ernie_hip_text_block_forward(ernie_hip_ctx* ctx, int index, const float* x, float* out, const float* cos_t,
                                  const float* sin_t, const float* mask, int causal, int S)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     const int rc = check_text_call(ctx, index, S, x, out, cos_t, sin_t);
     if (rc) return rc;
@@ -1522,6 +1616,7 @@ int ernie_hip_text_block_forward(ernie_hip_ctx* ctx, int index, const float* x, 
 int ernie_hip_text_block_forward_noalloc(ernie_hip_ctx* ctx, int index, const float* x, float* out,
                                          const float* cos_t, const float* sin_t, const float* mask, int causal, int S)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     int rc = check_text_call(ctx, index, S, x, out, cos_t, sin_t);
     if (rc) return rc;
@@ -1555,6 +1650,7 @@ int ernie_hip_text_block_sequence(ernie_hip_ctx* ctx, const int* blocks, int cou
                                   const float* cos_t, const float* sin_t, const float* mask, int causal, int S,
                                   double* seconds)
 {
+    DeviceGuard guard(ctx);
     if (!ctx || !blocks) return ERNIE_ERROR;
     if (count < 1 || count > 25) return fail(ctx, ERNIE_ERROR, "Text path requires 1..25 blocks");
     for (int i = 0; i < count; ++i) {
@@ -1574,54 +1670,86 @@ int ernie_hip_text_block_sequence(ernie_hip_ctx* ctx, const int* blocks, int cou
 }
 
 // ---- heads --------------------------------------------------------------------------------
+int ernie_hip_heads_upload_tensors(ernie_hip_ctx* ctx, const ernie_heads_host_tensors* w, int dim, int latent_ch,
+                                   int text_dim, int dtype, int parts)
+{
+    DeviceGuard guard(ctx);
+    if (!ctx || !w) return ERNIE_ERROR;
+    const int all = ERNIE_HEAD_INPUT | ERNIE_HEAD_OUTPUT;
+    if (parts < 1 || parts > all) return fail(ctx, ERNIE_ERROR, "head parts must be ERNIE_HEAD_INPUT and/or _OUTPUT");
+    const bool in = parts & ERNIE_HEAD_INPUT, out = parts & ERNIE_HEAD_OUTPUT;
+    if (!valid_dtype(dtype) || dim < 128 || dim % 128 || latent_ch < 1 || (in && text_dim < 1))
+        return fail(ctx, ERNIE_ERROR, "invalid head dimensions");
+    if (latent_ch % 32 || (in && text_dim % 32)) return fail(ctx, ERNIE_ERROR, "head widths must be multiples of 32");
+    HeadWeights& h = ctx->heads;
+    const int kept = h.parts & ~parts;
+    if (kept && (h.dim != dim || h.latent_ch != latent_ch || h.dtype != dtype))
+        return fail(ctx, ERNIE_ERROR, std::string("the resident ") + (kept == ERNIE_HEAD_INPUT ? "input" : "output") +
+                                          " head has another width, channel count or storage dtype");
+    free_heads(h, parts);
+    const size_t e = esize(dtype), D = dim;
+    int rc = 0;
+    auto mat = [&](DeviceBuffer& b, const ernie_host_tensor& t, size_t n, const char* what) {
+        if (rc) return;
+        if (!t.data) { rc = fail(ctx, ERNIE_ERROR, std::string("null ") + what); return; }
+        rc = dev_alloc(ctx, b, n * e, what);
+        if (!rc) rc = upload_tensor(ctx, b.ptr, 0, dtype, t.data, t.dtype, n, what);
+    };
+    auto vec = [&](DeviceBuffer& b, const ernie_host_tensor& t, size_t n, const char* what) {
+        if (rc) return;
+        if (!t.data) { rc = fail(ctx, ERNIE_ERROR, std::string("null ") + what); return; }
+        rc = dev_alloc(ctx, b, n * 4, what);
+        if (!rc) rc = upload_tensor(ctx, b.ptr, 0, ERNIE_DTYPE_FP32, t.data, t.dtype, n, what);
+    };
+    if (in) {
+        mat(h.x_w, w->x_w, D * latent_ch, "x_w");
+        vec(h.x_b, w->x_b, D, "x_b");
+        mat(h.text_w, w->text_w, D * text_dim, "text_w");
+        mat(h.t1_w, w->t1_w, D * D, "t1_w");
+        vec(h.t1_b, w->t1_b, D, "t1_b");
+        mat(h.t2_w, w->t2_w, D * D, "t2_w");
+        vec(h.t2_b, w->t2_b, D, "t2_b");
+        mat(h.mod_w, w->mod_w, 6 * D * D, "mod_w");
+        vec(h.mod_b, w->mod_b, 6 * D, "mod_b");
+    }
+    if (out) {
+        mat(h.out_mod_w, w->out_mod_w, 2 * D * D, "out_mod_w");
+        vec(h.out_mod_b, w->out_mod_b, 2 * D, "out_mod_b");
+        mat(h.proj_w, w->proj_w, (size_t)latent_ch * D, "proj_w");
+        vec(h.proj_b, w->proj_b, latent_ch, "proj_b");
+    }
+    if (!rc) rc = hip_status(ctx, hipStreamSynchronize(ctx->stream), "heads upload");
+    if (rc) {
+        free_heads(h, parts);
+        return rc;
+    }
+    h.dim = dim;
+    h.latent_ch = latent_ch;
+    h.dtype = dtype;
+    if (in) h.text_dim = text_dim;
+    h.parts |= parts;
+    return ERNIE_OK;
+}
+
 int ernie_hip_heads_upload(ernie_hip_ctx* ctx, const ernie_heads_host_weights* w, int dim, int latent_ch, int text_dim,
                            int dtype)
 {
     if (!ctx || !w) return ERNIE_ERROR;
-    if (!valid_dtype(dtype) || dim < 128 || dim % 128 || latent_ch < 1 || text_dim < 1)
-        return fail(ctx, ERNIE_ERROR, "invalid head dimensions");
-    if (latent_ch % 32 || text_dim % 32) return fail(ctx, ERNIE_ERROR, "head widths must be multiples of 32");
-    free_heads(ctx->heads);
-    HeadWeights& h = ctx->heads;
-    const size_t e = esize(dtype), D = dim;
-    int rc = 0;
-    auto mat = [&](DeviceBuffer& b, const float* src, size_t n, const char* what) {
-        if (rc) return;
-        if (!src) { rc = fail(ctx, ERNIE_ERROR, std::string("null ") + what); return; }
-        rc = dev_alloc(ctx, b, n * e, what);
-        if (!rc) rc = upload_tensor(ctx, b.ptr, 0, dtype, src, ERNIE_DTYPE_FP32, n, what);
-    };
-    auto vec = [&](DeviceBuffer& b, const float* src, size_t n, const char* what) {
-        if (rc) return;
-        if (!src) { rc = fail(ctx, ERNIE_ERROR, std::string("null ") + what); return; }
-        rc = dev_alloc(ctx, b, n * 4, what);
-        if (!rc) rc = upload_tensor(ctx, b.ptr, 0, ERNIE_DTYPE_FP32, src, ERNIE_DTYPE_FP32, n, what);
-    };
-    mat(h.x_w, w->x_w, D * latent_ch, "x_w");
-    vec(h.x_b, w->x_b, D, "x_b");
-    mat(h.text_w, w->text_w, D * text_dim, "text_w");
-    mat(h.t1_w, w->t1_w, D * D, "t1_w");
-    vec(h.t1_b, w->t1_b, D, "t1_b");
-    mat(h.t2_w, w->t2_w, D * D, "t2_w");
-    vec(h.t2_b, w->t2_b, D, "t2_b");
-    mat(h.mod_w, w->mod_w, 6 * D * D, "mod_w");
-    vec(h.mod_b, w->mod_b, 6 * D, "mod_b");
-    mat(h.out_mod_w, w->out_mod_w, 2 * D * D, "out_mod_w");
-    vec(h.out_mod_b, w->out_mod_b, 2 * D, "out_mod_b");
-    mat(h.proj_w, w->proj_w, (size_t)latent_ch * D, "proj_w");
-    vec(h.proj_b, w->proj_b, latent_ch, "proj_b");
-    if (!rc) rc = hip_status(ctx, hipStreamSynchronize(ctx->stream), "heads upload");
-    if (rc) {
-        free_heads(h);
-        return rc;
-    }
-    h.dim = dim; h.latent_ch = latent_ch; h.text_dim = text_dim; h.dtype = dtype; h.loaded = true;
-    return ERNIE_OK;
+    const int F32 = ERNIE_DTYPE_FP32;
+    const ernie_heads_host_tensors t = {{w->x_w, F32},     {w->x_b, F32},  {w->text_w, F32},   {w->t1_w, F32},
+                                        {w->t1_b, F32},    {w->t2_w, F32}, {w->t2_b, F32},     {w->mod_w, F32},
+                                        {w->mod_b, F32},   {w->out_mod_w, F32}, {w->out_mod_b, F32},
+                                        {w->proj_w, F32},  {w->proj_b, F32}};
+    return ernie_hip_heads_upload_tensors(ctx, &t, dim, latent_ch, text_dim, dtype,
+                                          ERNIE_HEAD_INPUT | ERNIE_HEAD_OUTPUT);
 }
+
+int ernie_hip_heads_loaded(const ernie_hip_ctx* ctx) { return ctx ? ctx->heads.parts : 0; }
 
 int ernie_hip_heads_init_random(ernie_hip_ctx* ctx, int dim, int latent_ch, int text_dim, int dtype, uint64_t seed,
                                 float std_dev)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     if (!valid_dtype(dtype) || dim < 128 || dim % 128 || latent_ch < 32 || latent_ch % 32 || text_dim < 32 ||
         text_dim % 32)
@@ -1648,15 +1776,17 @@ int ernie_hip_heads_init_random(ernie_hip_ctx* ctx, int dim, int latent_ch, int 
         free_heads(h);
         return rc;
     }
-    h.dim = dim; h.latent_ch = latent_ch; h.text_dim = text_dim; h.dtype = dtype; h.loaded = true;
+    h.dim = dim; h.latent_ch = latent_ch; h.text_dim = text_dim; h.dtype = dtype;
+    h.parts = ERNIE_HEAD_INPUT | ERNIE_HEAD_OUTPUT;
     return ERNIE_OK;
 }
 
 int ernie_hip_input_head(ernie_hip_ctx* ctx, const float* latent, int hw, const float* text, int text_tokens,
                          const float* time_features, float* x, float* c, float* mods)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
-    if (!ctx->heads.loaded) return fail(ctx, ERNIE_ERROR, "heads are not loaded");
+    if (!(ctx->heads.parts & ERNIE_HEAD_INPUT)) return fail(ctx, ERNIE_ERROR, "the input head is not loaded");
     if (!latent || !time_features || !x || !c || !mods || hw < 1 || text_tokens < 0 || (text_tokens && !text))
         return fail(ctx, ERNIE_ERROR, "invalid input head arguments");
     return input_head(ctx, latent, hw, text, text_tokens, time_features, x, c, mods);
@@ -1664,8 +1794,9 @@ int ernie_hip_input_head(ernie_hip_ctx* ctx, const float* latent, int hw, const 
 
 int ernie_hip_output_head(ernie_hip_ctx* ctx, const float* x, int S, int hw, const float* c, float* prediction)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
-    if (!ctx->heads.loaded) return fail(ctx, ERNIE_ERROR, "heads are not loaded");
+    if (!(ctx->heads.parts & ERNIE_HEAD_OUTPUT)) return fail(ctx, ERNIE_ERROR, "the output head is not loaded");
     if (!x || !c || !prediction || hw < 1 || hw > S) return fail(ctx, ERNIE_ERROR, "invalid output head arguments");
     return output_head(ctx, x, hw, c, prediction);
 }
@@ -1674,8 +1805,10 @@ int ernie_hip_dit_forward(ernie_hip_ctx* ctx, const float* latent, int hw, const
                           const float* time_features, const float* cos_t, const float* sin_t, const float* mask,
                           int valid_keys, const int* blocks, int count, float* prediction)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
-    if (!ctx->heads.loaded) return fail(ctx, ERNIE_ERROR, "heads are not loaded");
+    if (ctx->heads.parts != (ERNIE_HEAD_INPUT | ERNIE_HEAD_OUTPUT))
+        return fail(ctx, ERNIE_ERROR, "the input and output heads are not both loaded");
     const int D = ctx->heads.dim, S = hw + text_tokens;
     if (!blocks || count < 1 || count > 36) return fail(ctx, ERNIE_ERROR, "Expected 1..36 blocks");
     for (int i = 0; i < count; ++i) {
@@ -1700,6 +1833,7 @@ int ernie_hip_dit_forward(ernie_hip_ctx* ctx, const float* latent, int hw, const
 // ---- profiling ------------------------------------------------------------------------------
 int ernie_hip_profile_enable(ernie_hip_ctx* ctx, int enable)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     if (!enable) {
         int rc = collect(ctx);
@@ -1712,6 +1846,7 @@ int ernie_hip_profile_enable(ernie_hip_ctx* ctx, int enable)
 
 int ernie_hip_profile_classes(ernie_hip_ctx* ctx, unsigned class_mask)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     ctx->profile_mask = class_mask;
     return ERNIE_OK;
@@ -1719,6 +1854,7 @@ int ernie_hip_profile_classes(ernie_hip_ctx* ctx, unsigned class_mask)
 
 int ernie_hip_profile_stride(ernie_hip_ctx* ctx, int stride)
 {
+    DeviceGuard guard(ctx);
     if (!ctx || stride < 1) return ERNIE_ERROR;
     ctx->profile_stride = stride;
     for (long& n : ctx->class_seen) n = 0;
@@ -1729,6 +1865,7 @@ int ernie_hip_profile_collect(ernie_hip_ctx* ctx) { return ctx ? collect(ctx) : 
 
 int ernie_hip_profile_reset(ernie_hip_ctx* ctx)
 {
+    DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     int rc = collect(ctx);
     for (int i = 0; i < ERNIE_PROFILE_CLASSES; ++i) {
@@ -1746,6 +1883,67 @@ int ernie_hip_profile_query(const ernie_hip_ctx* ctx, int cls, long* launches, d
     if (flop) *flop = ctx->flop[cls];
     if (bytes) *bytes = ctx->bytes[cls];
     return ERNIE_OK;
+}
+
+int ernie_hip_mfma_rate(ernie_hip_ctx* ctx, int iters, int launches, double* flop_per_s, double* clock_hz,
+                        double* seconds)
+{
+    DeviceGuard guard(ctx);
+    if (!ctx || iters < 1 || iters > (1 << 24) || launches < 1 || launches > 1000)
+        return fail(ctx, ERNIE_ERROR, "mfma_rate: iters in [1, 2^24] and launches in [1, 1000]");
+    int cus = 0, rtc_khz = 0;
+    int rc = hip_status(ctx, hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device),
+                        "mfma_rate: CU count");
+    if (!rc)
+        rc = hip_status(ctx, hipDeviceGetAttribute(&rtc_khz, hipDeviceAttributeWallClockRate, ctx->device),
+                        "mfma_rate: constant counter rate");
+    if (rc) return rc;
+    if (cus < 1 || rtc_khz < 1) return fail(ctx, ERNIE_ERROR, "mfma_rate: device reports no CUs or counter rate");
+    const size_t waves = mfma_rate_waves(cus);
+    DeviceBuffer sink, stamps;
+    rc = dev_alloc(ctx, sink, (size_t)cus * 512 * sizeof(float), "mfma_rate sink");
+    if (!rc) rc = dev_alloc(ctx, stamps, waves * 4 * sizeof(unsigned long long), "mfma_rate stamps");
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    if (!rc) rc = hip_status(ctx, hipEventCreate(&ev[0]), "mfma_rate event");
+    if (!rc) rc = hip_status(ctx, hipEventCreate(&ev[1]), "mfma_rate event");
+    auto* sk = static_cast<float*>(sink.ptr);
+    auto* st = static_cast<unsigned long long*>(stamps.ptr);
+    // One untimed launch first (clocks ramp, code object loaded).
+    if (!rc) rc = kernel_status(ctx, launch_mfma_rate(cus, iters, sk, st, ctx->stream), "mfma_rate");
+    if (!rc) rc = hip_status(ctx, hipEventRecord(ev[0], ctx->stream), "mfma_rate event");
+    for (int i = 0; i < launches && !rc; ++i)
+        rc = kernel_status(ctx, launch_mfma_rate(cus, iters, sk, st, ctx->stream), "mfma_rate");
+    if (!rc) rc = hip_status(ctx, hipEventRecord(ev[1], ctx->stream), "mfma_rate event");
+    if (!rc) rc = hip_status(ctx, hipEventSynchronize(ev[1]), "mfma_rate");
+    float ms = 0.f;
+    if (!rc) rc = hip_status(ctx, hipEventElapsedTime(&ms, ev[0], ev[1]), "mfma_rate elapsed");
+    std::vector<unsigned long long> h(waves * 4);
+    if (!rc)
+        rc = hip_status(ctx, hipMemcpy(h.data(), st, h.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost),
+                        "mfma_rate stamps");
+    if (!rc) {
+        // Median over the last launch's waves of shader cycles per constant-counter tick.
+        std::vector<double> hz;
+        hz.reserve(waves);
+        for (size_t w = 0; w < waves; ++w) {
+            const unsigned long long dc = h[4 * w + 1] - h[4 * w + 0], dr = h[4 * w + 3] - h[4 * w + 2];
+            if (dr > 0) hz.push_back((double)dc / (double)dr * rtc_khz * 1e3);
+        }
+        if (hz.empty()) {
+            rc = fail(ctx, ERNIE_ERROR, "mfma_rate: no wave recorded a time span");
+        } else {
+            std::nth_element(hz.begin(), hz.begin() + hz.size() / 2, hz.end());
+            if (clock_hz) *clock_hz = hz[hz.size() / 2];
+            const double s = ms * 1e-3;
+            if (seconds) *seconds = s;
+            if (flop_per_s) *flop_per_s = s > 0 ? mfma_rate_flop(cus, iters) * launches / s : 0.0;
+        }
+    }
+    for (hipEvent_t e : ev)
+        if (e) (void)hipEventDestroy(e);
+    dev_free(sink);
+    dev_free(stamps);
+    return rc;
 }
 
 }  // extern "C"

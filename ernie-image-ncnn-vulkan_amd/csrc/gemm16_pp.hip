@@ -991,7 +991,9 @@ __global__ void __launch_bounds__(512, 1) kernel(Params p)
 
 }  // namespace pingpong
 
-// CUs of the current device, rounded down to a multiple of 8 (one per XCD slot).
+// CUs of the current device, rounded down to a multiple of 8 (one per XCD slot). Every
+// extern "C" entry point makes its context's device current first, so this is the CU
+// count of the device the launch goes to.
 static int cu_count()
 {
     static int cached[64] = {};

@@ -150,4 +150,12 @@ int tile_k32(const void* in, void* out, int rows, int cols, hipStream_t s, int h
 // Up or gate matrix [rows][cols] (dtype in_dt) -> its rows of the interleaved W_ug (parity 0 = up).
 int interleave_up_gate(const void* in, int in_dt, void* out, int dt, int rows, int cols, int parity, hipStream_t s);
 
+// Matrix-core issue-rate probe (mfma_rate.hip): `workgroups` of 512 threads, each wave
+// `iters` iterations of 8 independent v_mfma_f32_16x16x32_f16 from registers. sink holds
+// workgroups * 512 floats; stamps 4 u64 per wave (s_memtime start / end, s_memrealtime
+// start / end).
+size_t mfma_rate_waves(int workgroups);
+double mfma_rate_flop(int workgroups, int iters);
+int launch_mfma_rate(int workgroups, int iters, float* sink, unsigned long long* stamps, hipStream_t stream);
+
 }  // namespace ehip

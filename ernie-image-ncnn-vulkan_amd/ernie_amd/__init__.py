@@ -133,6 +133,11 @@ def hip():
             "ernie_hip_profile_reset": (c_int, [c_vp]),
             "ernie_hip_profile_query": (c_int, [c_vp, c_int, ctypes.POINTER(c_long), ctypes.POINTER(c_double),
                                                 ctypes.POINTER(c_double), ctypes.POINTER(c_double)]),
+            "ernie_hip_heads_upload_tensors": (c_int, [c_vp, c_vp, c_int, c_int, c_int, c_int, c_int]),
+            "ernie_hip_heads_loaded": (c_int, [c_vp]),
+            "ernie_hip_set_qk_rounding": (c_int, [c_vp, c_int]),
+            "ernie_hip_mfma_rate": (c_int, [c_vp, c_int, c_int, ctypes.POINTER(c_double), ctypes.POINTER(c_double),
+                                            ctypes.POINTER(c_double)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -218,6 +223,12 @@ def facade():
             "ernie_block_file_inspect": (c_int, [cp, cp, c_int, cp, ctypes.POINTER(BlockFileInfo), cp, c_size_t]),
             "ernie_block_load": (c_int, [c_vp, c_int, cp, cp, c_int, c_int, cp, ctypes.POINTER(BlockFileInfo), cp,
                                          c_size_t]),
+            "ernie_head_file_inspect": (c_int, [cp, cp, c_int, cp, ctypes.POINTER(HeadFileInfo), cp, c_size_t]),
+            "ernie_head_load": (c_int, [c_vp, cp, cp, c_int, c_int, cp, ctypes.POINTER(HeadFileInfo), cp, c_size_t]),
+            "ernie_text_block_file_inspect": (c_int, [cp, cp, c_int, cp, ctypes.POINTER(TextBlockFileInfo), cp,
+                                                      c_size_t]),
+            "ernie_text_block_load": (c_int, [c_vp, c_int, cp, cp, c_int, c_int, cp,
+                                              ctypes.POINTER(TextBlockFileInfo), cp, c_size_t]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -368,6 +379,72 @@ def sha256_hex(data):
 
 def _path(p):
     return None if p is None else str(p).encode()
+
+
+HEAD_INPUT, HEAD_OUTPUT = 1, 2
+HEAD_SECTIONS = {HEAD_INPUT: ("conv_1", "conv_1.bias", "gemm_0", "linear_2", "linear_2.bias", "linear_3",
+                              "linear_3.bias", "linear_4", "linear_4.bias"),
+                 HEAD_OUTPUT: ("linear_2", "linear_2.bias", "gemm_0", "gemm_0.bias")}
+TEXT_WEIGHT_LAYERS = ("rmsn_8", "gemm_0", "gemm_1", "gemm_2", "gemm_3", "rmsn_9", "gemm_4", "gemm_5", "gemm_6")
+
+
+def _sections(info, names):
+    return [{"layer": names[i], "dtype": info.section_dtype[i], "begin": info.section_begin[i],
+             "data": info.section_data[i], "end": info.section_end[i]} for i in range(info.section_count)]
+
+
+class HeadFileInfo(ctypes.Structure):
+    """ernie_head_file_info (include/ernie.h)."""
+    _fields_ = [("part", c_int), ("dim", c_int), ("latent_ch", c_int), ("text_dim", c_int), ("text_tokens", c_int),
+                ("image_tokens", c_int), ("tokens", c_int), ("width", c_int), ("height", c_int),
+                ("reviewed", c_int), ("contract_sha256", ctypes.c_char * 65), ("bin_bytes", c_size_t),
+                ("section_count", c_int), ("section_dtype", c_int * 9), ("section_begin", c_size_t * 9),
+                ("section_data", c_size_t * 9), ("section_end", c_size_t * 9)]
+
+    def as_dict(self):
+        d = {k: getattr(self, k) for k in ("part", "dim", "latent_ch", "text_dim", "text_tokens", "image_tokens",
+                                           "tokens", "width", "height", "bin_bytes")}
+        d["reviewed"] = bool(self.reviewed)
+        d["contract_sha256"] = self.contract_sha256.decode()
+        d["sections"] = _sections(self, HEAD_SECTIONS.get(self.part, ()))
+        return d
+
+
+class TextBlockFileInfo(ctypes.Structure):
+    """ernie_text_block_file_info (include/ernie.h)."""
+    _fields_ = [("tokens", c_int), ("hidden", c_int), ("heads", c_int), ("kv_heads", c_int), ("ffn", c_int),
+                ("reviewed", c_int), ("contract_sha256", ctypes.c_char * 65), ("bin_bytes", c_size_t),
+                ("section_count", c_int), ("section_dtype", c_int * 9), ("section_begin", c_size_t * 9),
+                ("section_data", c_size_t * 9), ("section_end", c_size_t * 9)]
+
+    def as_dict(self):
+        d = {k: getattr(self, k) for k in ("tokens", "hidden", "heads", "kv_heads", "ffn", "bin_bytes")}
+        d["reviewed"] = bool(self.reviewed)
+        d["contract_sha256"] = self.contract_sha256.decode()
+        d["sections"] = _sections(self, TEXT_WEIGHT_LAYERS)
+        return d
+
+
+def head_file_inspect(param_path, bin_path=None, allow_unreviewed=False, expected_bin_sha256=None):
+    """Checks a DiT head.ncnn.param (and walks head.ncnn.bin when given) without a device."""
+    info = HeadFileInfo()
+    e = _err()
+    rc = facade().ernie_head_file_inspect(_path(param_path), _path(bin_path), int(bool(allow_unreviewed)),
+                                          _path(expected_bin_sha256), ctypes.byref(info), e, 512)
+    if rc:
+        _raise(rc, e.value)
+    return info.as_dict()
+
+
+def text_block_file_inspect(param_path, bin_path=None, allow_unreviewed=False, expected_bin_sha256=None):
+    """Checks a text.ncnn.param (and walks text.ncnn.bin when given) without a device."""
+    info = TextBlockFileInfo()
+    e = _err()
+    rc = facade().ernie_text_block_file_inspect(_path(param_path), _path(bin_path), int(bool(allow_unreviewed)),
+                                                _path(expected_bin_sha256), ctypes.byref(info), e, 512)
+    if rc:
+        _raise(rc, e.value)
+    return info.as_dict()
 
 
 def block_file_inspect(param_path, bin_path=None, allow_unreviewed=False, expected_bin_sha256=None):
@@ -547,6 +624,22 @@ class Context:
         arr = (c_vp * len(fields))(*[a.ctypes.data for a in keep])
         self.call("heads_upload", ctypes.cast(arr, c_vp), dim, latent_ch, text_dim, dtype)
 
+    HEAD_FIELDS = ("x_w", "x_b", "text_w", "t1_w", "t1_b", "t2_w", "t2_b", "mod_w", "mod_b", "out_mod_w",
+                   "out_mod_b", "proj_w", "proj_b")
+
+    def heads_upload_tensors(self, tensors, dim, latent_ch, text_dim, dtype, parts=3):
+        """ernie_hip_heads_upload_tensors: tensors maps HEAD_FIELDS names to (numpy array, element dtype) (FP16 /
+        BF16 arrays hold raw uint16 bits); the fields of a part not in `parts` may be absent."""
+        import numpy as np
+        keep = {f: np.ascontiguousarray(tensors[f][0]) for f in self.HEAD_FIELDS if f in tensors}
+        arr = (HostTensor * len(self.HEAD_FIELDS))(*[
+            HostTensor(keep[f].ctypes.data, tensors[f][1]) if f in keep else HostTensor(None, FP32)
+            for f in self.HEAD_FIELDS])
+        self.call("heads_upload_tensors", ctypes.cast(arr, c_vp), dim, latent_ch, text_dim, dtype, parts)
+
+    def heads_loaded(self):
+        return self.L.ernie_hip_heads_loaded(self.ctx)
+
     def heads_init_random(self, dim, latent_ch, text_dim, dtype, seed, std=0.02):
         self.call("heads_init_random", dim, latent_ch, text_dim, dtype, seed, std)
 
@@ -581,6 +674,13 @@ class Context:
             self.call("profile_query", i, ctypes.byref(n), ctypes.byref(ms), ctypes.byref(fl), ctypes.byref(by))
             out[name] = {"launches": n.value, "ms": ms.value, "flop": fl.value, "bytes": by.value}
         return out
+
+    def mfma_rate(self, iters=4096, launches=10):
+        """The device's measured dense FP16 MFMA ceiling (ernie_hip_mfma_rate): FLOP/s over
+        `launches` timed launches, their seconds, and the shader clock in Hz."""
+        f, hz, s = c_double(), c_double(), c_double()
+        self.call("mfma_rate", iters, launches, ctypes.byref(f), ctypes.byref(hz), ctypes.byref(s))
+        return {"flop_per_s": f.value, "clock_hz": hz.value, "seconds": s.value}
 
 
 class Facade:
@@ -632,6 +732,27 @@ class Facade:
         rc = self.L.ernie_block_load(self.dev, index, _path(param_path), _path(bin_path), dtype,
                                      int(bool(allow_unreviewed)), _path(expected_bin_sha256), ctypes.byref(info), e,
                                      512)
+        if rc:
+            _raise(rc, e.value)
+        return info.as_dict()
+
+    def head_load(self, param_path, bin_path, dtype, allow_unreviewed=False, expected_bin_sha256=None):
+        """Loads a DiT head.ncnn.param + head.ncnn.bin (input or output head, as the graph says)."""
+        info = HeadFileInfo()
+        e = _err()
+        rc = self.L.ernie_head_load(self.dev, _path(param_path), _path(bin_path), dtype, int(bool(allow_unreviewed)),
+                                    _path(expected_bin_sha256), ctypes.byref(info), e, 512)
+        if rc:
+            _raise(rc, e.value)
+        return info.as_dict()
+
+    def text_block_load(self, index, param_path, bin_path, dtype, allow_unreviewed=False, expected_bin_sha256=None):
+        """Loads text.ncnn.param + text.ncnn.bin into resident text block slot `index`."""
+        info = TextBlockFileInfo()
+        e = _err()
+        rc = self.L.ernie_text_block_load(self.dev, index, _path(param_path), _path(bin_path), dtype,
+                                          int(bool(allow_unreviewed)), _path(expected_bin_sha256),
+                                          ctypes.byref(info), e, 512)
         if rc:
             _raise(rc, e.value)
         return info.as_dict()

@@ -128,43 +128,49 @@ std::string component_hash(const std::string& text, int tokens)
     return sha256_hex(canon.data(), canon.size());
 }
 
-// Runtime form (src/shape_graph.cpp:23-27,64-95, kind "dit"): in each listed
-// node exactly one parameter with the key, equal to <key>=<tokens>, becomes
-// <key>=TOTAL_TOKENS; all thirteen must be present. Empty otherwise.
+// Runtime form (src/shape_graph.cpp:23-27,64-95, kind "dit"): the token field of the
+// seven Gemms and six reshapes becomes TOTAL_TOKENS.
 std::string runtime_hash(const std::string& text, int tokens)
 {
-    static const std::map<std::string, std::string> rules = {
-        {"gemm_0", "7"},     {"gemm_1", "7"},     {"gemm_2", "7"},     {"gemm_3", "7"},       {"gemm_4", "7"},
-        {"gemm_5", "7"},     {"gemm_6", "7"},     {"reshape_12", "2"}, {"reshape_13", "2"},   {"reshape_14", "2"},
-        {"reshape_15", "1"}, {"unsqueeze_20", "1"}, {"unsqueeze_21", "1"}};
     const std::string t = std::to_string(tokens);
+    std::vector<ShapeField> fields;
+    for (const char* node : {"gemm_0", "gemm_1", "gemm_2", "gemm_3", "gemm_4", "gemm_5", "gemm_6"})
+        fields.push_back({node, "7", "TOTAL_TOKENS", t});
+    for (const char* node : {"reshape_12", "reshape_13", "reshape_14"}) fields.push_back({node, "2", "TOTAL_TOKENS", t});
+    for (const char* node : {"reshape_15", "unsqueeze_20", "unsqueeze_21"})
+        fields.push_back({node, "1", "TOTAL_TOKENS", t});
+    return shape_contract_sha256(text, fields);
+}
+
+}  // namespace
+
+std::string shape_contract_sha256(const std::string& text, const std::vector<ShapeField>& fields)
+{
     std::string canon;
     size_t seen = 0;
     for (const std::string& line : split_lines(text)) {
         std::vector<std::string> f = split_fields(line);
         if (f.size() > 1) {
-            const auto rule = rules.find(f[1]);
-            if (rule != rules.end()) {
+            for (const ShapeField& field : fields) {
+                if (f[1] != field.node) continue;
                 if (f.size() < 6) return "";
                 const size_t start = 4 + (size_t)std::atol(f[2].c_str()) + (size_t)std::atol(f[3].c_str());
                 size_t index = 0, count = 0;
                 for (size_t i = start; i < f.size(); ++i)
-                    if (f[i].substr(0, f[i].find('=')) == rule->second) {
+                    if (f[i].substr(0, f[i].find('=')) == field.key) {
                         index = i;
                         ++count;
                     }
-                if (count != 1 || f[index] != rule->second + "=" + t) return "";
-                f[index] = rule->second + "=TOTAL_TOKENS";
+                if (count != 1 || f[index] != std::string(field.key) + "=" + field.value) return "";
+                f[index] = std::string(field.key) + "=" + field.name;
                 ++seen;
             }
         }
         canon += join(f) + "\n";
     }
-    if (seen != rules.size()) return "";
+    if (seen != fields.size()) return "";
     return sha256_hex(canon.data(), canon.size());
 }
-
-}  // namespace
 
 const std::string* GraphLayer::param(const std::string& key) const
 {
@@ -299,43 +305,73 @@ BlockGraph inspect_block_graph(const std::string& text, bool allow_unreviewed)
     return bg;
 }
 
+WeightSection tagged_section(const std::string& layer, const unsigned char* bin, size_t size, size_t offset,
+                             size_t count)
+{
+    WeightSection s;
+    s.layer = layer;
+    s.count = count;
+    s.begin = offset;
+    if (offset > size || size - offset < 4) bad("weight file ends inside the tag of " + layer);
+    const unsigned tag = (unsigned)bin[offset] | (unsigned)bin[offset + 1] << 8 | (unsigned)bin[offset + 2] << 16 |
+                         (unsigned)bin[offset + 3] << 24;
+    s.data = offset + 4;
+    if (tag == kTagFp32) {
+        s.dtype = ERNIE_DTYPE_FP32;
+        s.end = s.data + 4 * count;
+    } else if (tag == kTagBf16 || tag == kTagFp16) {
+        s.dtype = tag == kTagBf16 ? ERNIE_DTYPE_BF16 : ERNIE_DTYPE_FP16;
+        s.end = s.data + (2 * count + 3) / 4 * 4;
+    } else {
+        char buf[96];
+        std::snprintf(buf, sizeof(buf), "unsupported ModelBin storage tag 0x%08x in %s", tag, layer.c_str());
+        bad(buf);
+    }
+    if (s.end > size) bad("weight file is truncated inside " + layer);
+    return s;
+}
+
+WeightSection raw_section(const std::string& layer, size_t size, size_t offset, size_t count)
+{
+    WeightSection s;
+    s.layer = layer;
+    s.count = count;
+    s.dtype = ERNIE_DTYPE_FP32;
+    s.begin = s.data = offset;
+    s.end = offset + 4 * count;
+    if (offset > size || s.end > size) bad("weight file is truncated inside " + layer);
+    return s;
+}
+
+void check_sections_end(const std::vector<WeightSection>& sections, size_t size)
+{
+    const size_t off = sections.empty() ? 0 : sections.back().end;
+    if (off != size) bad("weight file holds " + std::to_string(size - off) + " bytes beyond the component's sections");
+}
+
+void check_bin_sha256(const unsigned char* bin, size_t size, const std::string& expected, std::string* digest)
+{
+    if (expected.empty()) return;
+    const std::string got = sha256_hex(bin, size);
+    if (digest) *digest = got;
+    if (got != lower(expected)) bad("weight file checksum mismatch: " + got);
+}
+
 std::vector<WeightSection> block_sections(const BlockGraph& g, const unsigned char* bin, size_t size)
 {
     std::vector<WeightSection> out;
     size_t off = 0;
     for (const GraphLayer& l : g.graph.layers) {
         if (l.type != "RMSNorm" && l.type != "Gemm") continue;
-        WeightSection s;
-        s.layer = l.name;
-        s.begin = off;
-        if (l.type == "RMSNorm") {
-            s.count = (size_t)std::atol(l.param("0")->c_str());
-            s.dtype = ERNIE_DTYPE_FP32;
-            s.data = off;
-            s.end = off + 4 * s.count;
-        } else {
-            s.count = (size_t)std::atol(l.param("8")->c_str()) * (size_t)std::atol(l.param("9")->c_str());
-            if (size - off < 4) bad("weight file ends inside the tag of " + l.name);
-            const unsigned tag = (unsigned)bin[off] | (unsigned)bin[off + 1] << 8 | (unsigned)bin[off + 2] << 16 |
-                                 (unsigned)bin[off + 3] << 24;
-            s.data = off + 4;
-            if (tag == kTagFp32) {
-                s.dtype = ERNIE_DTYPE_FP32;
-                s.end = s.data + 4 * s.count;
-            } else if (tag == kTagBf16 || tag == kTagFp16) {
-                s.dtype = tag == kTagBf16 ? ERNIE_DTYPE_BF16 : ERNIE_DTYPE_FP16;
-                s.end = s.data + (2 * s.count + 3) / 4 * 4;
-            } else {
-                char buf[96];
-                std::snprintf(buf, sizeof(buf), "unsupported ModelBin storage tag 0x%08x in %s", tag, l.name.c_str());
-                bad(buf);
-            }
-        }
-        if (s.end > size) bad("weight file is truncated inside " + l.name);
-        off = s.end;
-        out.push_back(s);
+        if (l.type == "RMSNorm")
+            out.push_back(raw_section(l.name, size, off, (size_t)std::atol(l.param("0")->c_str())));
+        else
+            out.push_back(tagged_section(l.name, bin, size, off,
+                                         (size_t)std::atol(l.param("8")->c_str()) *
+                                             (size_t)std::atol(l.param("9")->c_str())));
+        off = out.back().end;
     }
-    if (off != size) bad("weight file holds " + std::to_string(size - off) + " bytes beyond the block's sections");
+    check_sections_end(out, size);
     return out;
 }
 
@@ -388,10 +424,7 @@ BlockFile inspect_block_bytes(const std::string& param_path, const unsigned char
         return f;
     }
     f.bin_bytes = size;
-    if (!expected_bin_sha256.empty()) {
-        f.bin_sha256 = sha256_hex(bin, size);
-        if (f.bin_sha256 != lower(expected_bin_sha256)) bad("weight file checksum mismatch: " + f.bin_sha256);
-    }
+    check_bin_sha256(bin, size, expected_bin_sha256, &f.bin_sha256);
     f.sections = block_sections(f.graph, bin, size);
     return f;
 }

@@ -2,12 +2,14 @@
 // C entry points over the C++ facade (declared in include/ernie.h).
 #include "ernie.h"
 
+#include <algorithm>
 #include <cstring>
 #include <exception>
 #include <stdexcept>
 #include <string>
 
 #include "ernie/block_files.h"
+#include "ernie/component_files.h"
 #include "ernie/conditioning.h"
 #include "ernie/denoiser.h"
 #include "ernie/dit.h"
@@ -79,6 +81,53 @@ void fill_info(ernie_block_file_info* info, const ernie::BlockFile& f)
         info->section_data[i] = f.sections[i].data;
         info->section_end[i] = f.sections[i].end;
     }
+}
+
+template <class Info, class File>
+void fill_sections(Info* info, const File& f, size_t max)
+{
+    info->bin_bytes = f.bin_bytes;
+    info->section_count = static_cast<int>(std::min(f.sections.size(), max));
+    for (size_t i = 0; i < f.sections.size() && i < max; ++i) {
+        info->section_dtype[i] = f.sections[i].dtype;
+        info->section_begin[i] = f.sections[i].begin;
+        info->section_data[i] = f.sections[i].data;
+        info->section_end[i] = f.sections[i].end;
+    }
+}
+
+void fill_head_info(ernie_head_file_info* info, const ernie::HeadFile& f)
+{
+    if (!info) return;
+    std::memset(info, 0, sizeof(*info));
+    const auto& g = f.graph;
+    info->part = static_cast<int>(g.kind);
+    info->dim = g.dim;
+    info->latent_ch = g.latent_ch;
+    info->text_dim = g.text_dim;
+    info->text_tokens = g.text_tokens;
+    info->image_tokens = g.image_tokens;
+    info->tokens = g.tokens;
+    info->width = g.width;
+    info->height = g.height;
+    info->reviewed = g.reviewed;
+    std::strncpy(info->contract_sha256, g.contract_sha256.c_str(), 64);
+    fill_sections(info, f, 9);
+}
+
+void fill_text_info(ernie_text_block_file_info* info, const ernie::TextBlockFile& f)
+{
+    if (!info) return;
+    std::memset(info, 0, sizeof(*info));
+    const auto& g = f.graph;
+    info->tokens = g.tokens;
+    info->hidden = g.hidden;
+    info->heads = g.heads;
+    info->kv_heads = g.kv_heads;
+    info->ffn = g.ffn;
+    info->reviewed = g.reviewed;
+    std::strncpy(info->contract_sha256, g.contract_sha256.c_str(), 64);
+    fill_sections(info, f, 9);
 }
 
 ernie::Option option_for(const ernie::Device& d, int dtype)
@@ -296,7 +345,10 @@ int ernie_denoise_observed(ernie_device* device, const int* blocks, int count, f
 {
     return guarded(err, errlen, [&]() -> int {
         if (!device || !blocks || count < 0) throw std::invalid_argument("null denoise argument");
+        const auto& d = device->device;
         ernie::DenoiseModel model;
+        model.input_head = ernie::resident_head(d, ERNIE_HEAD_INPUT);
+        model.output_head = ernie::resident_head(d, ERNIE_HEAD_OUTPUT);
         for (int i = 0; i < count; ++i) model.blocks.push_back({blocks[i]});
         const int S = height * width + text_tokens;
         ernie::DeviceMat m = mask ? wrap(mask, S) : ernie::DeviceMat{};
@@ -305,7 +357,6 @@ int ernie_denoise_observed(ernie_device* device, const int* blocks, int count, f
             text_tokens ? wrap(text, 3072, text_tokens, 1, 2) : ernie::DeviceMat{}, wrap(cos_t, 128, S),
             wrap(sin_t, 128, S), m};
         std::vector<ernie::DenoiseStepStats> stats;
-        const auto& d = device->device;
         ernie::StepObserver step_observer;
         if (observer)
             step_observer = [&](size_t step, const ernie::DeviceMat& prediction, const ernie::DeviceMat& sample) {
@@ -345,7 +396,10 @@ int ernie_run_dit(ernie_device* device, const int* blocks, int count, const floa
     return guarded(err, errlen, [&]() -> int {
         if (!device || !blocks || count < 0 || !latent || !time_features || !prediction || dim < 1)
             throw std::invalid_argument("null run_dit argument");
+        const auto& d = device->device;
         ernie::DitModel model;
+        model.input_head = ernie::resident_head(d, ERNIE_HEAD_INPUT);
+        model.output_head = ernie::resident_head(d, ERNIE_HEAD_OUTPUT);
         for (int i = 0; i < count; ++i) model.blocks.push_back({blocks[i]});
         const int S = height * width + text_tokens;
         ernie::DeviceMat m = mask ? wrap(mask, S) : ernie::DeviceMat{};
@@ -360,7 +414,6 @@ int ernie_run_dit(ernie_device* device, const int* blocks, int count, const floa
             stage_observer = [&](const std::string& stage, const ernie::DeviceMat& t) {
                 observer(stage.c_str(), t.data, t.w, t.h, t.c, user);
             };
-        const auto& d = device->device;
         const auto result = ernie::run_dit(model, inputs, option_for(d, storage_dtype), stats, stage_observer);
         ernie::check_status(ernie_hip_convert(d.ctx(), result.data, ERNIE_DTYPE_FP32, prediction, ERNIE_DTYPE_FP32,
                                               result.total()),
@@ -402,6 +455,59 @@ int ernie_block_load(ernie_device* device, int index, const char* param_path, co
         const auto f = ernie::load_block_files(device->device, index, param_path, bin_path, storage_dtype,
                                                allow_unreviewed != 0, expected_bin_sha256 ? expected_bin_sha256 : "");
         fill_info(info, f);
+        return ERNIE_OK;
+    });
+}
+
+int ernie_head_file_inspect(const char* param_path, const char* bin_path, int allow_unreviewed,
+                            const char* expected_bin_sha256, ernie_head_file_info* info, char* err, size_t errlen)
+{
+    return guarded(err, errlen, [&]() -> int {
+        if (!param_path) throw std::invalid_argument("null graph path");
+        const auto f = ernie::inspect_head_files(param_path, bin_path ? bin_path : "", allow_unreviewed != 0,
+                                                 expected_bin_sha256 ? expected_bin_sha256 : "");
+        fill_head_info(info, f);
+        return ERNIE_OK;
+    });
+}
+
+int ernie_head_load(ernie_device* device, const char* param_path, const char* bin_path, int storage_dtype,
+                    int allow_unreviewed, const char* expected_bin_sha256, ernie_head_file_info* info, char* err,
+                    size_t errlen)
+{
+    return guarded(err, errlen, [&]() -> int {
+        if (!device || !param_path || !bin_path) throw std::invalid_argument("null head load argument");
+        ernie::HeadFile f;
+        ernie::load_head_files(device->device, param_path, bin_path, storage_dtype, allow_unreviewed != 0,
+                               expected_bin_sha256 ? expected_bin_sha256 : "", &f);
+        fill_head_info(info, f);
+        return ERNIE_OK;
+    });
+}
+
+int ernie_text_block_file_inspect(const char* param_path, const char* bin_path, int allow_unreviewed,
+                                  const char* expected_bin_sha256, ernie_text_block_file_info* info, char* err,
+                                  size_t errlen)
+{
+    return guarded(err, errlen, [&]() -> int {
+        if (!param_path) throw std::invalid_argument("null graph path");
+        const auto f = ernie::inspect_text_block_files(param_path, bin_path ? bin_path : "", allow_unreviewed != 0,
+                                                       expected_bin_sha256 ? expected_bin_sha256 : "");
+        fill_text_info(info, f);
+        return ERNIE_OK;
+    });
+}
+
+int ernie_text_block_load(ernie_device* device, int index, const char* param_path, const char* bin_path,
+                          int storage_dtype, int allow_unreviewed, const char* expected_bin_sha256,
+                          ernie_text_block_file_info* info, char* err, size_t errlen)
+{
+    return guarded(err, errlen, [&]() -> int {
+        if (!device || !param_path || !bin_path) throw std::invalid_argument("null text block load argument");
+        const auto f = ernie::load_text_block_files(device->device, index, param_path, bin_path, storage_dtype,
+                                                    allow_unreviewed != 0,
+                                                    expected_bin_sha256 ? expected_bin_sha256 : "");
+        fill_text_info(info, f);
         return ERNIE_OK;
     });
 }

@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <exception>
 #include <stdexcept>
 
 namespace ernie {
@@ -12,10 +13,26 @@ namespace {
 
 using Clock = std::chrono::steady_clock;
 
+// A latent found non-finite by the step-behind check: the error the reference raises
+// before it starts the next step (src/denoiser.cpp:56-57, 84-86). Kept apart from device
+// failures so the error path below can tell them apart; callers see the base types.
+struct NonFiniteInitial : std::invalid_argument {
+    using std::invalid_argument::invalid_argument;
+};
+struct NonFiniteStep : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+// The facade's own finite-check slots and stream markers (reserved in ernie_hip.h).
+constexpr int kStepSlot = ERNIE_FINITE_SLOTS;           // two, alternating by step
+constexpr int kInitialSlot = ERNIE_FINITE_SLOTS + 2;
+constexpr int kStepMarker = ERNIE_MARKERS;              // three, rotating by step
+
 // src/denoiser.cpp:12-19.
 void check_request(const DenoiseModel& model, const DeviceMat& initial, size_t constants)
 {
-    if (model.blocks.empty() || model.blocks.size() > 36 || constants != 4 || initial.empty() || initial.dims != 3 ||
+    if (model.input_head.part != ERNIE_HEAD_INPUT || model.output_head.part != ERNIE_HEAD_OUTPUT ||
+        model.blocks.empty() || model.blocks.size() > 36 || constants != 4 || initial.empty() || initial.dims != 3 ||
         initial.c != 128 || initial.w < 1 || initial.h < 1 || initial.w > 256 || initial.h > 256)
         throw std::invalid_argument("Require heads, 1..36 blocks, four constants and a pack1 FP32 latent");
 }
@@ -71,12 +88,11 @@ DeviceMat denoise(const DenoiseModel& model, const DeviceMat& initial, const std
     // The initial latent's check is read once step 0's DiT is queued (the reference
     // rejects a non-finite initial latent before any step, src/denoiser.cpp:56-57; here
     // the queued work of that step is simply dropped).
-    constexpr int kInitialSlot = 2;
     check_status(ernie_hip_finite_begin(ctx, sample.data, sample.total(), kInitialSlot), ctx, "Latent finite check");
     auto check_initial = [&]() {
         int finite = 0;
         check_status(ernie_hip_finite_end(ctx, kInitialSlot, &finite), ctx, "Latent finite check");
-        if (!finite) throw std::invalid_argument("Initial latent is not finite");
+        if (!finite) throw NonFiniteInitial("Initial latent is not finite");
     };
 
     // Each step is queued without a wait. Its finiteness flag is read one step behind:
@@ -85,13 +101,14 @@ DeviceMat denoise(const DenoiseModel& model, const DeviceMat& initial, const std
     // observer still sees its prediction and sample (step i + 1's Euler update, which
     // replaces the sample, is queued after the check). elapsed_seconds is the device
     // time from the end of the previous step (or the loop start) to the end of this one,
-    // from stream markers 0..2.
+    // from the facade's three step markers.
     struct Pending {
         size_t stat;
         int step, slot, mark_from, mark_to;
         DeviceMat prediction;
     };
     std::vector<Pending> pending;
+    bool in_observer = false;  // set while the observer runs inside resolve()
     auto resolve = [&]() {
         Pending p = pending.back();
         pending.clear();
@@ -101,13 +118,17 @@ DeviceMat denoise(const DenoiseModel& model, const DeviceMat& initial, const std
         check_status(ernie_hip_marker_elapsed(ctx, p.mark_from, p.mark_to, &seconds), ctx, "Step timing");
         DenoiseStepStats& st = stats[p.stat];
         st.elapsed_seconds = seconds;
-        if (!finite) throw std::runtime_error("Non-finite latent after denoise step " + std::to_string(p.step + 1));
+        if (!finite) throw NonFiniteStep("Non-finite latent after denoise step " + std::to_string(p.step + 1));
         st.complete = true;
-        if (observer) observer(size_t(p.step), p.prediction, sample);
+        if (observer) {
+            in_observer = true;
+            observer(size_t(p.step), p.prediction, sample);
+            in_observer = false;
+        }
     };
 
-    check_status(ernie_hip_marker_record(ctx, 0), ctx, "Step timing");
-    DitModel dit{model.blocks};
+    check_status(ernie_hip_marker_record(ctx, kStepMarker), ctx, "Step timing");
+    DitModel dit{model.input_head, model.blocks, model.output_head};
     for (int i = start_step; i < steps; ++i) {
         const int k = i - start_step;
         const auto start = Clock::now();
@@ -121,21 +142,33 @@ DeviceMat denoise(const DenoiseModel& model, const DeviceMat& initial, const std
                                                 constants[1], constants[2], constants[3]};
             prediction = run_dit(dit, inputs, option, step.dit);
         } catch (...) {
-            // An earlier failure comes first (check_initial / resolve throw it); else this one's.
-            if (k == 0) check_initial();
-            if (!pending.empty()) resolve();
+            // The reference finishes each step (finite check, observer) before it starts the
+            // next, so what that would have raised first wins: a non-finite earlier latent,
+            // or the observer's own exception. A device error met while reading the earlier
+            // check gives way to this step's failure, which is rethrown as it was raised.
+            const std::exception_ptr failure = std::current_exception();
+            try {
+                if (k == 0) check_initial();
+                if (!pending.empty()) resolve();
+            } catch (const NonFiniteInitial&) {
+                throw;
+            } catch (const NonFiniteStep&) {
+                throw;
+            } catch (...) {
+                if (in_observer) throw;
+            }
             step.elapsed_seconds = std::chrono::duration<double>(Clock::now() - start).count();
             stats.push_back(step);
-            throw;
+            std::rethrow_exception(failure);
         }
         if (k == 0) check_initial();
         if (!pending.empty()) resolve();
         euler_step(device, sample, prediction, step.delta, sample);
-        const int slot = k % 2;
+        const int slot = kStepSlot + k % 2;
         check_status(ernie_hip_finite_begin(ctx, sample.data, sample.total(), slot), ctx, "Latent finite check");
-        check_status(ernie_hip_marker_record(ctx, (k + 1) % 3), ctx, "Step timing");
+        check_status(ernie_hip_marker_record(ctx, kStepMarker + (k + 1) % 3), ctx, "Step timing");
         stats.push_back(step);
-        pending.push_back({stats.size() - 1, i, slot, k % 3, (k + 1) % 3, prediction});
+        pending.push_back({stats.size() - 1, i, slot, kStepMarker + k % 3, kStepMarker + (k + 1) % 3, prediction});
         if (k + 1 < executed) upload_features(k + 1);
     }
     resolve();

@@ -16,9 +16,14 @@
 namespace ernie {
 namespace {
 
-// Stream markers of a timed DiT: before the input head, after it, after the blocks,
-// after the output head.
-enum { kMarkStart = 60, kMarkHead = 61, kMarkBlocks = 62, kMarkEnd = 63 };
+// Stream markers of a timed DiT, from the facade's reserved range (the denoise loop has
+// the first three): before the input head, after it, after the blocks, after the output head.
+enum {
+    kMarkStart = ERNIE_MARKERS + 3,
+    kMarkHead = ERNIE_MARKERS + 4,
+    kMarkBlocks = ERNIE_MARKERS + 5,
+    kMarkEnd = ERNIE_MARKERS + 6
+};
 
 double marker_seconds(ernie_hip_ctx* ctx, int from, int to)
 {
@@ -33,6 +38,8 @@ DeviceMat run_dit(const DitModel& model, const std::vector<DeviceMat>& inputs, c
                   const StageObserver& observer)
 {
     if (inputs.size() != 6 || !option.device) throw std::invalid_argument("Require six device DiT inputs and a device");
+    if (model.input_head.part != ERNIE_HEAD_INPUT || model.output_head.part != ERNIE_HEAD_OUTPUT)
+        throw std::invalid_argument("Require the input and output heads");
     if (model.blocks.empty() || model.blocks.size() > 36)
         throw std::invalid_argument("Expected 1..36 blocks and nine shared constants");
     option.dtype();
@@ -92,15 +99,15 @@ DeviceMat run_dit(const DitModel& model, const std::vector<DeviceMat>& inputs, c
     if (collect_details) check_status(ernie_hip_marker_record(ctx, kMarkBlocks), ctx, "DiT timing");
     stats.blocks.peak_loaded_nets = count;
     stats.blocks.compute_submissions = count;
-    // Per-block device time is measured only when details are collected; otherwise no
-    // entry is recorded and a metrics consumer attributes the step's whole time to
-    // compute (as src/pipeline.cpp:56-66 does with what remains unaccounted).
-    if (collect_details)
-        for (int i = 0; i < count; ++i) {
-            stats.blocks.load_seconds.push_back(0.0);
-            stats.blocks.compute_seconds.push_back(seconds[i]);
-            stats.blocks.details.push_back({i, "extract_compute_composite", "complete", seconds[i]});
-        }
+    // One load and one compute entry per block, as the reference records them
+    // (src/block_sequence.cpp:87,252). Blocks are resident, so nothing is loaded; per-block
+    // device time is measured only when details are collected (every block is otherwise
+    // queued without a wait) and reads 0 when it was not.
+    for (int i = 0; i < count; ++i) {
+        stats.blocks.load_seconds.push_back(0.0);
+        stats.blocks.compute_seconds.push_back(seconds[i]);
+        if (collect_details) stats.blocks.details.push_back({i, "extract_compute_composite", "complete", seconds[i]});
+    }
 
     check_status(ernie_hip_output_head(ctx, x.data, S, hw, c.data, prediction.data), ctx, "output head");
     if (collect_details) {

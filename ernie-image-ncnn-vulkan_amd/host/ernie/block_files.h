@@ -33,6 +33,21 @@ struct Graph {
 // and consumed only after it is produced. Throws std::invalid_argument.
 Graph parse_graph(const std::string& text);
 
+// One field of the reference's runtime shape contract (src/shape_graph.cpp:23-31): in
+// the layer named `node`, the one parameter with key `key` must read key=value (this
+// graph's dimension) and becomes key=name (the dimension's upper-case name) in the
+// normalised text.
+struct ShapeField {
+    const char* node;
+    const char* key;
+    const char* name;
+    std::string value;
+};
+// SHA-256 of the graph text normalised by `fields` as src/shape_graph.cpp:52-95 does
+// (whitespace-separated fields joined by one space, one '\n' per line), or "" when a
+// field is missing, repeated or holds another value. A node may carry several fields.
+std::string shape_contract_sha256(const std::string& text, const std::vector<ShapeField>& fields);
+
 // Which reviewed topology a block graph matches once its token count is
 // normalised: the component export checked by tools/build_dit_weights.py:18,34-50
 // (BinaryOp residual adds) or the runtime package checked by
@@ -61,6 +76,20 @@ struct WeightSection {
     size_t data = 0;      // first element
     size_t end = 0;       // one past the section, padding included
 };
+
+// A ModelBin section read with load type 0 (ncnn's tagged form: Gemm, InnerProduct and
+// Convolution weights): a 4-byte tag, 0 = FP32, 0x01348B83 = BF16 or 0x01306B47 = FP16
+// (halves padded to 4 bytes), then `count` elements, starting at byte `offset`. Other tags
+// (quantized sections) and truncation throw std::invalid_argument.
+WeightSection tagged_section(const std::string& layer, const unsigned char* bin, size_t size, size_t offset,
+                             size_t count);
+// A section read with load type 1: `count` raw FP32 values (RMSNorm gammas, biases).
+WeightSection raw_section(const std::string& layer, size_t size, size_t offset, size_t count);
+// Throws unless the last section ends exactly at `size` (no trailing bytes).
+void check_sections_end(const std::vector<WeightSection>& sections, size_t size);
+// Compares the SHA-256 of the bytes with a non-empty `expected` (hex, any case) and
+// throws std::invalid_argument on a mismatch; `digest` (nullable) receives the hash.
+void check_bin_sha256(const unsigned char* bin, size_t size, const std::string& expected, std::string* digest);
 
 // Walks a block's weight bytes in graph order. RMSNorm gammas are raw FP32;
 // each Gemm section starts with a 4-byte tag: 0 = FP32, 0x01348B83 = BF16 and

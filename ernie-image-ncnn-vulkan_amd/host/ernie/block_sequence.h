@@ -23,7 +23,7 @@ struct BlockModel {
 struct BlockSequenceStats {
     struct Detail { int block = -1; std::string boundary, status; double seconds = 0; };
     std::vector<double> load_seconds;
-    std::vector<double> compute_seconds;  // device time per block (HIP events)
+    std::vector<double> compute_seconds;  // device time per block (HIP events; 0 when run_dit does not collect details)
     int peak_loaded_nets = 0;
     int compute_submissions = 0;
     bool collect_details = false;

@@ -12,8 +12,11 @@ namespace ernie {
 // src/denoiser.cpp:22-39. Throws std::invalid_argument outside [0,1000].
 std::vector<float> timestep_features(float timestep);
 
+// src/denoiser.h:13-17: the two head components and the blocks, here resident in the
+// device context.
 struct DenoiseModel {
-    std::vector<BlockModel> blocks;  // heads are resident in the device context
+    HeadModel input_head, output_head;
+    std::vector<BlockModel> blocks;
 };
 
 struct DenoiseStepStats {

@@ -2,6 +2,7 @@
 // DiT = input head + blocks + output head (src/dit.h:6-40).
 #pragma once
 #include "ernie/block_sequence.h"
+#include "ernie/component_files.h"
 
 namespace ernie {
 
@@ -14,13 +15,17 @@ struct DitStats {
     std::vector<Detail> details;
 };
 
-// Heads are resident in the device context next to the blocks.
+// The argument triple of run_dit (src/dit.h:17-19): input head, blocks, output head,
+// each resident in the device context (load_head_files / resident_head, load_block_files).
 struct DitModel {
+    HeadModel input_head;
     std::vector<BlockModel> blocks;
+    HeadModel output_head;
 };
 
 // inputs: packed latent [128][H][W], text [T][3072], time features [4096],
-// cosine, sine, mask. Returns the prediction [128][H][W].
+// cosine, sine, mask. Returns the prediction [128][H][W]. Throws std::invalid_argument
+// without both heads, 1..36 blocks and six inputs.
 DeviceMat run_dit(const DitModel& model, const std::vector<DeviceMat>& inputs, const Option& option, DitStats& stats,
                   const StageObserver& observer = {});
 

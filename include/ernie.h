@@ -161,6 +161,55 @@ int ernie_block_load(ernie_device* device, int index, const char* param_path, co
                      int storage_dtype, int allow_unreviewed, const char* expected_bin_sha256,
                      ernie_block_file_info* info, char* err, size_t errlen);
 
+/* ---- on-disk DiT heads (heads/input, heads/output head.ncnn.{param,bin}) ----------- */
+typedef struct {
+    int part;                     /* ERNIE_HEAD_INPUT or ERNIE_HEAD_OUTPUT */
+    int dim, latent_ch;
+    int text_dim, text_tokens;    /* input head: text_proj width and the graph's text slots */
+    int image_tokens, tokens;     /* image tokens; image + text tokens (output head) */
+    int width, height;            /* output head: packed latent grid */
+    int reviewed;                 /* 1 when the graph matches the reviewed runtime contract */
+    char contract_sha256[65];     /* the normalised graph's hash, "" when a contract field is missing */
+    size_t bin_bytes;             /* 0 when no weight file was read */
+    int section_count;            /* 9 (input) or 4 (output) weights and biases, or 0 without a weight file */
+    int section_dtype[9];
+    size_t section_begin[9], section_data[9], section_end[9];
+} ernie_head_file_info;
+/* Checks a head graph (the input or output head of src/dit.cpp:22-45; the reference's
+ * runtime contract of src/shape_graph.cpp:27-31) and, when bin_path is non-NULL, walks its
+ * ModelBin sections: each weight tagged (FP32 0, BF16 0x01348B83, FP16 0x01306B47), each
+ * bias raw FP32. An unreviewed topology is rejected (-22) unless allow_unreviewed. No device. */
+int ernie_head_file_inspect(const char* param_path, const char* bin_path, int allow_unreviewed,
+                            const char* expected_bin_sha256, ernie_head_file_info* info, char* err, size_t errlen);
+/* ernie_head_file_inspect, then uploads the head into the context at storage_dtype
+ * (ernie_hip_heads_upload_tensors with the part the graph declares): replaces the head
+ * Net's load_component (src/dit.cpp:22-45, src/component_files.cpp:37-60). */
+int ernie_head_load(ernie_device* device, const char* param_path, const char* bin_path, int storage_dtype,
+                    int allow_unreviewed, const char* expected_bin_sha256, ernie_head_file_info* info, char* err,
+                    size_t errlen);
+
+/* ---- on-disk Mistral text blocks (text.ncnn.{param,bin}) ------------------------- */
+typedef struct {
+    int tokens, hidden, heads, kv_heads, ffn;
+    int reviewed;                 /* 1 when the graph matches the reviewed runtime contract */
+    char contract_sha256[65];
+    size_t bin_bytes;
+    int section_count;            /* 9, or 0 without a weight file */
+    int section_dtype[9];
+    size_t section_begin[9], section_data[9], section_end[9];
+} ernie_text_block_file_info;
+/* Checks a text block graph (tests/fixtures/text-s64.ncnn.param form; the runtime contract
+ * of src/shape_graph.cpp:25,31) and walks its ModelBin sections (RMSNorm gammas raw FP32,
+ * Gemms tagged, tools/build_text_weights.py:52-74). No device. */
+int ernie_text_block_file_inspect(const char* param_path, const char* bin_path, int allow_unreviewed,
+                                  const char* expected_bin_sha256, ernie_text_block_file_info* info, char* err,
+                                  size_t errlen);
+/* ernie_text_block_file_inspect, then uploads the block into resident text slot `index`:
+ * replaces load_component of a text block Net (src/text_encoder.cpp:30-40). */
+int ernie_text_block_load(ernie_device* device, int index, const char* param_path, const char* bin_path,
+                          int storage_dtype, int allow_unreviewed, const char* expected_bin_sha256,
+                          ernie_text_block_file_info* info, char* err, size_t errlen);
+
 #ifdef __cplusplus
 }
 #endif

@@ -115,6 +115,16 @@ int ernie_hip_sdpa_causal(ernie_hip_ctx* ctx, const void* q, const void* k, cons
 int ernie_hip_set_attention_query_rows(ernie_hip_ctx* ctx, int rows);
 /* attention_internal_submissions (src/ernie_attention.cpp:256-265): always 0 here. */
 uint64_t ernie_hip_attention_internal_submissions(const ernie_hip_ctx* ctx);
+/* Rounding order of the Q/K RMSNorm (rmsn_9 / rmsn_10) in 16-bit DiT blocks. The reference
+ * graph rounds the gemm_0 / gemm_1 outputs to the storage dtype and normalises and rotates
+ * those (block.ncnn.param lines 19-57): ERNIE_QK_ROUND_STORAGE does the same, with a
+ * separate pass after the QKV GEMM. ERNIE_QK_ROUND_FUSED (the default) normalises and
+ * rotates Q and K from the GEMM's FP32 accumulators in its epilogue and rounds once, after
+ * the rotation: one rounding fewer and no extra pass. FP32 blocks are the same either way.
+ * The mode applies to block forwards issued after the call. */
+#define ERNIE_QK_ROUND_FUSED 0
+#define ERNIE_QK_ROUND_STORAGE 1
+int ernie_hip_set_qk_rounding(ernie_hip_ctx* ctx, int mode);
 /* rmsn_9/rmsn_10 + rotary (block.ncnn.param lines 28-57) in place on `heads`
  * heads of 128 values per token at x + t*row_stride + h*128; cos/sin [rows][128].
  * gamma NULL: rotary only (the text block's q/k path, text-s64.ncnn.param lines 18-44). */
@@ -133,6 +143,10 @@ int ernie_hip_finite(ernie_hip_ctx* ctx, const float* x, size_t count, int* fini
  * flag to pinned host memory in `slot`, and _end waits for that copy only (work queued
  * after _begin keeps the device busy meanwhile). One check may be pending per slot. */
 #define ERNIE_FINITE_SLOTS 4
+/* Slots ERNIE_FINITE_SLOTS .. ERNIE_FINITE_SLOTS + 2 belong to the C++ facade (its denoise
+ * loop, ernie/denoiser.h); they are accepted here but a caller that keeps to slots
+ * 0 .. ERNIE_FINITE_SLOTS - 1 never shares a slot with a facade call on the same context. */
+#define ERNIE_FINITE_SLOTS_RESERVED 3
 int ernie_hip_finite_begin(ernie_hip_ctx* ctx, const float* x, size_t count, int slot);
 int ernie_hip_finite_end(ernie_hip_ctx* ctx, int slot, int* finite);
 /* Stream markers: pooled HIP events recorded on the context stream without a wait;
@@ -140,6 +154,9 @@ int ernie_hip_finite_end(ernie_hip_ctx* ctx, int slot, int* finite);
  * stand in for the host clock the reference reads around each synchronous submission
  * (src/denoiser.cpp:104-146, src/block_sequence.cpp:241-253). */
 #define ERNIE_MARKERS 64
+/* Markers ERNIE_MARKERS .. ERNIE_MARKERS + 7 belong to the C++ facade (denoise steps use
+ * the first three, run_dit's stage timing the next four); callers keep to 0 .. 63. */
+#define ERNIE_MARKERS_RESERVED 8
 int ernie_hip_marker_record(ernie_hip_ctx* ctx, int marker);
 int ernie_hip_marker_elapsed(ernie_hip_ctx* ctx, int from, int to, double* seconds);
 /* Counter-based N(mean, std) synthetic data directly in device memory. */
@@ -268,6 +285,27 @@ typedef struct {
 
 int ernie_hip_heads_upload(ernie_hip_ctx* ctx, const ernie_heads_host_weights* w, int dim, int latent_ch,
                            int text_dim, int dtype);
+/* The two head components (src/denoiser.h:13-17 holds them as separate input_head and
+ * output_head ComponentFiles); each can be loaded on its own. */
+#define ERNIE_HEAD_INPUT 1
+#define ERNIE_HEAD_OUTPUT 2
+/* The head tensors, each in the element type it is stored in: the ModelBin sections of
+ * heads/input and heads/output head.ncnn.bin keep Convolution, InnerProduct and Gemm
+ * weights tagged FP32 (BF16 / FP16 also accepted) and their biases raw FP32. */
+typedef struct {
+    ernie_host_tensor x_w, x_b, text_w, t1_w, t1_b, t2_w, t2_b, mod_w, mod_b; /* input head */
+    ernie_host_tensor out_mod_w, out_mod_b, proj_w, proj_b;                   /* output head */
+} ernie_heads_host_tensors;
+/* Replaces load_model of the head Nets (src/dit.cpp:22-45): uploads the parts in `parts`
+ * (ERNIE_HEAD_INPUT and/or ERNIE_HEAD_OUTPUT), converting each matrix on the device to the
+ * storage dtype (biases stay FP32); the fields of a part not uploaded are not read, and
+ * text_dim is read only for the input head. A resident part of the same kind is replaced.
+ * The other part stays resident and must have the same dim, latent_ch and dtype, else the
+ * call is rejected. The host memory may be released when the call returns. */
+int ernie_hip_heads_upload_tensors(ernie_hip_ctx* ctx, const ernie_heads_host_tensors* w, int dim, int latent_ch,
+                                   int text_dim, int dtype, int parts);
+/* ERNIE_HEAD_INPUT | ERNIE_HEAD_OUTPUT bits of the head parts resident in the context. */
+int ernie_hip_heads_loaded(const ernie_hip_ctx* ctx);
 int ernie_hip_heads_init_random(ernie_hip_ctx* ctx, int dim, int latent_ch, int text_dim, int dtype,
                                 uint64_t seed, float std_dev);
 /* Input head: latent [latent_ch][hw], text [text_tokens][text_dim], time features
@@ -300,6 +338,18 @@ int ernie_hip_profile_reset(ernie_hip_ctx* ctx);
 /* launches, total milliseconds, algorithmic FLOP and HBM bytes summed over launches. */
 int ernie_hip_profile_query(const ernie_hip_ctx* ctx, int cls, long* launches, double* ms, double* flop,
                             double* bytes);
+
+/* ---- matrix-core ceiling of the device (no reference counterpart) ----------------
+ * The reference publishes no device ceiling; this measures the one the FP16 roofline
+ * fractions are read against. `launches` back-to-back launches (after one untimed
+ * launch) of a kernel in which every wave of one 512-thread workgroup per CU (two
+ * waves per SIMD) issues `iters` x 8 independent v_mfma_f32_16x16x32_f16 from
+ * registers, with operand bits toggling between consecutive MFMAs. Synchronises.
+ * Returns the dense FP16 FLOP/s over the timed launches (HIP events), their seconds,
+ * and the shader clock in Hz the chip held during the last launch (median over its
+ * waves of s_memtime ticks per s_memrealtime tick, times the constant counter rate). */
+int ernie_hip_mfma_rate(ernie_hip_ctx* ctx, int iters, int launches, double* flop_per_s, double* clock_hz,
+                        double* seconds);
 
 #ifdef __cplusplus
 }

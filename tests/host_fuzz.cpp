@@ -1,7 +1,7 @@
 // SPDX-License-Identifier: MIT
 // Deterministic fuzz driver for the host-side parsers and helpers that take caller
-// data: the ncnn .param graph checks, the ModelBin section walk, the file readers,
-// SHA-256 and the text padding / RoPE-table helpers. Built by
+// data: the ncnn .param graph checks (DiT blocks, DiT heads, text blocks), the ModelBin
+// section walks, the file readers, SHA-256 and the text padding / RoPE-table helpers. Built by
 // tests/test_host_sanitizers.py with AddressSanitizer and UndefinedBehaviorSanitizer
 // on the CPU; every input either passes the checks or is rejected with a C++
 // exception, and the sanitizers abort the run on any memory or UB error.
@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "ernie/block_files.h"
+#include "ernie/component_files.h"
 #include "ernie/conditioning.h"
 #include "ernie/latent_ops.h"
 #include "ernie/sha256.h"
@@ -107,6 +108,66 @@ std::string weight_bytes(const ernie::BlockGraph& g, Rng& rng)
         }
     }
     return bin;
+}
+
+// A reference graph with every parameter value found in `values` replaced (lines whose
+// layer name is in `only`, or every line when `only` is empty).
+std::string rewrite_values(const std::string& graph, const std::vector<std::pair<std::string, std::string>>& values,
+                           const std::vector<std::string>& only = {})
+{
+    std::istringstream in(graph);
+    std::string line, out;
+    while (std::getline(in, line)) {
+        std::vector<std::string> f = tokens_of(line);
+        bool pick = only.empty();
+        for (const std::string& n : only) pick |= f.size() > 1 && f[1] == n;
+        if (pick)
+            for (size_t i = 4; i < f.size(); ++i) {
+                const size_t eq = f[i].find('=');
+                if (eq == std::string::npos) continue;
+                for (const auto& kv : values)
+                    if (f[i].substr(eq + 1) == kv.first) {
+                        f[i] = f[i].substr(0, eq + 1) + kv.second;
+                        break;
+                    }
+            }
+        for (size_t i = 0; i < f.size(); ++i) out += (i ? " " : "") + f[i];
+        out += "\n";
+    }
+    return out;
+}
+
+// Weight bytes for a list of (elements, tagged) sections: tagged ones get a random tag.
+std::string section_bytes(const std::vector<std::pair<size_t, bool>>& sections, Rng& rng)
+{
+    std::string bin;
+    auto put32 = [&](uint32_t v) { bin.append(reinterpret_cast<const char*>(&v), 4); };
+    for (const auto& sec : sections) {
+        if (!sec.second) {
+            bin.append(4 * sec.first, '\0');
+            continue;
+        }
+        const int kind = (int)rng.below(3);
+        put32(kind == 0 ? 0u : kind == 1 ? 0x01348B83u : 0x01306B47u);
+        bin.append(kind == 0 ? 4 * sec.first : (2 * sec.first + 3) / 4 * 4, '\0');
+    }
+    return bin;
+}
+
+std::vector<std::pair<size_t, bool>> head_layout(const ernie::HeadGraph& h)
+{
+    const size_t D = h.dim;
+    if (h.kind == ernie::HeadKind::Input)
+        return {{D * h.latent_ch, true}, {D, false}, {D * h.text_dim, true}, {D * D, true}, {D, false},
+                {D * D, true}, {D, false}, {6 * D * D, true}, {6 * D, false}};
+    return {{2 * D * D, true}, {2 * D, false}, {(size_t)h.latent_ch * D, true}, {(size_t)h.latent_ch, false}};
+}
+
+std::vector<std::pair<size_t, bool>> text_layout(const ernie::TextBlockGraph& t)
+{
+    const size_t H = t.hidden, Q = 128 * (size_t)t.heads, KV = 128 * (size_t)t.kv_heads, F = t.ffn;
+    return {{H, false}, {Q * H, true}, {KV * H, true}, {KV * H, true}, {H * Q, true},
+            {H, false}, {F * H, true}, {F * H, true}, {H * F, true}};
 }
 
 const char* const kNumbers[] = {"0", "-1", "1", "7", "128", "4096", "2147483647", "-2147483648",
@@ -212,6 +273,32 @@ int main(int argc, char** argv)
     const std::string small = synthetic_graph(component, 256, 512, 40);
     const ernie::BlockGraph small_g = ernie::inspect_block_graph(small, true);
 
+    // The reference's head and text graphs pass; narrow copies give small weight files.
+    std::vector<std::string> heads;
+    for (const char* name : {"head_input_s288", "head_input_s4160", "head_output_s288", "head_output_s4160"}) {
+        heads.push_back(read_file(golden + "/" + name + ".ncnn.param"));
+        if (!ernie::inspect_head_graph(heads.back(), false).reviewed) {
+            std::fprintf(stderr, "reference head graph %s not recognised\n", name);
+            return 1;
+        }
+    }
+    const std::string text64 = read_file(golden + "/text_s64.ncnn.param");
+    if (!ernie::inspect_text_block_graph(text64, false).reviewed) {
+        std::fprintf(stderr, "reference text graph not recognised\n");
+        return 1;
+    }
+    const std::vector<std::pair<std::string, std::string>> narrow_head = {
+        {"4096", "256"}, {"524288", "8192"}, {"3072", "64"}, {"16777216", "65536"}, {"24576", "1536"},
+        {"100663296", "393216"}, {"8192", "512"}, {"33554432", "131072"}};
+    const std::string small_in = rewrite_values(heads[0], narrow_head);
+    const std::string small_out = rewrite_values(heads[2], narrow_head);
+    const ernie::HeadGraph small_in_g = ernie::inspect_head_graph(small_in, true);
+    const ernie::HeadGraph small_out_g = ernie::inspect_head_graph(small_out, true);
+    const std::string small_text = rewrite_values(
+        rewrite_values(text64, {{"3072", "256"}, {"4096", "512"}, {"1024", "256"}, {"9216", "512"}}),
+        {{"32", "4"}, {"8", "2"}}, {"reshape_10", "reshape_11", "reshape_12"});
+    const ernie::TextBlockGraph small_text_g = ernie::inspect_text_block_graph(small_text, true);
+
     for (long it = 0; it < iters; ++it) {
         // 1. Graph text: parse and inspect mutated graphs, with and without the contract.
         const std::string& base = (it % 3 == 0) ? runtime : (it % 3 == 1 ? component : small);
@@ -229,6 +316,32 @@ int main(int argc, char** argv)
                 if (s.end > bin.size() || s.data < s.begin || s.end < s.data) throw std::logic_error("bad section");
         });
 
+        // 2b. Head and text block graphs and section walks.
+        {
+            const std::string& hbase = (it % 5 < 4) ? heads[it % 4] : (it & 1 ? small_in : small_out);
+            const std::string htext = mutate_text(hbase, rng);
+            expect_clean([&] { ernie::inspect_head_graph(htext, (it & 2) != 0); });
+            const std::string ttext = mutate_text(it & 1 ? text64 : small_text, rng);
+            expect_clean([&] { ernie::inspect_text_block_graph(ttext, (it & 2) != 0); });
+            const ernie::HeadGraph& hg = (it & 1) ? small_in_g : small_out_g;
+            std::string hbin = section_bytes(head_layout(hg), rng);
+            if (it % 3) hbin = mutate_bytes(hbin, rng);
+            expect_clean([&] {
+                for (const ernie::WeightSection& sec :
+                     ernie::head_sections(hg, reinterpret_cast<const unsigned char*>(hbin.data()), hbin.size()))
+                    if (sec.end > hbin.size() || sec.data < sec.begin || sec.end < sec.data)
+                        throw std::logic_error("bad head section");
+            });
+            std::string tbin = section_bytes(text_layout(small_text_g), rng);
+            if (it % 3) tbin = mutate_bytes(tbin, rng);
+            expect_clean([&] {
+                for (const ernie::WeightSection& sec : ernie::text_block_sections(
+                         small_text_g, reinterpret_cast<const unsigned char*>(tbin.data()), tbin.size()))
+                    if (sec.end > tbin.size() || sec.data < sec.begin || sec.end < sec.data)
+                        throw std::logic_error("bad text section");
+            });
+        }
+
         // 3. The file readers on mutated files (every 16th iteration: file system work).
         if (it % 16 == 0) {
             const std::string gp = scratch + "/g.param", bp = scratch + "/w.bin";
@@ -240,6 +353,13 @@ int main(int argc, char** argv)
             expect_clean([&] { ernie::inspect_block_files(scratch, bp, true); });   // a directory
             expect_clean([&] { ernie::inspect_block_files(gp, scratch, true); });   // a directory
             expect_clean([&] { ernie::read_graph_text(scratch + "/missing"); });
+            write_file(gp, (it % 32 == 0) ? mutate_text(small_in, rng) : small_in);
+            write_file(bp, mutate_bytes(section_bytes(head_layout(small_in_g), rng), rng));
+            expect_clean([&] { ernie::inspect_head_files(gp, bp, true); });
+            expect_clean([&] { ernie::inspect_head_files(gp, bp, true, std::string(64, 'b')); });
+            write_file(gp, (it % 32 == 0) ? mutate_text(small_text, rng) : small_text);
+            write_file(bp, mutate_bytes(section_bytes(text_layout(small_text_g), rng), rng));
+            expect_clean([&] { ernie::inspect_text_block_files(gp, bp, true); });
         }
 
         // 4. SHA-256: one-shot against random split points.

@@ -341,3 +341,44 @@ def test_facade_block_sequence_validation_and_parity():
     with pytest.raises(E.ErnieInvalidRequest):
         fac.run_block_sequence([], dev(x), 40, dim, md, dev(cos), dev(sin), out)
     fac.close()
+
+
+@pytest.mark.parametrize("dim,ffn,S,image,valid", [(4096, 1024, 4160, (64, 64), 40), (1024, 2048, 4136, (64, 64), 20)],
+                         ids=["light-tail-tiles", "split-tail"])
+@pytest.mark.parametrize("dt", [E.FP16, E.BF16], ids=lambda d: NAMES[d])
+def test_qk_rounding_orders(ctx, dt, dim, ffn, S, image, valid):
+    # 16-bit blocks normalise and rotate Q and K from the QKV GEMM's FP32 accumulators
+    # (ERNIE_QK_ROUND_FUSED, the default); ERNIE_QK_ROUND_STORAGE first rounds the
+    # projections to the storage dtype, as the reference graph does (gemm_0/gemm_1 ->
+    # rmsn_9/rmsn_10). At 4160 tokens and width 4096 the Q/K/V GEMM finishes its 64 tail
+    # rows in light tiles; at width 1024 and 4136 tokens (192 full tiles) in a split tail
+    # row, whose rows take the storage order in both modes. (GEMMs of at most 128 tiles
+    # split every tile along K and so always take the storage order.) The two orders
+    # differ by one rounding of Q and K: their block outputs are held to each other by the
+    # reference's block gate for the dtype and by NRMSE <= 1e-3 (FP16) / 8e-3 (BF16), an
+    # eighth and a quarter of that gate, and to the oracle by the gate where the oracle
+    # runs (the narrower case).
+    w = small_block(dim=dim, ffn=ffn, seed=15)
+    x, mods, cos, sin, mask = small_inputs(S=S, dim=dim, image=image, valid=valid, seed=16)
+    ctx.block_upload(8, w, dim, ffn, dt)
+    keys = int(np.sum(mask == 0))
+    fused = run_block(ctx, 8, x, mods, cos, sin, mask, keys)
+    ctx.call("set_qk_rounding", 1)
+    try:
+        storage = run_block(ctx, 8, x, mods, cos, sin, mask, keys)
+        np.testing.assert_array_equal(run_block(ctx, 8, x, mods, cos, sin, mask, keys), storage)
+    finally:
+        ctx.call("set_qk_rounding", 0)
+    np.testing.assert_array_equal(run_block(ctx, 8, x, mods, cos, sin, mask, keys), fused)
+    assert not np.array_equal(fused, storage)
+    g = kat.gate(fused, storage, *kat.BLOCK_GATES[NAMES[dt]])
+    print(f"qk rounding orders {NAMES[dt]} S={S}: max|d| {g['max_abs_error']:.3g} nrmse {g['nrmse']:.3g}", flush=True)
+    assert g["passed"] and g["nrmse"] <= (1e-3 if dt == E.FP16 else 8e-3), g
+    if dim <= 1024:
+        ref = O.block_forward(w, x, mods, cos, sin, mask)
+        for name, got in (("fused", fused), ("storage", storage)):
+            go = kat.gate(got, ref, *kat.BLOCK_GATES[NAMES[dt]])
+            assert go["passed"], (name, go)
+    with pytest.raises(E.ErnieError):
+        ctx.call("set_qk_rounding", 2)
+    ctx.call("block_release", 8)

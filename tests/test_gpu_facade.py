@@ -40,7 +40,9 @@ def test_finite_check_in_flight_on_two_slots(ctx):
     with pytest.raises(E.ErnieError):
         ctx.finite_end(0)
     with pytest.raises(E.ErnieError):
-        ctx.finite_begin(good, 1000, E_SLOTS)
+        ctx.finite_begin(good, 1000, E_SLOTS + E_SLOTS_RESERVED)
+    with pytest.raises(E.ErnieError):
+        ctx.finite_begin(good, 1000, -1)
     nan_host = np.zeros(64, np.float32)
     nan_host[0] = np.nan
     ctx.finite_begin(dev(nan_host), 64, 2)
@@ -51,7 +53,8 @@ def test_finite_check_in_flight_on_two_slots(ctx):
         ctx.marker_elapsed(0, 63)  # never recorded
 
 
-E_SLOTS = 4
+E_SLOTS = 4           # ERNIE_FINITE_SLOTS: the callers' slots
+E_SLOTS_RESERVED = 3  # ERNIE_FINITE_SLOTS_RESERVED: the facade's, after them
 
 
 def test_upload_async_copies_before_the_source_is_reused(ctx):
@@ -213,6 +216,39 @@ def test_denoise_names_the_non_finite_step(start):
             fac.denoise_observed([0], dev(bad), H, W, dev(tx), text, dev(cos), dev(sin), dev(mask), H * W + valid, 4,
                                  start_step=start, dtype=E.FP16, observer=lambda *a: seen.append(a[0]))
         assert seen == []
+    finally:
+        torch.cuda.synchronize()
+        fac.close()
+
+
+def test_denoise_reports_a_later_steps_own_failure():
+    # Step k's DiT fails (its block was released by the observer of step k - 2, after the
+    # device had finished with it) while step k - 1's finite check is still pending. That
+    # check passes, so the error that comes back is step k's own device error, not
+    # a finite-check or timing error, and every earlier step was observed.
+    import torch
+    dim, ffn = 4096, 512
+    fac = E.Facade(0)
+    try:
+        fac.hip.heads_upload(small_heads(dim=dim, latent_ch=128, text_dim=3072, seed=60), dim, 128, 3072, E.FP16)
+        fac.hip.block_upload(0, small_block(dim, ffn, seed=61), dim, ffn, E.FP16)
+        H = W = 4
+        text, valid = 8, 5
+        tx = O.normal((text, 3072), 62)
+        cos, sin, mask = O.dit_constants(O.rope_frequencies(), W, H, valid, text)
+        seen = []
+
+        def observer(step, *_):
+            seen.append(step)
+            if step == 0:
+                fac.hip.synchronize()  # step 1 is queued on the block: let it finish first
+                fac.hip.call("block_release", 0)
+
+        with pytest.raises(E.ErnieError, match="not loaded") as info:
+            fac.denoise_observed([0], dev(O.normal((128, H, W), 63)), H, W, dev(tx), text, dev(cos), dev(sin),
+                                 dev(mask), H * W + valid, 4, dtype=E.FP16, observer=observer)
+        assert type(info.value) is E.ErnieError  # neither an allocation error nor a rejected request
+        assert seen == [0, 1]
     finally:
         torch.cuda.synchronize()
         fac.close()

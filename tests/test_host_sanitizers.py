@@ -1,8 +1,9 @@
 """The host-side parsers of caller-supplied data under AddressSanitizer and
 UndefinedBehaviorSanitizer (CPU only).
 
-tests/host_fuzz.cpp drives the ncnn .param graph checks, the ModelBin section walk,
-the graph/weight file readers (host/block_files.cpp), SHA-256, pad_text,
+tests/host_fuzz.cpp drives the ncnn .param graph checks, the ModelBin section walks,
+the graph/weight file readers (host/block_files.cpp, and host/component_files.cpp for the
+DiT heads and text blocks), SHA-256, pad_text,
 dit_constants and FlowSchedule::turbo with seeded mutations of the reference's own
 graph fixtures and of well-formed weight files. Every input must either pass the
 checks or raise a C++ exception; any sanitizer report aborts the run.
@@ -17,7 +18,8 @@ import pytest
 ROOT = Path(__file__).resolve().parent.parent
 HOST = ROOT / "ernie-image-ncnn-vulkan_amd" / "host"
 SOURCES = [ROOT / "tests" / "host_fuzz.cpp"] + [HOST / f for f in
-                                                 ("block_files.cpp", "sha256.cpp", "conditioning.cpp", "latent_ops.cpp")]
+                                                 ("block_files.cpp", "component_files.cpp", "sha256.cpp",
+                                                  "conditioning.cpp", "latent_ops.cpp")]
 
 
 @pytest.fixture(scope="module")

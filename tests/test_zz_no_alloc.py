@@ -67,3 +67,40 @@ def test_no_alloc_text_block_matches_the_allocating_entry(dt):
     finally:
         torch.cuda.synchronize()
         c.close()
+
+
+def test_no_alloc_text_block_under_graph_capture():
+    # The callers the entry point is for: one call recorded into a HIP graph on the
+    # context's stream, then replayed on new inputs copied into the same buffers. Each
+    # replay (with this program's own eager work and a synchronisation between replays)
+    # must equal the allocating entry point on the same inputs, bitwise.
+    import torch
+    dt, S = E.FP16, 48
+    c = E.Context(0)
+    stream = torch.cuda.Stream()
+    try:
+        w = small_text_block(seed=71, hidden=HIDDEN, heads=HEADS, kv_heads=KV_HEADS, ffn=FFN, std=0.02)
+        c.text_block_upload(0, w, HIDDEN, HEADS, KV_HEADS, FFN, dt)
+        x, cos, sin, _ = text_inputs(S, seed=72)
+        xd, cd, sd, out = dev(x), dev(cos), dev(sin), empty((S, HIDDEN))
+        args = (0, E.ptr(xd), E.ptr(out), E.ptr(cd), E.ptr(sd), None, 1, S)
+        torch.cuda.synchronize()
+        c.call("set_stream", E.c_vp(stream.cuda_stream))
+        c.call("text_block_forward_noalloc", *args)  # code objects loaded outside the capture
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream, capture_error_mode="relaxed"):
+            c.call("text_block_forward_noalloc", *args)
+        for seed in (73, 74, 75):
+            xn, _, _, _ = text_inputs(S, seed=seed)
+            xd.copy_(torch.from_numpy(xn).cuda())
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            got = host(out)
+            ref = forward(c, "text_block_forward", 0, xd, empty((S, HIDDEN)), cd, sd, None, True, S)
+            assert np.isfinite(ref).all()
+            np.testing.assert_array_equal(got, ref, err_msg=f"replay with input seed {seed}")
+    finally:
+        torch.cuda.synchronize()
+        c.close()
