@@ -3,6 +3,9 @@
     lib/libernie_hip.so  kernels + extern "C" ABI (include/ernie_hip.h), hipcc
     lib/libernie.so      C++ facade mirroring the reference's block-runner /
                          DiT / denoise API, g++, linked against libernie_hip.so
+    lib/ernie-block-runner, lib/ernie-denoise-runner
+                         command-line runners with the reference probes' flags
+                         (probes/block_runner.cpp, probes/denoise_runner.cpp), g++
 
 Usage: python build.py [--jobs N]
 """
@@ -17,6 +20,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 HOST = PKG / "host"
+RUNNERS = PKG / "runners"
 LIB = PKG / "lib"
 OBJ = LIB / "obj"
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
@@ -70,7 +74,19 @@ def build(jobs=8, verbose=False):
     run(["g++", "-shared", "-fPIC", "-o", str(tmp), *[str(o) for _, o in host_results], f"-L{LIB}", "-lernie_hip",
          "-Wl,-rpath,$ORIGIN", "-Wl,--no-as-needed"])
     os.replace(tmp, host_so)
-    return hip_so, host_so
+
+    def runner(name, src):
+        exe = LIB / name
+        tmp = LIB / (name + ".tmp")
+        run(["g++", *CXX_FLAGS, f"-I{RUNNERS}", str(RUNNERS / src), "-o", str(tmp), f"-L{LIB}", "-lernie",
+             "-lernie_hip", "-Wl,-rpath,$ORIGIN"])
+        os.replace(tmp, exe)
+        return exe
+
+    with ThreadPoolExecutor(max_workers=2) as pool:
+        runners = list(pool.map(lambda a: runner(*a), (("ernie-block-runner", "block_runner.cpp"),
+                                                       ("ernie-denoise-runner", "denoise_runner.cpp"))))
+    return (hip_so, host_so, *runners)
 
 
 if __name__ == "__main__":

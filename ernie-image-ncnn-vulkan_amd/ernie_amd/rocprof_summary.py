@@ -16,11 +16,14 @@
         SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_LDS GRBM_GUI_ACTIVE: per kernel, the clock
         it ran at, the matrix cores' busy fraction and VALU / LDS instructions per MFMA.
 
-Writes Markdown to stdout. Reads only the CSV files it is given.
+Writes Markdown to stdout, or to --output FILE. Each summary states the commands that
+made it: the profiler runs given with --command, then this tool's own invocation.
+Reads only the CSV files it is given.
 """
 import argparse
 import csv
 import json
+import shlex
 import statistics
 import sys
 from collections import defaultdict
@@ -42,6 +45,29 @@ SHORT = [
     ("tokens_latent", "to latent"), ("convert_kernel", "convert/copy"), ("normal_kernel", "normal init"),
     ("tile_k32", "k32 tiling"),
 ]
+
+
+def invocation():
+    """This tool's command line as run from the repository root."""
+    script = Path(__file__).resolve()
+    try:
+        script = script.relative_to(Path.cwd().resolve())
+    except ValueError:
+        pass
+    return " ".join(["python3", shlex.quote(str(script)), *map(shlex.quote, sys.argv[1:])])
+
+
+def commands(args):
+    """The profiler runs (--command) and then the summary's own invocation."""
+    return [*args.command, invocation()]
+
+
+def emit(args, lines):
+    text = "\n".join(lines) + "\n"
+    if getattr(args, "output", None):
+        Path(args.output).write_text(text)
+    else:
+        sys.stdout.write(text)
 
 
 def short(name):
@@ -101,8 +127,7 @@ def trace(args):
         dur[r["Kernel_Name"]].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
     total = sum(sum(v) for v in dur.values())
     out = [f"# {args.title}", ""]
-    if args.command:
-        out += ["Command (from the repository root, on one MI355X):", "", "```", *args.command, "```", ""]
+    out += ["Commands (from the repository root, on one MI355X):", "", "```", *commands(args), "```", ""]
     if args.note:
         out += [args.note, ""]
     out += ["| kernel | calls | avg us | min us | max us | % time |", "|---|---:|---:|---:|---:|---:|"]
@@ -153,7 +178,7 @@ def trace(args):
             out.append(f"| {a} | {b} | {len(v)} | {statistics.mean(v):.2f} | {max(v):.1f} | {sum(v) / K:.1f} |")
     if args.bench_log:
         out += bench_classes(args.bench_log)
-    print("\n".join(out))
+    emit(args, out)
 
 
 def counter_rows(directory, counter):
@@ -198,7 +223,7 @@ def traffic(args):
             stage_bytes[st] += fb + wb
             stage_launches[st] += main_kernel
     out = [f"# {args.title}", "", "Two counter runs (one counter each), from the repository root on one MI355X:", "",
-           "```", *args.command, "```", "",
+           "```", *commands(args), "```", "",
            f"Calibration: the plain FP32 copy kernel (`convert_kernel`, {args.copy_mib} MiB read + {args.copy_mib} MiB "
            f"written per dispatch) reads FETCH_SIZE = {f_cal:.0f} KiB and WRITE_SIZE = {w_cal:.0f} KiB, so bytes = "
            f"FETCH_SIZE x 1024 x {f_scale:.3f} and WRITE_SIZE x 1024 x {w_scale:.3f}.", "",
@@ -213,7 +238,7 @@ def traffic(args):
     record = {"kernel_sources_sha256": args.sources_sha256,
               "bytes_per_launch": {st: round(b) for st, b in per_launch.items()}}
     out += ["", "```json traffic", json.dumps(record, indent=1), "```"]
-    print("\n".join(out))
+    emit(args, out)
 
 
 def mfma(args):
@@ -224,7 +249,7 @@ def mfma(args):
         per[r["Kernel_Name"]][r["Counter_Name"]].append(float(r["Counter_Value"]))
         dur[r["Kernel_Name"]][r["Dispatch_Id"]] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
     out = [f"# {args.title}", "", "One counter run, from the repository root on one MI355X:", "", "```",
-           *args.command, "```", "",
+           *commands(args), "```", "",
            "Per dispatch means. GRBM_GUI_ACTIVE is summed over the 8 XCDs, so the clock the kernel ran at is "
            "GUI / 8 / duration (dispatch timestamps of this run, kernels serialised by the profiler). "
            "SQ_VALU_MFMA_BUSY_CYCLES is summed over the 1024 SIMDs, so MFMA busy = MFMA_BUSY / (1024 x GUI / 8): "
@@ -240,7 +265,7 @@ def mfma(args):
         ratio = (lambda k: f"{m[k] / n_mfma:.2f}" if n_mfma and k in m else "-")
         out.append(f"| `{name[:90]}` ({short(name)}) | {len(dur[name])} | {us:.1f} | {gui / us / 1e3:.2f} | "
                    f"{busy:.3f} | {ratio('SQ_INSTS_VALU')} | {ratio('SQ_INSTS_LDS')} |")
-    print("\n".join(out))
+    emit(args, out)
 
 
 def main(argv=None):
@@ -266,6 +291,8 @@ def main(argv=None):
     m.add_argument("dir")
     m.add_argument("--title", default="MFMA and VALU counters")
     m.add_argument("--command", action="append", default=[])
+    for p in (t, f, m):
+        p.add_argument("--output", default="", help="write the summary here instead of stdout")
     args = ap.parse_args(argv)
     {"trace": trace, "traffic": traffic, "mfma": mfma}[args.cmd](args)
 
