@@ -98,6 +98,7 @@ struct ernie_hip_ctx {
     DeviceBuffer head_ws;  // head intermediates
     DeviceBuffer dit_act;  // run_dit activations: x [S][dim], c, mods
     DeviceBuffer split_ws;   // GEMM tail-row split-K partial sums
+    DeviceBuffer rope_pack;  // [S][64] (cos, sin) pairs of the rotary angles, per call
     DeviceBuffer text_ws;    // text block activations
     DeviceBuffer ones;       // FP32 ones: unit gates of the text block's residual epilogues
     // Event timing.
@@ -462,8 +463,26 @@ int split_workspace(ernie_hip_ctx* ctx, int S, int heads, void** ws, size_t* byt
     return ERNIE_OK;
 }
 
+// The rotary angles (cos, sin) packed once per call (rope_pack) for the blocks in
+// `blocks` whose Q/K weights have the fused layout: into the context's buffer, or nullptr
+// when no block has it.
+int pack_rope(ernie_hip_ctx* ctx, const int* blocks, int count, const float* cos_t, const float* sin_t, int S,
+              const float** cs)
+{
+    *cs = nullptr;
+    bool fused = false;
+    for (int i = 0; i < count; ++i) fused |= ctx->blocks[blocks[i]].qk_fused;
+    if (!fused) return ERNIE_OK;
+    int rc = dev_alloc(ctx, ctx->rope_pack, (size_t)S * 128 * sizeof(float), "rotary angle pairs");
+    if (rc) return rc;
+    rc = kernel_status(ctx, rope_pack(cos_t, sin_t, S, static_cast<float*>(ctx->rope_pack.ptr), ctx->stream),
+                       "rotary angle pairs");
+    if (!rc) *cs = static_cast<const float*>(ctx->rope_pack.ptr);
+    return rc;
+}
+
 int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, float* out, const float* mods,
-                  const float* cos_t, const float* sin_t, const float* mask, int valid_keys, int S)
+                  const float* cos_t, const float* sin_t, const float* cs_t, const float* mask, int valid_keys, int S)
 {
     const int D = w.dim, F = w.ffn, dt = w.dtype, H = D / kHeadDim;
     const double e = (double)esize(dt), dS = S;
@@ -490,9 +509,10 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
         g.epilogue = EPI_STORE; g.C = ws.qkv; g.ldc = 3 * D; g.c_dtype = dt;
         if (w.qk_fused && !ctx->qk_storage_rounding) {
             g.epilogue = EPI_QKROPE;
+            g.cs_t = cs_t;
             g.qk_cols = 2 * D; g.k_col = D;
             g.gq = static_cast<const float*>(w.norm_q.ptr); g.gk = static_cast<const float*>(w.norm_k.ptr);
-            g.cos_t = cos_t; g.sin_t = sin_t; g.qk_eps = 1e-6f;
+            g.qk_eps = 1e-6f;
         }
         rc = split_workspace(ctx, S, H, &g.split_ws, &g.split_ws_bytes);
         if (rc) return rc;
@@ -506,7 +526,7 @@ int block_forward(ernie_hip_ctx* ctx, const BlockWeights& w, const float* x, flo
         Timed t(ctx, P_ROPE, 0, dS * 2 * D * e * 2 + dS * 128 * 8);
         rc = kernel_status(ctx, qk_norm_rope_permuted(ws.qkv, dt, 0, S, H, H, 3L * D, D,
                                                       static_cast<const float*>(w.norm_q.ptr),
-                                                      static_cast<const float*>(w.norm_k.ptr), cos_t, sin_t, 1e-6f, s),
+                                                      static_cast<const float*>(w.norm_k.ptr), cs_t, 1e-6f, s),
                            "qk_norm_rope");
         if (rc) return rc;
     } else if (!w.qk_fused) {
@@ -978,6 +998,7 @@ void ernie_hip_destroy(ernie_hip_ctx* ctx)
     dev_free(ctx->head_ws);
     dev_free(ctx->dit_act);
     dev_free(ctx->split_ws);
+    dev_free(ctx->rope_pack);
     for (hipEvent_t e : ctx->event_pool) (void)hipEventDestroy(e);
     for (hipEvent_t e : ctx->seq_events) (void)hipEventDestroy(e);
     for (auto& st : ctx->upload_staging) {
@@ -1478,8 +1499,10 @@ int ernie_hip_block_forward(ernie_hip_ctx* ctx, int index, const float* x, float
     DeviceGuard guard(ctx);
     if (!ctx) return ERNIE_ERROR;
     int rc = check_block_call(ctx, index, S, x, out, mods, cos_t, sin_t, valid_keys);
+    const float* cs = nullptr;
+    if (!rc) rc = pack_rope(ctx, &index, 1, cos_t, sin_t, S, &cs);
     if (rc) return rc;
-    return block_forward(ctx, ctx->blocks[index], x, out, mods, cos_t, sin_t, mask, valid_keys, S);
+    return block_forward(ctx, ctx->blocks[index], x, out, mods, cos_t, sin_t, cs, mask, valid_keys, S);
 }
 
 int ernie_hip_block_sequence(ernie_hip_ctx* ctx, const int* blocks, int count, const float* x, float* out,
@@ -1497,9 +1520,12 @@ int ernie_hip_block_sequence(ernie_hip_ctx* ctx, const int* blocks, int count, c
     }
     // One event before each block and one after the last; a single wait at the end.
     int rc = seconds ? sequence_events(ctx, count + 1) : ERNIE_OK;
+    const float* cs = nullptr;
+    if (!rc) rc = pack_rope(ctx, blocks, count, cos_t, sin_t, S, &cs);
     for (int i = 0; i < count && !rc; ++i) {
         if (seconds) (void)hipEventRecord(ctx->seq_events[i], ctx->stream);
-        rc = block_forward(ctx, ctx->blocks[blocks[i]], i == 0 ? x : out, out, mods, cos_t, sin_t, mask, valid_keys, S);
+        rc = block_forward(ctx, ctx->blocks[blocks[i]], i == 0 ? x : out, out, mods, cos_t, sin_t, cs, mask,
+                           valid_keys, S);
     }
     if (seconds && !rc) rc = sequence_seconds(ctx, count, seconds);
     return rc;
@@ -1824,8 +1850,10 @@ int ernie_hip_dit_forward(ernie_hip_ctx* ctx, const float* latent, int hw, const
     float* c = x + (size_t)S * D;
     float* mods = c + D;
     rc = input_head(ctx, latent, hw, text, text_tokens, time_features, x, c, mods);
+    const float* cs = nullptr;
+    if (!rc) rc = pack_rope(ctx, blocks, count, cos_t, sin_t, S, &cs);
     for (int i = 0; i < count && !rc; ++i)
-        rc = block_forward(ctx, ctx->blocks[blocks[i]], x, x, mods, cos_t, sin_t, mask, valid_keys, S);
+        rc = block_forward(ctx, ctx->blocks[blocks[i]], x, x, mods, cos_t, sin_t, cs, mask, valid_keys, S);
     if (!rc) rc = output_head(ctx, x, hw, c, prediction);
     return rc;
 }

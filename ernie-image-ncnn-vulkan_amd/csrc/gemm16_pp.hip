@@ -121,8 +121,7 @@ struct Params {
     long k_col;
     const float* gq;
     const float* gk;
-    const float* cos_t;
-    const float* sin_t;
+    const float* cs_t;  // [M][64] (cos, sin) pairs of each row's rotary angles (rope_pack)
     float qk_eps;
 };
 
@@ -415,8 +414,8 @@ __device__ __forceinline__ void qk_rope_epilogue(const Params& p, const f32x4 (&
         t += __shfl_xor(t, 32, 64);
         ss[i] = t;
     }
-    // Gammas for the whole tile and the first row's cos / sin are requested before the
-    // partner exchange; each later row's are requested while the previous row is rotated.
+    // Gammas for the whole tile and the first two rows' angles are requested before the
+    // partner exchange; each later row's are requested two rows ahead of their use.
     const int d0 = 32 * hf + 4 * q16;
     f32x4 ga[2], gb[2];
 #pragma unroll
@@ -424,31 +423,33 @@ __device__ __forceinline__ void qk_rope_epilogue(const Params& p, const f32x4 (&
         ga[j] = *reinterpret_cast<const f32x4*>(g + d0 + 16 * j);
         gb[j] = *reinterpret_cast<const f32x4*>(g + d0 + 16 * j + 64);
     }
-    // cs[b][j]: cos lo, cos hi, sin lo, sin hi of buffer b's row (clamped into [0, M)).
-    f32x4 cs[2][2][4];
-    auto load_row = [&](int i, f32x4 (&dst)[2][4]) {
+    // Dimensions d .. d + 3 (d = d0 + 16 j, even) use angles d / 2 and d / 2 + 1 (each
+    // twice), their partners d + 64 .. angles d / 2 + 32 and + 33. cs[b][j][0] holds
+    // (cos, sin, cos, sin) of the first two, cs[b][j][1] of the second two, for buffer
+    // b's row (clamped into [0, M)).
+    f32x4 cs[3][2][2];
+    auto load_row = [&](int i, f32x4 (&dst)[2][2]) {
         const size_t m = (size_t)min(row_w + 16 * i, p.M - 1) * 128;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const int d = d0 + 16 * j;
-            dst[j][0] = *reinterpret_cast<const f32x4*>(p.cos_t + m + d);
-            dst[j][1] = *reinterpret_cast<const f32x4*>(p.cos_t + m + d + 64);
-            dst[j][2] = *reinterpret_cast<const f32x4*>(p.sin_t + m + d);
-            dst[j][3] = *reinterpret_cast<const f32x4*>(p.sin_t + m + d + 64);
+            const int k = (d0 + 16 * j) >> 1;
+            dst[j][0] = *reinterpret_cast<const f32x4*>(p.cs_t + m + 2 * k);
+            dst[j][1] = *reinterpret_cast<const f32x4*>(p.cs_t + m + 2 * (k + 32));
         }
     };
     load_row(0, cs[0]);
+    if (2 * MSUB > 1) load_row(1, cs[1]);
     if (q16 == 0)
 #pragma unroll
         for (int i = 0; i < 2 * MSUB; ++i) red[(wave * 2 * MSUB + i) * 16 + r16] = ss[i];
     phase_barrier();
 #pragma unroll
     for (int i = 0; i < 2 * MSUB; ++i) {
-        if (i + 1 < 2 * MSUB) load_row(i + 1, cs[(i + 1) & 1]);
+        if (i + 2 < 2 * MSUB) load_row(i + 2, cs[(i + 2) % 3]);
         const int m = row_w + 16 * i;
         const float inv = 1.0f / sqrtf((ss[i] + red[((wave ^ 2) * 2 * MSUB + i) * 16 + r16]) / 128.f + p.qk_eps);
         OutT* crow = static_cast<OutT*>(p.C) + (size_t)m * p.ldc + head_col;
-        const f32x4(&c)[2][4] = cs[i & 1];
+        const f32x4(&c)[2][2] = cs[i % 3];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int d = d0 + 16 * j;
@@ -457,15 +458,16 @@ __device__ __forceinline__ void qk_rope_epilogue(const Params& p, const f32x4 (&
             for (int r = 0; r < 4; ++r) {
                 const float na = acc[i][j][r] * inv * ga[j][r];
                 const float nb = acc[i][j + 2][r] * inv * gb[j][r];
-                lo[r] = OutT(na * c[j][0][r] - nb * c[j][2][r]);
-                hi[r] = OutT(nb * c[j][1][r] + na * c[j][3][r]);
+                const int a = 2 * (r >> 1);
+                lo[r] = OutT(na * c[j][0][a] - nb * c[j][0][a + 1]);
+                hi[r] = OutT(nb * c[j][1][a] + na * c[j][1][a + 1]);
             }
             if (m < p.M) {
                 *reinterpret_cast<out4*>(crow + d) = lo;
                 *reinterpret_cast<out4*>(crow + d + 64) = hi;
             }
         }
-        // Two rows' loads in flight at most: hoisting every row's would raise the
+        // Three rows' angles in flight at most: hoisting every row's would raise the
         // register peak.
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -503,11 +505,10 @@ __device__ __forceinline__ void light_epilogue(const Params& p, const f32x4 (&la
             const int d = 32 * (wn & 1) + 4 * q16 + 16 * wm;
             const f32x4 ga = *reinterpret_cast<const f32x4*>(g + d);
             const f32x4 gb = *reinterpret_cast<const f32x4*>(g + d + 64);
+            // (cos, sin) of angles d / 2, d / 2 + 1 and of d / 2 + 32, + 33 (see qk_rope_epilogue).
             const size_t mc = (size_t)min(m, p.M - 1) * 128;
-            const f32x4 clo = *reinterpret_cast<const f32x4*>(p.cos_t + mc + d);
-            const f32x4 chi = *reinterpret_cast<const f32x4*>(p.cos_t + mc + d + 64);
-            const f32x4 slo = *reinterpret_cast<const f32x4*>(p.sin_t + mc + d);
-            const f32x4 shi = *reinterpret_cast<const f32x4*>(p.sin_t + mc + d + 64);
+            const f32x4 cl = *reinterpret_cast<const f32x4*>(p.cs_t + mc + d);
+            const f32x4 ch = *reinterpret_cast<const f32x4*>(p.cs_t + mc + d + 64);
             phase_barrier();
             const int w0 = wave & ~3;
             const float ss = (lred[w0 * 16 + r16] + lred[(w0 + 1) * 16 + r16]) +
@@ -518,8 +519,9 @@ __device__ __forceinline__ void light_epilogue(const Params& p, const f32x4 (&la
             for (int r = 0; r < 4; ++r) {
                 const float na = lacc[0][r] * inv * ga[r];
                 const float nb = lacc[1][r] * inv * gb[r];
-                lo[r] = OutT(na * clo[r] - nb * slo[r]);
-                hi[r] = OutT(nb * chi[r] + na * shi[r]);
+                const int a = 2 * (r >> 1);
+                lo[r] = OutT(na * cl[a] - nb * cl[a + 1]);
+                hi[r] = OutT(nb * ch[a] + na * ch[a + 1]);
             }
             if (m < p.M) {
                 OutT* crow = static_cast<OutT*>(p.C) + (size_t)m * p.ldc + head_col;
@@ -1094,8 +1096,8 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
     const bool qk = a.epilogue == EPI_QKROPE;
     const int other = a.w_k32 || a.a_k32_rows || a.c_k32_rows || qk ? -1 : 1;
     if (qk && (a.c_dtype != a.dtype || !a.w_k32 || a.qk_cols <= 0 || a.qk_cols % BN_QK || a.qk_cols > a.N ||
-               a.k_col <= 0 || a.k_col % 128 || a.k_col >= a.qk_cols || !a.gq || !a.gk || !a.cos_t || !a.sin_t ||
-               a.ldc % 4 || (uintptr_t)a.C % 8))
+               a.k_col <= 0 || a.k_col % 128 || a.k_col >= a.qk_cols || !a.gq || !a.gk || !a.cs_t ||
+               (uintptr_t)a.cs_t % 16 || a.ldc % 4 || (uintptr_t)a.C % 8))
         return -1;
     if (a.dtype == DT_F32 || a.K % pingpong::BK) return other;
     if (a.epilogue == EPI_STORE && a.c_dtype != DT_F32 && a.c_dtype != a.dtype) return -1;
@@ -1128,7 +1130,7 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
         if (a.epilogue == EPI_GATE_RESID) v = v && aligned(a.resid, 16) && aligned(a.gate, 16) && a.ld_resid % 4 == 0;
         p.vec = v;
     }
-    p.qk_cols = a.qk_cols; p.k_col = a.k_col; p.gq = a.gq; p.gk = a.gk; p.cos_t = a.cos_t; p.sin_t = a.sin_t;
+    p.qk_cols = a.qk_cols; p.k_col = a.k_col; p.gq = a.gq; p.gk = a.gk; p.cs_t = a.cs_t;
     p.qk_eps = a.qk_eps;
     p.w_bytes = (uint32_t)((long)a.N * a.ldw * 2);
     p.w_row_bytes = a.w_k32 ? pingpong::ROWB : (int)(a.ldw * 2);
@@ -1322,8 +1324,8 @@ int gemm16_pingpong(const GemmArgs& a, hipStream_t s)
         // tiles were split, else the tail rows.
         const int r0 = p.split_all ? 0 : p.m_full * pingpong::BM;
         const int rc = qk_norm_rope_permuted(a.C, a.dtype, r0, a.M, (int)(a.k_col / 128),
-                                             (int)((a.qk_cols - a.k_col) / 128), a.ldc, a.k_col, a.gq, a.gk, a.cos_t,
-                                             a.sin_t, a.qk_eps, s);
+                                             (int)((a.qk_cols - a.k_col) / 128), a.ldc, a.k_col, a.gq, a.gk, a.cs_t,
+                                             a.qk_eps, s);
         if (rc) return rc;
     }
     const hipError_t e = hipGetLastError();

@@ -56,13 +56,12 @@ struct GemmArgs {
     void* split_ws = nullptr;
     size_t split_ws_bytes = 0;
     // EPI_QKROPE: Q / K columns [0, qk_cols) (K heads from k_col), their gammas [128],
-    // cos / sin [M][128] FP32.
+    // and each row's rotary angles as rope_pack writes them, [M][64] (cos, sin) pairs.
     int qk_cols = 0;
     long k_col = 0;
     const float* gq = nullptr;
     const float* gk = nullptr;
-    const float* cos_t = nullptr;
-    const float* sin_t = nullptr;
+    const float* cs_t = nullptr;
     float qk_eps = 1e-6f;
 };
 int gemm(const GemmArgs& a, hipStream_t stream);
@@ -118,10 +117,15 @@ int qk_norm_rope_qk(void* x, int dtype, int rows, int nq, int nk, long row_strid
                     const float* gk, const float* cos_t, const float* sin_t, hipStream_t s);
 // The same in place on rows [r0, r1) whose Q / K head values are stored permuted
 // (qk_stored_column order, as a QKV GEMM over permuted weights writes them): each head
-// is normalised and rotated and written back in natural order.
+// is normalised and rotated and written back in natural order. cs_t: the rows' rotary
+// angles as rope_pack writes them, [rows][64] (cos, sin).
 int qk_norm_rope_permuted(void* x, int dtype, int r0, int r1, int nq, int nk, long row_stride, long k_offset,
-                          const float* gq, const float* gk, const float* cos_t, const float* sin_t, float eps,
-                          hipStream_t s);
+                          const float* gq, const float* gk, const float* cs_t, float eps, hipStream_t s);
+// ERNIE rotary tables [rows][128] whose columns 2k and 2k + 1 repeat angle k (the layout
+// src/conditioning.cpp:34-37 builds) -> out [rows][64][2] = (cos, sin) of each angle, the
+// form the fused Q/K epilogue reads. Where the two columns of a pair differ (another
+// table layout), both values of the pair are NaN, so such a table cannot pass unnoticed.
+int rope_pack(const float* cos_t, const float* sin_t, int rows, float* out, hipStream_t s);
 int gelu_inplace(void* x, int dtype, size_t n, hipStream_t s);
 int residual_add(const void* a, int a_dtype, const void* b, int b_dtype, float* out, size_t n, hipStream_t s);
 int euler_step(const float* x, const float* v, float delta, size_t n, float* out, hipStream_t s);

@@ -412,14 +412,14 @@ __global__ void __launch_bounds__(256) transpose_kernel(const E* __restrict__ in
 // One wave per (row, head) of rows [r0, r1): lane l takes head dimensions l and l + 64
 // from their permuted columns, and writes the normalised, rotated pair back to columns
 // l and l + 64. Every load of a head precedes its stores (the stores depend on the
-// wave-wide sum), so rewriting the head in place is safe.
+// wave-wide sum), so rewriting the head in place is safe. The angles come packed
+// (rope_pack): dimension d rotates by angle d / 2, whose (cos, sin) pair is at 2 (d / 2).
 template <typename T>
 __global__ void __launch_bounds__(256) qk_rope_permuted_kernel(T* __restrict__ x, int r0, int r1, int nq, int nk,
                                                                long row_stride, long k_offset,
                                                                const float* __restrict__ gq,
                                                                const float* __restrict__ gk,
-                                                               const float* __restrict__ cos_t,
-                                                               const float* __restrict__ sin_t, float eps)
+                                                               const float* __restrict__ cs_t, float eps)
 {
     const int lane = threadIdx.x & 63;
     const long w = (long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
@@ -434,11 +434,26 @@ __global__ void __launch_bounds__(256) qk_rope_permuted_kernel(T* __restrict__ x
     const float ss = wave_sum(a * a + b * b);
     const float inv = 1.0f / sqrtf(ss / 128.f + eps);
     const float na = a * inv * g[d0], nb = b * inv * g[d1];
-    const float* c = cos_t + (size_t)m * 128;
-    const float* sn = sin_t + (size_t)m * 128;
-    const float lo = na * c[d0] - nb * sn[d0], hi = nb * c[d1] + na * sn[d1];
+    const f32x2 c0 = *reinterpret_cast<const f32x2*>(cs_t + (size_t)m * 128 + 2 * (d0 >> 1));
+    const f32x2 c1 = *reinterpret_cast<const f32x2*>(cs_t + (size_t)m * 128 + 2 * (d1 >> 1));
+    const float lo = na * c0[0] - nb * c0[1], hi = nb * c1[0] + na * c1[1];
     v[d0] = T(lo);
     v[d1] = T(hi);
+}
+
+// Angle i = (row, k) of the flattened [rows][64]: columns 2k and 2k + 1 of the cos and sin rows must
+// hold the same bits; their value goes to out[r][k] as a (cos, sin) pair, else NaN.
+__global__ void rope_pack_kernel(const float* __restrict__ cos_t, const float* __restrict__ sin_t, size_t n,
+                                 float* __restrict__ out)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const f32x2 c = *reinterpret_cast<const f32x2*>(cos_t + 2 * i);
+        const f32x2 sn = *reinterpret_cast<const f32x2*>(sin_t + 2 * i);
+        const bool same =
+            __float_as_uint(c[0]) == __float_as_uint(c[1]) && __float_as_uint(sn[0]) == __float_as_uint(sn[1]);
+        *reinterpret_cast<f32x2*>(out + 2 * i) =
+            same ? f32x2{c[0], sn[0]} : f32x2{__builtin_nanf(""), __builtin_nanf("")};
+    }
 }
 
 __global__ void fill_int_kernel(int* __restrict__ p, int value, size_t n)
@@ -781,21 +796,29 @@ int transpose2d(const void* in, int dt, int rows, int cols, void* out, hipStream
 }
 
 int qk_norm_rope_permuted(void* x, int dt, int r0, int r1, int nq, int nk, long row_stride, long k_offset,
-                          const float* gq, const float* gk, const float* cos_t, const float* sin_t, float eps,
-                          hipStream_t s)
+                          const float* gq, const float* gk, const float* cs_t, float eps, hipStream_t s)
 {
-    if (!x || !gq || !gk || !cos_t || !sin_t || r0 < 0 || r1 < r0 || nq < 0 || nk < 0 || dt == DT_F32 ||
-        !valid_dt(dt))
+    if (!x || !gq || !gk || !cs_t || (uintptr_t)cs_t % 8 || r0 < 0 || r1 < r0 || nq < 0 || nk < 0 ||
+        dt == DT_F32 || !valid_dt(dt))
         return -1;
     const long waves = (long)(r1 - r0) * (nq + nk);
     if (!waves) return 0;
     const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
     if (dt == DT_F16)
         hipLaunchKernelGGL(qk_rope_permuted_kernel<f16>, grid, block, 0, s, static_cast<f16*>(x), r0, r1, nq, nk,
-                           row_stride, k_offset, gq, gk, cos_t, sin_t, eps);
+                           row_stride, k_offset, gq, gk, cs_t, eps);
     else
         hipLaunchKernelGGL(qk_rope_permuted_kernel<bf16>, grid, block, 0, s, static_cast<bf16*>(x), r0, r1, nq, nk,
-                           row_stride, k_offset, gq, gk, cos_t, sin_t, eps);
+                           row_stride, k_offset, gq, gk, cs_t, eps);
+    return launch_status();
+}
+
+int rope_pack(const float* cos_t, const float* sin_t, int rows, float* out, hipStream_t s)
+{
+    if (!cos_t || !sin_t || !out || rows < 0 || ((uintptr_t)cos_t | (uintptr_t)sin_t | (uintptr_t)out) % 8) return -1;
+    const size_t n = (size_t)rows * 64;
+    if (!n) return 0;
+    hipLaunchKernelGGL(rope_pack_kernel, dim3(grid_for(n)), dim3(256), 0, s, cos_t, sin_t, n, out);
     return launch_status();
 }
 

@@ -216,7 +216,12 @@ int ernie_hip_block_count(const ernie_hip_ctx* ctx);
 /* One DiT block = block.ncnn.param: in0 = x [S][dim] FP32 (device), mods =
  * in1..in6 as 6 x dim FP32 (shift_sa, scale_sa, gate_sa, shift_mlp, scale_mlp,
  * gate_mlp), cos/sin = in7/in8 [S][128] FP32, mask = in9 one-row additive [S]
- * (NULL allowed) and/or valid_keys (0 = all). out0 [S][dim] FP32; out may alias x. */
+ * (NULL allowed) and/or valid_keys (0 = all). out0 [S][dim] FP32; out may alias x.
+ * cos/sin hold each rotary angle in two adjacent columns (2k, 2k + 1), as the
+ * reference's tables do (src/conditioning.cpp:34-37): 16-bit blocks of a width that is a
+ * multiple of 256 read the angles once per pair, and a row whose pair columns differ gets
+ * NaN Q/K values there (a table of another layout shows as a non-finite output, never as
+ * a silently different one). */
 int ernie_hip_block_forward(ernie_hip_ctx* ctx, int index, const float* x, float* out, const float* mods,
                             const float* cos_t, const float* sin_t, const float* mask, int valid_keys, int S);
 /* run_block_sequence core (src/block_sequence.cpp:56-94): blocks[0..count) in order.

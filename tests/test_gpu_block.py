@@ -382,3 +382,25 @@ def test_qk_rounding_orders(ctx, dt, dim, ffn, S, image, valid):
     with pytest.raises(E.ErnieError):
         ctx.call("set_qk_rounding", 2)
     ctx.call("block_release", 8)
+
+
+@pytest.mark.parametrize("dt", [E.FP16, E.BF16], ids=lambda d: NAMES[d])
+def test_rotary_pairs_must_repeat(ctx, dt):
+    # 16-bit blocks read each rotary angle once from its pair of columns (2k, 2k + 1). The
+    # reference's tables repeat every angle there (src/conditioning.cpp:34-37); a table
+    # whose pair columns differ makes the output non-finite instead of silently using one
+    # of the two values.
+    w = small_block(dim=256, ffn=512, seed=21)
+    x, mods, cos, sin, mask = small_inputs(S=300, dim=256, image=(16, 16), valid=30, seed=22)
+    ctx.block_upload(9, w, 256, 512, dt)
+    keys = int(np.sum(mask == 0))
+    good = run_block(ctx, 9, x, mods, cos, sin, mask, keys)
+    assert np.isfinite(good).all()
+    ref = O.block_forward(w, x, mods, cos, sin, mask)
+    g = kat.gate(good, ref, *kat.BLOCK_GATES[NAMES[dt]])
+    assert g["passed"], g
+    bad = cos.copy()
+    bad[7, 11] += 0.25  # column 11 no longer repeats column 10 in row 7
+    assert not np.isfinite(run_block(ctx, 9, x, mods, bad, sin, mask, keys)).all()
+    np.testing.assert_array_equal(run_block(ctx, 9, x, mods, cos, sin, mask, keys), good)
+    ctx.call("block_release", 9)
