@@ -62,6 +62,10 @@ constexpr int V_BASE = 2 * KSTAGE;           // the V ring follows the two K sta
 constexpr int LDS_BYTES = V_BASE + 2 * KV_BYTES;
 constexpr uint32_t kRsrcFlags = 0x00020000;
 constexpr float kRescaleSlack = 8.0f;
+// A tile whose maximum was not taken before its softmax (see step) has it taken after
+// all when its probabilities sum to at least this much: below it every probability is
+// below 2^6, so the tile maximum is below offset + 6 and could not raise the offset.
+constexpr float kLazyCheck = 64.0f;
 constexpr int kMaxParts = 16;  // most key-range parts of the split query tile
 
 struct Params {
@@ -408,14 +412,26 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
             sacc[n & 1] = Mfma<T>::run(__builtin_bit_cast(vec8, kf[n]), qf[n >> 1], sacc[n & 1]);
         }
     };
+    // Tiles whose scores are masked per lane here: past the valid keys, or (causal)
+    // across this wave's diagonal, or any tile under a mask tensor.
+    auto needs_prep = [&](int it) {
+        const int kv0 = it * BKV;
+        return MM != MASK_NONE || kv0 + BKV > p.kv_end || (p.causal && kv0 + BKV - 1 > q_base + wave * 32 + p.qk_off);
+    };
+    // Tile maximum in the log2 domain (scores already scaled by c when `scaled`).
+    auto tile_max = [&](const f32x16 (&sacc)[2], bool scaled) {
+        float tmax = max3(sacc[0][0], sacc[0][1], sacc[0][2]);
+#pragma unroll
+        for (int i = 3; i < 31; i += 2) tmax = max3(tmax, sacc[i >> 4][i & 15], sacc[(i + 1) >> 4][(i + 1) & 15]);
+        tmax = pair_max(fmaxf(tmax, sacc[1][15]));
+        return scaled ? tmax : tmax * c;
+    };
     // Mask, bound and tile maximum (log2 domain) of tile `it`; raises the running
     // offset when the maximum passes it by more than the slack. Returns the factor
     // the softmax applies to the scores: 1 when they were scaled here, else c.
     auto prep = [&](f32x16 (&sacc)[2], int it) -> float {
         const int kv0 = it * BKV;
-        // Masked per lane: past the valid keys, or (causal) across this wave's diagonal.
-        const bool scaled = MM != MASK_NONE || kv0 + BKV > p.kv_end ||
-                            (p.causal && kv0 + BKV - 1 > q_base + wave * 32 + p.qk_off);
+        const bool scaled = needs_prep(it);
         if (scaled) {
 #pragma unroll
             for (int t = 0; t < 2; ++t)
@@ -425,11 +441,7 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
                     sacc[t][r] = kv0 + kk < key_lim ? sacc[t][r] * c : -INFINITY;
                 }
         }
-        float tmax = max3(sacc[0][0], sacc[0][1], sacc[0][2]);
-#pragma unroll
-        for (int i = 3; i < 31; i += 2) tmax = max3(tmax, sacc[i >> 4][i & 15], sacc[(i + 1) >> 4][(i + 1) & 15]);
-        tmax = pair_max(fmaxf(tmax, sacc[1][15]));
-        if (!scaled) tmax *= c;
+        const float tmax = tile_max(sacc, scaled);
         const bool raise = tmax > m_run + kRescaleSlack;
         if (__any(raise)) {
             const float m_new = raise ? tmax : m_run;
@@ -456,6 +468,28 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) l_run = Mfma<T>::rowsum(pf[t][hh], l_run);
     };
+    // The offset check of an unmasked tile whose maximum was not taken before its
+    // softmax: its probabilities were computed with the running offset, adding to l_run
+    // from l_before. When they sum to less than kLazyCheck no score passed the offset by
+    // the slack, which is the common case after the first tiles, and they stand. Else
+    // the tile maximum decides as prep would have: if it raises the offset, O and
+    // l_before are rescaled and the probabilities recomputed, so the outcome is exactly
+    // prep's, in the same order of operations.
+    auto settle = [&](const f32x16 (&cur)[2], float l_before, vec8 (&pf)[2][2]) {
+        if (!__any(pair_sum(l_run - l_before) >= kLazyCheck)) return;
+        const float tmax = tile_max(cur, false);
+        const bool raise = tmax > m_run + kRescaleSlack;
+        if (!__any(raise)) return;
+        const float m_new = raise ? tmax : m_run;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run = l_before * alpha;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
+        m_run = m_new;
+        softmax(cur, c, pf);
+    };
     // O^T += V^T P^T; P's register r of (t, hh) is key 32t + 16hh + 8(r/4 & 1) + 4g + r%4.
     // MFMA k (0..15) takes key block b = k / 4 (keys 16 b .. + 15, i.e. t = b / 2,
     // hh = b % 2) and value group dt = k % 4; its V^T operand is two transposing
@@ -480,19 +514,23 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
     };
 
     // Software pipeline over the key tiles i = 0 .. n-1 of [it0, it1): step i computes
-    // S of tile i+1 on the matrix cores while the VALU turns the prepared S of tile i
-    // into probabilities, then accumulates P_i V_i and prepares tile i+1. K_{i+1} and
-    // V_i are in LDS at the top of step i; it loads K_{i+2} and V_{i+1} into the
-    // stages tiles i and i-1 left.
+    // S of tile i+1 on the matrix cores while the VALU turns the S of tile i into
+    // probabilities, then accumulates P_i V_i. K_{i+1} and V_i are in LDS at the top of
+    // step i; it loads K_{i+2} and V_{i+1} into the stages tiles i and i-1 left.
+    // Masked tiles and the first one are prepared (bound, maximum, offset) before their
+    // softmax; the others take the running offset as it stands and are settled after
+    // it, which almost never has to take their maximum.
     const int n = it1 - it0;
     f32x16 sa[2], sb[2];
     vec8 pf[2][2];
     float cs_cur = c, cs_nxt = c;
+    bool lazy_cur = false, lazy_nxt = false;  // the tile's maximum was not taken before its softmax
     // P = i % 2 as a compile-time constant: K_{i+1} sits in stage 1 - P, V_i in stage P.
     auto step = [&](int i, f32x16 (&cur)[2], f32x16 (&nxt)[2], auto has_next, auto parity) {
         constexpr int P = decltype(parity)::value;
         __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // this wave's loads of K_{i+1}, V_i landed
         lds_barrier();                                         // ... every wave's; tile i-1 fully consumed
+        const float l_before = l_run;
         if constexpr (decltype(has_next)::value) {
             if (i + 2 < n) issue_k(it0 + i + 2, P);
             issue_v(it0 + i + 1, 1 - P);
@@ -519,10 +557,13 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
                 if ((k & 3) == 3) l_run = Mfma<T>::rowsum(pf[k >> 3][(k >> 2) & 1], l_run);
                 __builtin_amdgcn_sched_barrier(0);
             }
+            if (lazy_cur) settle(cur, l_before, pf);
             pv(P, pf);
-            cs_nxt = prep(nxt, it0 + i + 1);
+            lazy_nxt = !needs_prep(it0 + i + 1);
+            cs_nxt = lazy_nxt ? c : prep(nxt, it0 + i + 1);
         } else {
             softmax(cur, cs_cur, pf);
+            if (lazy_cur) settle(cur, l_before, pf);
             pv(P, pf);
         }
     };
@@ -542,12 +583,15 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
         for (; i + 2 < n; i += 2) {
             step(i, sa, sb, more(), even());
             cs_cur = cs_nxt;
+            lazy_cur = lazy_nxt;
             step(i + 1, sb, sa, more(), odd());
             cs_cur = cs_nxt;
+            lazy_cur = lazy_nxt;
         }
         if (n - i == 2) {
             step(i, sa, sb, more(), even());
             cs_cur = cs_nxt;
+            lazy_cur = lazy_nxt;
             step(i + 1, sb, sa, last(), odd());
         } else {
             step(i, sa, sb, last(), even());
