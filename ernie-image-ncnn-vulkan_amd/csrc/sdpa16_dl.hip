@@ -6,7 +6,8 @@
 // valid-key bound. Every mask form goes through the same arithmetic, so a row
 // mask and its dense broadcast give bitwise identical results.
 //
-//   * One workgroup = 4 waves = 128 queries of one head; each wave holds its 32
+//   * One workgroup = 4 waves = 128 queries of one head (8 waves = 256 queries when the
+//     unmasked problem has whole 256-query tiles); each wave holds its 32
 //     queries' Q fragments in registers and computes S^T = K Q^T, so each lane owns
 //     one query column and the probabilities are already the B operand of
 //     O^T = V^T P^T. Lanes l and l ^ 32 share a query: the tile maximum is exchanged
@@ -76,10 +77,11 @@ struct Params {
     const float* mask; long mask_hs;  // additive FP32 mask: one row [sk] or per query [sq][sk] per head
     float scale_log2;
     int causal, qk_off;  // causal: keys > query + qk_off (= sk - sq) excluded
-    // Split of the last, partial query tile (sq % 128 queries) along the keys:
-    // tail_parts > 0 parts per head write unnormalised FP32 O and their (m, l) to
-    // part_o [heads * tail_parts][128][128] / part_ml [heads * tail_parts][128][2].
-    int full_qt, tail_parts;
+    // Split of the last, partial query tile (sq % part_rows queries, part_rows = the
+    // workgroup's queries) along the keys: tail_parts > 0 parts per head write
+    // unnormalised FP32 O and their (m, l) to part_o [heads * tail_parts][part_rows][128]
+    // / part_ml [heads * tail_parts][part_rows][2].
+    int full_qt, tail_parts, part_rows;
     float* part_o;
     float* part_ml;
 };
@@ -95,8 +97,8 @@ __global__ void __launch_bounds__(256) combine_kernel(Params p, int tail_q)
     if (wq >= p.heads * tail_q) return;
     const int lane = threadIdx.x & 63;
     const int h = wq / tail_q, ql = wq - h * tail_q;
-    const float* ml = p.part_ml + ((size_t)h * p.tail_parts * BQ + ql) * 2;
-    const float* po = p.part_o + ((size_t)h * p.tail_parts * BQ + ql) * D + 2 * lane;
+    const float* ml = p.part_ml + ((size_t)h * p.tail_parts * p.part_rows + ql) * 2;
+    const float* po = p.part_o + ((size_t)h * p.tail_parts * p.part_rows + ql) * D + 2 * lane;
     // Every part's loads are issued before the first use (at most kMaxParts parts);
     // the merge then runs in part order.
     float mv[kMaxParts], lv[kMaxParts];
@@ -104,9 +106,9 @@ __global__ void __launch_bounds__(256) combine_kernel(Params p, int tail_q)
 #pragma unroll
     for (int q = 0; q < kMaxParts; ++q) {
         if (q < p.tail_parts) {
-            mv[q] = ml[(size_t)q * BQ * 2];
-            lv[q] = ml[(size_t)q * BQ * 2 + 1];
-            ov[q] = *reinterpret_cast<const f32x2*>(po + (size_t)q * BQ * D);
+            mv[q] = ml[(size_t)q * p.part_rows * 2];
+            lv[q] = ml[(size_t)q * p.part_rows * 2 + 1];
+            ov[q] = *reinterpret_cast<const f32x2*>(po + (size_t)q * p.part_rows * D);
         }
     }
     float M = -INFINITY;
@@ -123,7 +125,7 @@ __global__ void __launch_bounds__(256) combine_kernel(Params p, int tail_q)
             O1 += ov[q][1] * w;
         }
     }
-    const int qi = p.full_qt * BQ + ql, d = 2 * lane;
+    const int qi = p.full_qt * p.part_rows + ql, d = 2 * lane;
     typedef T t2 __attribute__((ext_vector_type(2)));
     *reinterpret_cast<t2*>(static_cast<T*>(p.o) + (size_t)h * p.o_hs + (size_t)qi * p.o_rs + (size_t)(d >> 5) * p.o_ds +
                            (d & 31)) = t2{T(O0 / L), T(O1 / L)};
@@ -227,13 +229,20 @@ __device__ __forceinline__ void lgkm_wait_for(u32x4& a, int after)
 // returned and the memory clobber keeps LDS accesses on their side.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// A workgroup of NW waves: BQW queries, and RPW key rows of each tile loaded per wave
+// by IPW 1-KiB instructions.
+template <int NW> struct Waves {
+    static constexpr int BQW = 32 * NW, RPW = BKV / NW, IPW = RPW / 4;
+};
+
 // Mask modes: none, one row broadcast over the queries, one row per query.
 enum { MASK_NONE = 0, MASK_ROW = 1, MASK_DENSE = 2 };
 
-template <typename T, int MM>
-__global__ void __launch_bounds__(256, 2) kernel(Params p)
+template <typename T, int MM, int NW>
+__global__ void __launch_bounds__(64 * NW, 8 / NW) kernel(Params p)
 {
     typedef typename Mfma<T>::vec vec8;
+    constexpr int BQW = Waves<NW>::BQW, RPW = Waves<NW>::RPW, IPW = Waves<NW>::IPW;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[LDS_BYTES];
 
     // Workgroup -> (head, query tile[, key range]). Workgroup b runs on XCD b % 8:
@@ -243,9 +252,9 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
     const int ntiles = (p.kv_end + BKV - 1) / BKV;
     int h, q_base, it0 = 0, it1 = ntiles, part = -1;
     {
-        const int full = p.tail_parts ? p.full_qt * p.heads : ((p.sq + BQ - 1) / BQ) * p.heads;
+        const int full = p.tail_parts ? p.full_qt * p.heads : ((p.sq + BQW - 1) / BQW) * p.heads;
         const int tail = p.tail_parts * p.heads;
-        const int qt = p.tail_parts ? p.full_qt : (p.sq + BQ - 1) / BQ;
+        const int qt = p.tail_parts ? p.full_qt : (p.sq + BQW - 1) / BQW;
         const int bid = blockIdx.x;
         int f = -1, u = -1;
         if ((full & 7) == 0 && (tail & 7) == 0) {
@@ -258,14 +267,14 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
         }
         if (f >= 0) {
             h = f / qt;
-            q_base = (f - h * qt) * BQ;
+            q_base = (f - h * qt) * BQW;
         } else {
             h = u / p.tail_parts;
             part = u - h * p.tail_parts;
             q_base = p.full_qt * BQ;
         }
         // Causal: no key tile past the one holding the last query's diagonal.
-        const int nt = p.causal ? min(ntiles, (min(q_base + BQ, p.sq) - 1 + p.qk_off) / BKV + 1) : ntiles;
+        const int nt = p.causal ? min(ntiles, (min(q_base + BQW, p.sq) - 1 + p.qk_off) / BKV + 1) : ntiles;
         it1 = nt;
         if (part >= 0) {
             it0 = (int)((long)nt * part / p.tail_parts);
@@ -277,6 +286,9 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lrow = lane & 31, g = lane >> 5;
     const int my_q = q_base + wave * 32 + lrow;
+    // A wave whose 32 queries all lie past sq (in a partial last query tile) only loads
+    // its share of the K / V tiles and keeps the barriers.
+    const bool active = q_base + wave * 32 < p.sq;
     // Keys at or past key_lim are excluded: the valid-key bound, and the diagonal when causal.
     const int key_lim = p.causal ? min(p.kv_end, my_q + 1 + p.qk_off) : p.kv_end;
 
@@ -308,10 +320,10 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
     // four 1-KiB instructions each (4 rows x 256 bytes); lane l lands at row l >> 4,
     // physical chunk l & 15. K (with its mask row) and V have rings of their own
     // because K runs one tile ahead of V.
-    uint32_t k_src[4], v_src[4];
+    uint32_t k_src[4], v_src[4];  // IPW <= 4 used
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int row = wave * 16 + q * 4 + (lane >> 4);
+    for (int q = 0; q < IPW; ++q) {
+        const int row = wave * RPW + q * 4 + (lane >> 4);
         k_src[q] = (uint32_t)(((long)row * p.k_rs * 2) + (((lane & 15) ^ kswz(row)) << 4));
         v_src[q] = (uint32_t)(((long)row * p.v_rs * 2) + (((lane & 15) ^ vswz(row)) << 4));
     }
@@ -321,8 +333,8 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
     auto issue_k = [&](int it, int slot) {
         uint8_t* st = kstage(slot);
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr_t)(st + (wave * 16 + q * 4) * ROWB), 16, k_src[q],
+        for (int q = 0; q < IPW; ++q)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr_t)(st + (wave * RPW + q * 4) * ROWB), 16, k_src[q],
                                                      it * k_tile, 0, 0);
         if constexpr (MASKROW) {
             if (wave == 0)
@@ -332,8 +344,8 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
     auto issue_v = [&](int it, int slot) {
         uint8_t* st = vstage(slot);
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_ptr_t)(st + (wave * 16 + q * 4) * ROWB), 16, v_src[q],
+        for (int q = 0; q < IPW; ++q)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_ptr_t)(st + (wave * RPW + q * 4) * ROWB), 16, v_src[q],
                                                      it * v_tile, 0, 0);
     };
 
@@ -577,6 +589,18 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
         if (n > 1) issue_k(it0 + 1, 1);
         __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
         lds_barrier();
+        if (!active) {
+            // Loads and barriers only, step for step as below.
+            for (int i = 0; i < n; ++i) {
+                __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));
+                lds_barrier();
+                if (i + 1 < n) {
+                    if (i + 2 < n) issue_k(it0 + i + 2, i & 1);
+                    issue_v(it0 + i + 1, 1 - (i & 1));
+                }
+            }
+            return;
+        }
         qk(0, it0 * BKV, sa);
         cs_cur = prep(sa, it0);
         int i = 0;  // always even at the top of the loop
@@ -598,12 +622,13 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
         }
     }
 
+    if (!active) return;  // n == 0
     l_run = pair_sum(l_run);
     if (part >= 0) {
         // Key-range part of the split tail tile: unnormalised O and (m, l) for combine_kernel.
         const size_t slot = (size_t)h * p.tail_parts + part;
         const int ql = wave * 32 + lrow;
-        float* po = p.part_o + (slot * BQ + ql) * D;
+        float* po = p.part_o + (slot * p.part_rows + ql) * D;
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -612,8 +637,8 @@ __global__ void __launch_bounds__(256, 2) kernel(Params p)
                 *reinterpret_cast<f32x4*>(po + 32 * dt + 8 * rq + 4 * g) = v;
             }
         if (g == 0) {
-            p.part_ml[(slot * BQ + ql) * 2] = m_run;
-            p.part_ml[(slot * BQ + ql) * 2 + 1] = l_run;
+            p.part_ml[(slot * p.part_rows + ql) * 2] = m_run;
+            p.part_ml[(slot * p.part_rows + ql) * 2 + 1] = l_run;
         }
         return;
     }
@@ -661,30 +686,42 @@ int sdpa16_d128(const SdpaArgs& a, hipStream_t s)
     p.mask_hs = a.mask && a.mask_heads > 1 ? (long)a.sk * (dense ? a.sq : 1) : 0;
     const float scale = a.scale > 0.f ? a.scale : 1.f / sqrtf(128.f);
     p.scale_log2 = scale * sdl::kLog2e;
+    // Workgroups of 8 waves (256 queries, one per CU) when the unmasked, non-causal
+    // problem has whole 256-query tiles, else 4 waves (128 queries, two per CU). At 4096
+    // queries x 4160 keys the 8-wave form took 273 against 280 us, bitwise the same; with a
+    // partial last tile its key-range parts run on two of a CU's four SIMDs after the full
+    // tiles and cost more than that (4160 queries: 295-299 against 285 us).
+    const bool nw8 = !a.mask && !a.causal && a.sq % 256 == 0;
+    const int bqw = nw8 ? 256 : 128;
     // A partial last query tile is split along the keys when a workspace is given:
     // kSdpaSlots parts over all heads, at most 16 and at least 1 per head.
-    p.full_qt = a.sq / sdl::BQ;
-    const int tail_q = a.sq - p.full_qt * sdl::BQ;
+    p.part_rows = bqw;
+    p.full_qt = a.sq / bqw;
+    const int tail_q = a.sq - p.full_qt * bqw;
     if (tail_q && p.full_qt && a.split_ws) {
         int parts = std::min(std::min(sdl::kMaxParts, ntiles), std::max(1, kSdpaSlots / a.heads));
-        const size_t per_part = (size_t)a.heads * sdl::BQ * (sdl::D + 2) * sizeof(float);
+        const size_t per_part = (size_t)a.heads * bqw * (sdl::D + 2) * sizeof(float);
         while (parts > 1 && (size_t)parts * per_part > a.split_ws_bytes) --parts;
         if (parts > 1) {
             p.tail_parts = parts;
             p.part_o = static_cast<float*>(a.split_ws);
-            p.part_ml = p.part_o + (size_t)a.heads * parts * sdl::BQ * sdl::D;
+            p.part_ml = p.part_o + (size_t)a.heads * parts * bqw * sdl::D;
         }
     }
-    const int wgs = p.tail_parts ? (p.full_qt + p.tail_parts) * a.heads : ((a.sq + sdl::BQ - 1) / sdl::BQ) * a.heads;
+    const int wgs = p.tail_parts ? (p.full_qt + p.tail_parts) * a.heads : ((a.sq + bqw - 1) / bqw) * a.heads;
     const dim3 grid(wgs), block(256);
-    if (a.dtype == DT_F16) {
-        if (dense) hipLaunchKernelGGL((sdl::kernel<f16, sdl::MASK_DENSE>), grid, block, 0, s, p);
-        else if (a.mask) hipLaunchKernelGGL((sdl::kernel<f16, sdl::MASK_ROW>), grid, block, 0, s, p);
-        else hipLaunchKernelGGL((sdl::kernel<f16, sdl::MASK_NONE>), grid, block, 0, s, p);
+    if (nw8) {
+        const dim3 block8(512);
+        if (a.dtype == DT_F16) hipLaunchKernelGGL((sdl::kernel<f16, sdl::MASK_NONE, 8>), grid, block8, 0, s, p);
+        else hipLaunchKernelGGL((sdl::kernel<bf16, sdl::MASK_NONE, 8>), grid, block8, 0, s, p);
+    } else if (a.dtype == DT_F16) {
+        if (dense) hipLaunchKernelGGL((sdl::kernel<f16, sdl::MASK_DENSE, 4>), grid, block, 0, s, p);
+        else if (a.mask) hipLaunchKernelGGL((sdl::kernel<f16, sdl::MASK_ROW, 4>), grid, block, 0, s, p);
+        else hipLaunchKernelGGL((sdl::kernel<f16, sdl::MASK_NONE, 4>), grid, block, 0, s, p);
     } else {
-        if (dense) hipLaunchKernelGGL((sdl::kernel<bf16, sdl::MASK_DENSE>), grid, block, 0, s, p);
-        else if (a.mask) hipLaunchKernelGGL((sdl::kernel<bf16, sdl::MASK_ROW>), grid, block, 0, s, p);
-        else hipLaunchKernelGGL((sdl::kernel<bf16, sdl::MASK_NONE>), grid, block, 0, s, p);
+        if (dense) hipLaunchKernelGGL((sdl::kernel<bf16, sdl::MASK_DENSE, 4>), grid, block, 0, s, p);
+        else if (a.mask) hipLaunchKernelGGL((sdl::kernel<bf16, sdl::MASK_ROW, 4>), grid, block, 0, s, p);
+        else hipLaunchKernelGGL((sdl::kernel<bf16, sdl::MASK_NONE, 4>), grid, block, 0, s, p);
     }
     if (p.tail_parts) {
         const long n = (long)a.heads * tail_q;  // one wave per (head, query), four per workgroup

@@ -168,12 +168,14 @@ def test_sdpa_full_size_rows_against_oracle(ctx, dt):
 
 
 @pytest.mark.parametrize("dt", [E.FP16, E.BF16], ids=lambda d: NAMES[d])
-@pytest.mark.parametrize("S,H,valid", [(256, 2, 256), (512, 3, 500), (456, 2, 456), (300, 1, 290), (1088, 2, 1060)])
+@pytest.mark.parametrize("S,H,valid", [(256, 2, 256), (512, 3, 500), (1280, 2, 1270), (456, 2, 456), (300, 1, 290),
+                                         (1088, 2, 1060)])
 def test_sdpa_full_tiles_and_remainder(ctx, dt, S, H, valid):
-    # Unmasked attention at lengths around the kernel's 128-query workgroup tile:
-    # exact tiles, tiles plus a partial last tile of 72 / 44 / 64 queries (split
-    # along the keys) and valid-key counts that are not multiples of 64. Every row
-    # of every head is compared with the oracle.
+    # Unmasked attention at lengths around the kernel's workgroup tiles: whole
+    # 256-query tiles (the 8-wave form: 256, 512, 1280), 128-query tiles with a partial
+    # last tile of 72 / 44 / 64 queries, whose waves past the last query only load
+    # and keep the barriers, and valid-key counts that are not multiples of 64. Every
+    # row of every head is compared with the oracle.
     d = 128
     q = O.normal((S, H * d), 21)
     k = O.normal((S, H * d), 22)
