@@ -1188,6 +1188,14 @@ int ernie_hip_gemm(ernie_hip_ctx* ctx, const void* a, long lda, const void* w, l
     return kernel_status(ctx, gemm(g, ctx->stream), "gemm");
 }
 
+// The standalone attention takes the same key-range split of a partial last 128-query
+// tile as the block does (16-bit, head_dim 128), with the context's split workspace.
+static int attention_workspace(ernie_hip_ctx* ctx, SdpaArgs& a)
+{
+    if (a.d != 128 || a.dtype == ERNIE_DTYPE_FP32 || a.sq % 128 == 0 || a.sq < 128) return ERNIE_OK;
+    return split_workspace(ctx, a.sq, a.heads, &a.split_ws, &a.split_ws_bytes);
+}
+
 int ernie_hip_sdpa(ernie_hip_ctx* ctx, const void* q, const void* k, const void* v, void* out, int dtype, int heads,
                    int kv_heads, int sq, int sk, int d, long q_hs, long q_rs, long k_hs, long k_rs, long v_hs,
                    long v_rs, long o_hs, long o_rs, const float* mask, int mask_heads, int mask_rows, int valid_keys,
@@ -1200,6 +1208,8 @@ int ernie_hip_sdpa(ernie_hip_ctx* ctx, const void* q, const void* k, const void*
     a.sq = sq; a.sk = sk; a.d = d; a.q_hs = q_hs; a.q_rs = q_rs; a.k_hs = k_hs; a.k_rs = k_rs;
     a.v_hs = v_hs; a.v_rs = v_rs; a.o_hs = o_hs; a.o_rs = o_rs; a.mask = mask; a.mask_heads = mask_heads;
     a.mask_rows = mask_rows; a.valid_keys = valid_keys; a.scale = scale;
+    const int rc = attention_workspace(ctx, a);
+    if (rc) return rc;
     return kernel_status(ctx, sdpa(a, ctx->stream), "sdpa");
 }
 
@@ -1213,6 +1223,8 @@ int ernie_hip_sdpa_causal(ernie_hip_ctx* ctx, const void* q, const void* k, cons
     a.q = q; a.k = k; a.v = v; a.o = out; a.dtype = dtype; a.heads = heads; a.kv_heads = kv_heads;
     a.sq = sq; a.sk = sk; a.d = d; a.q_hs = q_hs; a.q_rs = q_rs; a.k_hs = k_hs; a.k_rs = k_rs;
     a.v_hs = v_hs; a.v_rs = v_rs; a.o_hs = o_hs; a.o_rs = o_rs; a.causal = 1; a.scale = scale;
+    const int rc = attention_workspace(ctx, a);
+    if (rc) return rc;
     return kernel_status(ctx, sdpa(a, ctx->stream), "sdpa causal");
 }
 

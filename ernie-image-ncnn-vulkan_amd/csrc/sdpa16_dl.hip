@@ -55,7 +55,7 @@ constexpr int kSdpaSlots = 192;
 namespace sdl {
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int BQ = 128, BKV = 64, D = 128;
+constexpr int BKV = 64, D = 128;
 constexpr int ROWB = D * 2;                 // 256 bytes per staged key row
 constexpr int KV_BYTES = BKV * ROWB;        // 16 KiB
 constexpr int KSTAGE = KV_BYTES + BKV * 4;  // K tile + its mask row
@@ -271,7 +271,7 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) kernel(Params p)
         } else {
             h = u / p.tail_parts;
             part = u - h * p.tail_parts;
-            q_base = p.full_qt * BQ;
+            q_base = p.full_qt * BQW;
         }
         // Causal: no key tile past the one holding the last query's diagonal.
         const int nt = p.causal ? min(ntiles, (min(q_base + BQW, p.sq) - 1 + p.qk_off) / BKV + 1) : ntiles;

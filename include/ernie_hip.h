@@ -97,7 +97,10 @@ int ernie_hip_gemm(ernie_hip_ctx* ctx, const void* a, long lda, const void* w, l
  * Strides in elements (head stride, row stride). mask: NULL or additive FP32
  * [mask_heads][mask_rows][sk] with mask_rows 1 (one row broadcast over queries)
  * or sq, mask_heads 1 or heads. valid_keys > 0 excludes keys >= valid_keys
- * (equivalent to the reference's -1e30 padded-text mask). scale <= 0 -> 1/sqrt(d). */
+ * (equivalent to the reference's -1e30 padded-text mask). scale <= 0 -> 1/sqrt(d).
+ * 16-bit calls with d = 128 and a partial last 128-query tile split that tile along
+ * the keys in the context's split workspace (allocated on first use and kept), as
+ * the block does. */
 int ernie_hip_sdpa(ernie_hip_ctx* ctx, const void* q, const void* k, const void* v, void* out, int dtype,
                    int heads, int kv_heads, int sq, int sk, int d, long q_head_stride, long q_row_stride,
                    long k_head_stride, long k_row_stride, long v_head_stride, long v_row_stride,

@@ -173,9 +173,10 @@ def test_sdpa_full_size_rows_against_oracle(ctx, dt):
 def test_sdpa_full_tiles_and_remainder(ctx, dt, S, H, valid):
     # Unmasked attention at lengths around the kernel's workgroup tiles: whole
     # 256-query tiles (the 8-wave form: 256, 512, 1280), 128-query tiles with a partial
-    # last tile of 72 / 44 / 64 queries, whose waves past the last query only load
-    # and keep the barriers, and valid-key counts that are not multiples of 64. Every
-    # row of every head is compared with the oracle.
+    # last tile of 72 / 44 / 64 queries (split along the keys into parts that a second
+    # launch merges; its waves past the last query only load and keep the barriers),
+    # and valid-key counts that are not multiples of 64. Every row of every head is
+    # compared with the oracle.
     d = 128
     q = O.normal((S, H * d), 21)
     k = O.normal((S, H * d), 22)
