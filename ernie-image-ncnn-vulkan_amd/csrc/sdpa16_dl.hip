@@ -7,12 +7,14 @@
 // mask and its dense broadcast give bitwise identical results.
 //
 //   * One workgroup = 4 waves = 128 queries of one head (8 waves = 256 queries when the
-//     unmasked problem has whole 256-query tiles); each wave holds its 32
-//     queries' Q fragments in registers and computes S^T = K Q^T, so each lane owns
-//     one query column and the probabilities are already the B operand of
-//     O^T = V^T P^T. Lanes l and l ^ 32 share a query: the tile maximum is exchanged
-//     with v_permlane32_swap (VALU, no LDS round trip) and the row sums are kept per
-//     lane and combined once after the last tile.
+//     unmasked problem has whole 256-query tiles); each wave holds its 32 queries' Q
+//     fragments in registers and computes S^T = K Q^T with v_mfma_f32_16x16x32 on
+//     16-key x 16-query blocks, so each lane owns two query columns (one per 16-query
+//     block) and the probabilities are already the Y operand of O^T = V^T P^T. Under
+//     this load the 16x16x32 form holds a higher clock than 32x32x16 (a probe of both
+//     at equal work: 2.04 against 1.77 GHz). The four lanes l % 16 + 16 g share a
+//     query: the tile maximum is exchanged with v_permlane16/32_swap (VALU, no LDS
+//     round trip) and the row sums are kept per lane and combined after the last tile.
 //   * exp2 is the bare v_exp_f32: results below 2^-126 flush to zero, which cannot
 //     move a row sum that is at least 1.
 //   * K and V tiles (64 keys) reach LDS through direct global->LDS loads into two
@@ -21,15 +23,19 @@
 //     load as zeros.
 //   * Software pipeline: while the matrix cores compute S of tile i+1, the VALU turns
 //     S of tile i into probabilities, in 16 hand-ordered groups (K fragment n + 2
-//     read, fragment n awaited, MFMA n, two probabilities) that sched_barrier keeps
-//     in order; then P_i V_i accumulates and tile i+1's maximum is taken. The LDS
-//     reads are inline assembly with explicit lgkmcnt waits (see ds_read_tr).
+//     read, fragment n awaited, its two MFMAs with a probability after each) that
+//     sched_barrier keeps in order; then P_i V_i accumulates and tile i+1's maximum
+//     is taken. The LDS reads are inline assembly with explicit lgkmcnt waits (see
+//     ds_read_tr).
 //   * Row sums use v_dot2_f32_{f16,bf16} on the rounded probabilities the MFMA
 //     consumes, so numerator and denominator see the same weights.
 //   * V^T fragments come from ds_read_b64_tr_b16: within each 16-lane group, lane
 //     i receives the (i % 4)-th 16-bit value at the addresses of lanes 4e + i/4
 //     (e = 0..3), so lanes pointing at 4 consecutive key rows deliver 4 keys of
-//     one head-dim column per lane.
+//     one head-dim column per lane. The MFMA sums over its 32 k positions in any
+//     order, so P and V^T only have to agree on which key sits at which position:
+//     positions 8 g .. 8 g + 7 hold keys 4 g + 0..3 and 16 + 4 g + 0..3 of the
+//     32-key chunk, the keys a lane's S^T accumulators already hold.
 //   * K rows are chunk-swizzled by (key & 15), V rows by 2 (key & 7) (32-byte
 //     pairs kept together for the transposing reads): both measured conflict-free
 //     for these read patterns.
@@ -145,8 +151,10 @@ template <> struct Mfma<f16> {
         for (int i = 0; i < 8; i += 2) acc = __builtin_amdgcn_fdot2(f16x2{p[i], p[i + 1]}, one, acc, false);
         return acc;
     }
-    static __device__ __forceinline__ f32x16 run(vec a, vec b, f32x16 c)
-    { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
+    // D = X Y^T on 16 x 16 blocks with k = 32: lane l supplies row l % 16 of X and of Y
+    // at k = 8 (l / 16) .. + 7 and receives D[4 (l / 16) + r][l % 16], r = 0..3.
+    static __device__ __forceinline__ f32x4 run(vec x, vec y, f32x4 c)
+    { return __builtin_amdgcn_mfma_f32_16x16x32_f16(x, y, c, 0, 0, 0); }
 };
 template <> struct Mfma<bf16> {
     typedef bf16x8 vec;
@@ -157,8 +165,8 @@ template <> struct Mfma<bf16> {
         for (int i = 0; i < 8; i += 2) acc = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{p[i], p[i + 1]}, one, acc, false);
         return acc;
     }
-    static __device__ __forceinline__ f32x16 run(vec a, vec b, f32x16 c)
-    { return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0); }
+    static __device__ __forceinline__ f32x4 run(vec x, vec y, f32x4 c)
+    { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, y, c, 0, 0, 0); }
 };
 
 // K rows: 16-byte chunk c of key row r at physical chunk c ^ (r & 15).
@@ -179,15 +187,22 @@ __device__ __forceinline__ float max3(float a, float b, float c)
     return r;
 }
 
-// max / sum of this lane's value and lane l ^ 32's (identical in both lanes).
-__device__ __forceinline__ float pair_max(float x)
+// max / sum over lanes l, l ^ 16, l ^ 32 and l ^ 48, the four lanes that hold one
+// query's scores: v_permlane16_swap exchanges 16-lane rows 0 <-> 1 and 2 <-> 3,
+// v_permlane32_swap the two halves (VALU, no LDS round trip). All four lanes get the
+// same bits: the sum is (r0 + r1) + (r2 + r3) in every one of them.
+__device__ __forceinline__ float quad_max(float x)
 {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
-__device__ __forceinline__ float pair_sum(float x)
+__device__ __forceinline__ float quad_sum(float x)
 {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
@@ -222,6 +237,15 @@ __device__ __forceinline__ u32x4 ds_read_b128(uint32_t addr, int offset)
 __device__ __forceinline__ void lgkm_wait_for(u32x4& a, int after)
 {
     asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a) : "i"(after));
+}
+
+// a ^ imm in one VALU instruction that the compiler keeps where it is written
+// (hoisted out of the key loop it would hold one register per immediate).
+__device__ __forceinline__ uint32_t xor_imm(uint32_t a, int imm)
+{
+    uint32_t r;
+    asm volatile("v_xor_b32 %0, %1, %2" : "=v"(r) : "i"(imm), "v"(a));
+    return r;
 }
 
 // Workgroup barrier without the release fence of __syncthreads() (that fence would
@@ -284,20 +308,24 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) kernel(Params p)
     const int kvh = h / p.group;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int lrow = lane & 31, g = lane >> 5;
-    const int my_q = q_base + wave * 32 + lrow;
+    const int l16 = lane & 15, g = lane >> 4;
+    // Each lane holds two queries, one of each 16-query block qb of its wave's 32.
+    auto my_q = [&](int qb) { return q_base + wave * 32 + 16 * qb + l16; };
+    // Keys at or past key_lim are excluded: the valid-key bound, and the diagonal when causal.
+    auto key_lim = [&](int qb) { return p.causal ? min(p.kv_end, my_q(qb) + 1 + p.qk_off) : p.kv_end; };
     // A wave whose 32 queries all lie past sq (in a partial last query tile) only loads
     // its share of the K / V tiles and keeps the barriers.
     const bool active = q_base + wave * 32 < p.sq;
-    // Keys at or past key_lim are excluded: the valid-key bound, and the diagonal when causal.
-    const int key_lim = p.causal ? min(p.kv_end, my_q + 1 + p.qk_off) : p.kv_end;
 
+    // Q fragments (Y of S^T = K Q^T): query block qb, head-dim chunk dc: row my_q[qb],
+    // values 32 dc + 8 g .. + 7.
     const T* Q = static_cast<const T*>(p.q) + (size_t)h * p.q_hs;
-    vec8 qf[8];
-    {
-        const T* qrow = Q + (size_t)min(my_q, p.sq - 1) * p.q_rs;
+    vec8 qf[2][4];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) qf[s] = *reinterpret_cast<const vec8*>(qrow + (2 * s + g) * 8);
+    for (int qb = 0; qb < 2; ++qb) {
+        const T* qrow = Q + (size_t)min(my_q(qb), p.sq - 1) * p.q_rs;
+#pragma unroll
+        for (int dc = 0; dc < 4; ++dc) qf[qb][dc] = *reinterpret_cast<const vec8*>(qrow + 32 * dc + 8 * g);
     }
 
     // Key rows past kv_end lie past the buffer range and load as zeros.
@@ -316,8 +344,8 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) kernel(Params p)
         rm = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.mask + (size_t)h * p.mask_hs), (short)0,
                                                (uint32_t)(p.sk * 4), kRsrcFlags);
 
-    // Direct loads: wave w fills key rows [16w, 16w+16) of the K and V tiles with
-    // four 1-KiB instructions each (4 rows x 256 bytes); lane l lands at row l >> 4,
+    // Direct loads: wave w fills key rows [RPW w, RPW (w + 1)) of the K and V tiles with
+    // IPW 1-KiB instructions each (4 rows x 256 bytes); lane l lands at row l >> 4,
     // physical chunk l & 15. K (with its mask row) and V have rings of their own
     // because K runs one tile ahead of V.
     uint32_t k_src[4], v_src[4];  // IPW <= 4 used
@@ -349,70 +377,73 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) kernel(Params p)
                                                      it * v_tile, 0, 0);
     };
 
-    // K fragment (A of S^T = K Q^T): key 32t + lrow, logical chunk 2s + g. The
-    // swizzle depends on lrow only, so per-lane LDS addresses (of stage 0) are fixed
-    // and the key-half and stage offsets fold into the reads' immediate offsets.
+    // K fragment (X of S^T = K Q^T) of key block kb (16 keys) and head-dim chunk dc: key
+    // 16 kb + l16, logical chunk 4 dc + g. The swizzle depends on l16 only, so the
+    // per-lane LDS addresses (of stage 0) are fixed per dc and the key-block and stage
+    // offsets fold into the reads' immediate offsets.
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr_t)smem;
-    uint32_t k_addr[8];
+    uint32_t k_addr[4];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) k_addr[s] = lds0 + lrow * ROWB + (((2 * s + g) ^ kswz(lrow)) << 4);
-    // V^T fragment (A of O^T = V^T P^T) by transposing reads: 16-lane group G = lane >> 4
-    // (k-half G >> 1, d half 16 (G & 1)), lane j = lane & 15 points at key
-    // kb + 4 (G >> 1) + (j >> 2) with kb a multiple of 8, so its swizzle 2 (key & 7)
-    // is fixed per lane; values d0 + 16 (G & 1) + 4 (j & 3) .. + 3.
-    const int G = lane >> 4, j = lane & 15;
-    const int v_key_off = 4 * (G >> 1) + (j >> 2);
-    const int v_d = 16 * (G & 1) + 4 * (j & 3);
-    uint32_t v_addr[4];  // LDS addresses in V stage 0
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-        const int d = 32 * dt + v_d;
-        v_addr[dt] = lds0 + V_BASE + v_key_off * ROWB + (((d >> 3) ^ vswz(v_key_off)) << 4) + (d & 7) * 2;
-    }
+    for (int dc = 0; dc < 4; ++dc) k_addr[dc] = lds0 + l16 * ROWB + (((4 * dc + g) ^ kswz(l16)) << 4);
+    // V^T fragment (X of O^T = V^T P^T) of head-dim block db (16 values) and key chunk kc
+    // (32 keys) by two transposing reads: lane j = l16 of 16-lane group g points at key
+    // 32 kc + 4 g + j / 4 (lo) or that + 16 (hi), values 16 db + 4 (j % 4) .. + 3, and
+    // receives value 16 db + j of keys 32 kc + 4 g + 0..3 (lo) and 32 kc + 16 + 4 g + 0..3
+    // (hi): the MFMA's k positions 8 g .. 8 g + 7 in that order. The swizzle 2 (key & 7)
+    // is fixed per lane: db's 32-byte pair lands at pair db ^ (key & 7), so the address
+    // of db is v_base ^ 32 db (v_base's bits 5-7 hold the lane's pair, the rest of the
+    // address has none there); the XOR is issued with the read, which keeps one
+    // register per lane instead of eight.
+    const int v_key = 4 * g + (l16 >> 2);
+    const uint32_t v_base = lds0 + V_BASE + v_key * ROWB + ((v_key & 7) << 5) + (((l16 & 3) >> 1) << 4) +
+                            (((4 * (l16 & 3)) & 7) << 1);
 
-    f32x16 oacc[4];
+    // O^T accumulators: oacc[db][qb][r] = value 16 db + 4 g + r of query my_q[qb].
+    f32x4 oacc[8][2];
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int db = 0; db < 8; ++db)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[t][r] = 0.f;
-    float m_run = -INFINITY, l_run = 0.f;
+        for (int qb = 0; qb < 2; ++qb) oacc[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
     const float c = p.scale_log2;
 
-    // S^T of one key tile: sacc[t] holds keys 32t + 8(r/4) + 4g + r%4 for this lane's
-    // query. With a mask the accumulators start at mask / scale, so the scaled score
+    // S^T of one key tile: sacc[qb][kb][r] = score of key 16 kb + 4 g + r for query
+    // my_q[qb]. With a mask the accumulators start at mask / scale, so the scaled score
     // is s c + mask log2(e) without holding the mask in registers. A row mask comes
     // from LDS; a per-query mask row is read straight from memory (its keys past sk
     // read as zero through the buffer range, and fall past kv_end anyway).
     const float inv_scale = kLog2e / c;
-    const uint32_t dense_row = (uint32_t)(min(my_q, p.sq - 1) * p.sk) * 4u;
-    auto qk_init = [&](const uint8_t* ks, int kv0, f32x16 (&sacc)[2]) {
+    auto dense_row = [&](int qb) { return (uint32_t)(min(my_q(qb), p.sq - 1) * p.sk) * 4u; };
+    auto qk_init = [&](const uint8_t* ks, int kv0, f32x4 (&sacc)[2][4]) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            if constexpr (MASKROW) {
-                const float* ms = reinterpret_cast<const float*>(ks + KV_BYTES);
+        for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) sacc[t][r] = ms[32 * t + 8 * (r >> 2) + 4 * g + (r & 3)] * inv_scale;
-            } else if constexpr (DENSE) {
+            for (int r = 0; r < 4; ++r) {
+                const int kk = 16 * kb + 4 * g + r;
+                if constexpr (MASKROW) {
+                    const float mv = reinterpret_cast<const float*>(ks + KV_BYTES)[kk] * inv_scale;
+                    sacc[0][kb][r] = mv;
+                    sacc[1][kb][r] = mv;
+                } else if constexpr (DENSE) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int kk = 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
-                    const float mv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                                   rm, dense_row + (uint32_t)(kv0 + kk) * 4u, 0, 0));
-                    sacc[t][r] = mv * inv_scale;
+                    for (int qb = 0; qb < 2; ++qb) {
+                        const float mv = __builtin_bit_cast(
+                            float, __builtin_amdgcn_raw_buffer_load_b32(rm, dense_row(qb) + (uint32_t)(kv0 + kk) * 4u, 0, 0));
+                        sacc[qb][kb][r] = mv * inv_scale;
+                    }
+                } else {
+                    sacc[0][kb][r] = 0.f;
+                    sacc[1][kb][r] = 0.f;
                 }
-            } else {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) sacc[t][r] = 0.f;
             }
-        }
     };
-    // K fragment n of the tile in stage `slot` (a compile-time constant at every
-    // call): key half n % 2, head-dim slice n / 2, so consecutive MFMAs accumulate
-    // into different halves and never wait on each other.
-    auto kfrag = [&](int slot, int n) { return ds_read_b128(k_addr[n >> 1], slot * KSTAGE + (n & 1) * 32 * ROWB); };
+    // K fragment n of the tile in stage `slot` (a compile-time constant at every call):
+    // head-dim chunk n / 4, key block n % 4. Each feeds the MFMAs of both query blocks,
+    // and an accumulator is used again only four fragments (eight MFMAs) later.
+    auto kfrag = [&](int slot, int n) { return ds_read_b128(k_addr[n >> 2], slot * KSTAGE + (n & 3) * 16 * ROWB); };
     // Wait for K fragment n when fragments up to n + 2 have been issued.
     auto kwait = [&](u32x4& f, int n) { lgkm_wait_for(f, n + 2 < 16 ? 2 : 15 - n); };
-    auto qk = [&](int slot, int kv0, f32x16 (&sacc)[2]) {
+    auto qk = [&](int slot, int kv0, f32x4 (&sacc)[2][4]) {
         qk_init(kstage(slot), kv0, sacc);
         u32x4 kf[16];
         kf[0] = kfrag(slot, 0);
@@ -421,7 +452,9 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) kernel(Params p)
         for (int n = 0; n < 16; ++n) {
             if (n + 2 < 16) kf[n + 2] = kfrag(slot, n + 2);
             kwait(kf[n], n);
-            sacc[n & 1] = Mfma<T>::run(__builtin_bit_cast(vec8, kf[n]), qf[n >> 1], sacc[n & 1]);
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb)
+                sacc[qb][n & 3] = Mfma<T>::run(__builtin_bit_cast(vec8, kf[n]), qf[qb][n >> 2], sacc[qb][n & 3]);
         }
     };
     // Tiles whose scores are masked per lane here: past the valid keys, or (causal)
@@ -430,98 +463,119 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) kernel(Params p)
         const int kv0 = it * BKV;
         return MM != MASK_NONE || kv0 + BKV > p.kv_end || (p.causal && kv0 + BKV - 1 > q_base + wave * 32 + p.qk_off);
     };
-    // Tile maximum in the log2 domain (scores already scaled by c when `scaled`).
-    auto tile_max = [&](const f32x16 (&sacc)[2], bool scaled) {
-        float tmax = max3(sacc[0][0], sacc[0][1], sacc[0][2]);
+    // Tile maximum of query block qb in the log2 domain (scores already scaled by c
+    // when `scaled`).
+    auto tile_max = [&](const f32x4 (&sacc)[2][4], int qb, bool scaled) {
+        float tmax = max3(sacc[qb][0][0], sacc[qb][0][1], sacc[qb][0][2]);
 #pragma unroll
-        for (int i = 3; i < 31; i += 2) tmax = max3(tmax, sacc[i >> 4][i & 15], sacc[(i + 1) >> 4][(i + 1) & 15]);
-        tmax = pair_max(fmaxf(tmax, sacc[1][15]));
+        for (int i = 3; i < 15; i += 2)
+            tmax = max3(tmax, sacc[qb][i >> 2][i & 3], sacc[qb][(i + 1) >> 2][(i + 1) & 3]);
+        tmax = quad_max(fmaxf(tmax, sacc[qb][3][3]));
         return scaled ? tmax : tmax * c;
+    };
+    // O and l of query block qb rescaled to the offset m_new.
+    auto rescale = [&](int qb, float m_new, float l_base) {
+        const float alpha = m_run[qb] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[qb] - m_new);
+        l_run[qb] = l_base * alpha;
+#pragma unroll
+        for (int db = 0; db < 8; ++db)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) oacc[db][qb][r] *= alpha;
+        m_run[qb] = m_new;
     };
     // Mask, bound and tile maximum (log2 domain) of tile `it`; raises the running
     // offset when the maximum passes it by more than the slack. Returns the factor
     // the softmax applies to the scores: 1 when they were scaled here, else c.
-    auto prep = [&](f32x16 (&sacc)[2], int it) -> float {
+    auto prep = [&](f32x4 (&sacc)[2][4], int it) -> float {
         const int kv0 = it * BKV;
         const bool scaled = needs_prep(it);
         if (scaled) {
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+            for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int kk = 32 * t + 8 * (r >> 2) + 4 * g + (r & 3);
-                    sacc[t][r] = kv0 + kk < key_lim ? sacc[t][r] * c : -INFINITY;
-                }
+                for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int kk = 16 * kb + 4 * g + r;
+                        sacc[qb][kb][r] = kv0 + kk < key_lim(qb) ? sacc[qb][kb][r] * c : -INFINITY;
+                    }
         }
-        const float tmax = tile_max(sacc, scaled);
-        const bool raise = tmax > m_run + kRescaleSlack;
-        if (__any(raise)) {
-            const float m_new = raise ? tmax : m_run;
-            const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
-            l_run *= alpha;
+        float tmax[2];
+        bool raise[2];
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt)
+        for (int qb = 0; qb < 2; ++qb) {
+            tmax[qb] = tile_max(sacc, qb, scaled);
+            raise[qb] = tmax[qb] > m_run[qb] + kRescaleSlack;
+        }
+        if (__any(raise[0] || raise[1])) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
-            m_run = m_new;
+            for (int qb = 0; qb < 2; ++qb) rescale(qb, raise[qb] ? tmax[qb] : m_run[qb], l_run[qb]);
         }
         return scaled ? 1.f : c;
     };
-    // Probabilities of a prepared tile as MFMA B operands, and their row sum.
-    auto softmax = [&](const f32x16 (&sacc)[2], float cs, vec8 (&pf)[2][2]) {
-        const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    // Probabilities of a prepared tile as MFMA Y operands, and their row sums:
+    // pf[qb][kc] = keys 32 kc + 4 g + 0..3 and 32 kc + 16 + 4 g + 0..3 of query my_q[qb],
+    // the order of the V^T fragments' k positions.
+    auto softmax = [&](const f32x4 (&sacc)[2][4], float cs, vec8 (&pf)[2][2]) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int qb = 0; qb < 2; ++qb) {
+            const float m_use = m_run[qb] == -INFINITY ? 0.f : m_run[qb];
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                pf[t][r >> 3][r & 7] = T(__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[t][r], cs, -m_use)));
+            for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+                for (int r = 0; r < 4; ++r)
+                    pf[qb][kb >> 1][4 * (kb & 1) + r] = T(__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[qb][kb][r], cs, -m_use)));
+        }
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh) l_run = Mfma<T>::rowsum(pf[t][hh], l_run);
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+            for (int kc = 0; kc < 2; ++kc) l_run[qb] = Mfma<T>::rowsum(pf[qb][kc], l_run[qb]);
     };
     // The offset check of an unmasked tile whose maximum was not taken before its
     // softmax: its probabilities were computed with the running offset, adding to l_run
-    // from l_before. When they sum to less than kLazyCheck no score passed the offset by
-    // the slack, which is the common case after the first tiles, and they stand. Else
-    // the tile maximum decides as prep would have: if it raises the offset, O and
-    // l_before are rescaled and the probabilities recomputed, so the outcome is exactly
-    // prep's, in the same order of operations.
-    auto settle = [&](const f32x16 (&cur)[2], float l_before, vec8 (&pf)[2][2]) {
-        if (!__any(pair_sum(l_run - l_before) >= kLazyCheck)) return;
-        const float tmax = tile_max(cur, false);
-        const bool raise = tmax > m_run + kRescaleSlack;
-        if (!__any(raise)) return;
-        const float m_new = raise ? tmax : m_run;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        l_run = l_before * alpha;
+    // from l_before. When each query's probabilities sum to less than kLazyCheck no score
+    // passed the offset by the slack, which is the common case after the first tiles,
+    // and they stand. Else the tile maxima decide as prep would have: if one raises its
+    // query's offset, O and l_before are rescaled and the probabilities recomputed, so
+    // the outcome is exactly prep's, in the same order of operations.
+    auto settle = [&](const f32x4 (&cur)[2][4], const float (&l_before)[2], vec8 (&pf)[2][2]) {
+        const bool big0 = quad_sum(l_run[0] - l_before[0]) >= kLazyCheck;
+        const bool big1 = quad_sum(l_run[1] - l_before[1]) >= kLazyCheck;
+        if (!__any(big0 || big1)) return;
+        float tmax[2];
+        bool raise[2];
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
+        for (int qb = 0; qb < 2; ++qb) {
+            tmax[qb] = tile_max(cur, qb, false);
+            raise[qb] = tmax[qb] > m_run[qb] + kRescaleSlack;
+        }
+        if (!__any(raise[0] || raise[1])) return;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) oacc[dt][r] *= alpha;
-        m_run = m_new;
+        for (int qb = 0; qb < 2; ++qb) rescale(qb, raise[qb] ? tmax[qb] : m_run[qb], l_before[qb]);
         softmax(cur, c, pf);
     };
-    // O^T += V^T P^T; P's register r of (t, hh) is key 32t + 16hh + 8(r/4 & 1) + 4g + r%4.
-    // MFMA k (0..15) takes key block b = k / 4 (keys 16 b .. + 15, i.e. t = b / 2,
-    // hh = b % 2) and value group dt = k % 4; its V^T operand is two transposing
-    // reads, issued two MFMAs ahead of their use.
+    // O^T += V^T P^T. V^T fragment n = 8 kc + db (two transposing reads, issued two
+    // fragments ahead of their use) feeds the MFMAs of both query blocks; an accumulator
+    // is used again eight fragments (sixteen MFMAs) later.
     auto pv = [&](int slot, const vec8 (&pf)[2][2]) {
         u32x2 lo[16], hi[16];
-        auto issue = [&](int k) {
-            lo[k] = ds_read_tr(v_addr[k & 3], slot * KV_BYTES + 16 * (k >> 2) * ROWB);
-            hi[k] = ds_read_tr(v_addr[k & 3], slot * KV_BYTES + (16 * (k >> 2) + 8) * ROWB);
+        auto issue = [&](int n) {
+            const int kc = n >> 3, db = n & 7;
+            const uint32_t a = xor_imm(v_base, 32 * db);
+            lo[n] = ds_read_tr(a, slot * KV_BYTES + 32 * kc * ROWB);
+            hi[n] = ds_read_tr(a, slot * KV_BYTES + (32 * kc + 16) * ROWB);
         };
         issue(0);
         issue(1);
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            if (k + 2 < 16) issue(k + 2);
-            // Reads issued after MFMA k's two: those of MFMAs k+1 and k+2 (if any).
-            lgkm_wait_for(lo[k], hi[k], 2 * ((k + 2 < 16 ? k + 2 : 15) - k));
-            const u32x4 packed = {lo[k][0], lo[k][1], hi[k][0], hi[k][1]};
-            const int b = k >> 2;
-            oacc[k & 3] = Mfma<T>::run(__builtin_bit_cast(vec8, packed), pf[b >> 1][b & 1], oacc[k & 3]);
+        for (int n = 0; n < 16; ++n) {
+            if (n + 2 < 16) issue(n + 2);
+            // Reads issued after fragment n's two: those of fragments n+1 and n+2 (if any).
+            lgkm_wait_for(lo[n], hi[n], 2 * ((n + 2 < 16 ? n + 2 : 15) - n));
+            const u32x4 packed = {lo[n][0], lo[n][1], hi[n][0], hi[n][1]};
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb)
+                oacc[n & 7][qb] = Mfma<T>::run(__builtin_bit_cast(vec8, packed), pf[qb][n >> 3], oacc[n & 7][qb]);
         }
     };
 
@@ -533,26 +587,26 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) kernel(Params p)
     // softmax; the others take the running offset as it stands and are settled after
     // it, which almost never has to take their maximum.
     const int n = it1 - it0;
-    f32x16 sa[2], sb[2];
+    f32x4 sa[2][4], sb[2][4];
     vec8 pf[2][2];
     float cs_cur = c, cs_nxt = c;
     bool lazy_cur = false, lazy_nxt = false;  // the tile's maximum was not taken before its softmax
     // P = i % 2 as a compile-time constant: K_{i+1} sits in stage 1 - P, V_i in stage P.
-    auto step = [&](int i, f32x16 (&cur)[2], f32x16 (&nxt)[2], auto has_next, auto parity) {
+    auto step = [&](int i, f32x4 (&cur)[2][4], f32x4 (&nxt)[2][4], auto has_next, auto parity) {
         constexpr int P = decltype(parity)::value;
         __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // this wave's loads of K_{i+1}, V_i landed
         lds_barrier();                                         // ... every wave's; tile i-1 fully consumed
-        const float l_before = l_run;
+        const float l_before[2] = {l_run[0], l_run[1]};
         if constexpr (decltype(has_next)::value) {
             if (i + 2 < n) issue_k(it0 + i + 2, P);
             issue_v(it0 + i + 1, 1 - P);
             // S of the next tile on the matrix cores, interleaved by hand with the
             // softmax of this one: each group issues K fragment n + 2, waits for
-            // fragment n, issues MFMA n and turns two scores of this tile into
-            // probabilities (plus a row-sum term when a probability vector is
-            // complete); sched_barrier keeps the groups in this order.
+            // fragment n, issues its two MFMAs (one per query block) and turns one score
+            // of this tile into a probability after each (plus a row-sum term when a
+            // probability vector is complete); sched_barrier keeps the groups in order.
             qk_init(kstage(1 - P), (it0 + i + 1) * BKV, nxt);
-            const float m_use = m_run == -INFINITY ? 0.f : m_run;
+            const float m_use[2] = {m_run[0] == -INFINITY ? 0.f : m_run[0], m_run[1] == -INFINITY ? 0.f : m_run[1]};
             u32x4 kf[16];
             kf[0] = kfrag(1 - P, 0);
             kf[1] = kfrag(1 - P, 1);
@@ -560,13 +614,20 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) kernel(Params p)
             for (int k = 0; k < 16; ++k) {
                 if (k + 2 < 16) kf[k + 2] = kfrag(1 - P, k + 2);
                 kwait(kf[k], k);
-                nxt[k & 1] = Mfma<T>::run(__builtin_bit_cast(vec8, kf[k]), qf[k >> 1], nxt[k & 1]);
 #pragma unroll
-                for (int e = 2 * k; e < 2 * k + 2; ++e) {
-                    const int t = e >> 4, r = e & 15;
-                    pf[t][r >> 3][r & 7] = T(__builtin_amdgcn_exp2f(__builtin_fmaf(cur[t][r], cs_cur, -m_use)));
+                for (int qb = 0; qb < 2; ++qb) {
+                    nxt[qb][k & 3] = Mfma<T>::run(__builtin_bit_cast(vec8, kf[k]), qf[qb][k >> 2], nxt[qb][k & 3]);
+                    // Score e = 2 k + qb of this tile: query block e / 16, key block e / 4 % 4, r = e % 4.
+                    const int e = 2 * k + qb, eq = e >> 4, kb = (e >> 2) & 3, r = e & 3;
+                    pf[eq][kb >> 1][4 * (kb & 1) + r] =
+                        T(__builtin_amdgcn_exp2f(__builtin_fmaf(cur[eq][kb][r], cs_cur, -m_use[eq])));
+                    // The two MFMAs of a fragment stay apart: an MFMA issued while the
+                    // previous one still occupies the matrix unit holds up the wave's
+                    // independent VALU work behind it.
+                    if (qb == 0) __builtin_amdgcn_sched_barrier(0);
                 }
-                if ((k & 3) == 3) l_run = Mfma<T>::rowsum(pf[k >> 3][(k >> 2) & 1], l_run);
+                // Probability vector (k / 8, k / 4 % 2) complete after score 2 k + 1.
+                if ((k & 3) == 3) l_run[k >> 3] = Mfma<T>::rowsum(pf[k >> 3][(k >> 2) & 1], l_run[k >> 3]);
                 __builtin_amdgcn_sched_barrier(0);
             }
             if (lazy_cur) settle(cur, l_before, pf);
@@ -623,38 +684,38 @@ __global__ void __launch_bounds__(64 * NW, 8 / NW) kernel(Params p)
     }
 
     if (!active) return;  // n == 0
-    l_run = pair_sum(l_run);
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) l_run[qb] = quad_sum(l_run[qb]);
     if (part >= 0) {
         // Key-range part of the split tail tile: unnormalised O and (m, l) for combine_kernel.
         const size_t slot = (size_t)h * p.tail_parts + part;
-        const int ql = wave * 32 + lrow;
-        float* po = p.part_o + (slot * p.part_rows + ql) * D;
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
+        for (int qb = 0; qb < 2; ++qb) {
+            const int ql = wave * 32 + 16 * qb + l16;
+            float* po = p.part_o + (slot * p.part_rows + ql) * D;
 #pragma unroll
-            for (int rq = 0; rq < 4; ++rq) {
-                const f32x4 v = {oacc[dt][4 * rq], oacc[dt][4 * rq + 1], oacc[dt][4 * rq + 2], oacc[dt][4 * rq + 3]};
-                *reinterpret_cast<f32x4*>(po + 32 * dt + 8 * rq + 4 * g) = v;
+            for (int db = 0; db < 8; ++db) *reinterpret_cast<f32x4*>(po + 16 * db + 4 * g) = oacc[db][qb];
+            if (g == 0) {
+                p.part_ml[(slot * p.part_rows + ql) * 2] = m_run[qb];
+                p.part_ml[(slot * p.part_rows + ql) * 2 + 1] = l_run[qb];
             }
-        if (g == 0) {
-            p.part_ml[(slot * p.part_rows + ql) * 2] = m_run;
-            p.part_ml[(slot * p.part_rows + ql) * 2 + 1] = l_run;
         }
         return;
     }
-    if (my_q >= p.sq) return;
-    const float inv = 1.f / l_run;
-    T* orow = static_cast<T*>(p.o) + (size_t)h * p.o_hs + (size_t)my_q * p.o_rs;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int qb = 0; qb < 2; ++qb) {
+        if (my_q(qb) >= p.sq) continue;
+        const float inv = 1.f / l_run[qb];
+        T* orow = static_cast<T*>(p.o) + (size_t)h * p.o_hs + (size_t)my_q(qb) * p.o_rs;
 #pragma unroll
-        for (int rq = 0; rq < 4; ++rq) {
-            // Values 32 dt + 8 rq + 4 g .. + 3: offset 8 rq + 4 g in the dt-th group of 32.
+        for (int db = 0; db < 8; ++db) {
+            // Values 16 db + 4 g .. + 3: offset 16 (db % 2) + 4 g in the (db / 2)-th group of 32.
             union { u32x2 u; T e[4]; } pk;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) pk.e[e] = T(oacc[dt][4 * rq + e] * inv);
-            *reinterpret_cast<u32x2*>(orow + (size_t)dt * p.o_ds + 8 * rq + 4 * g) = pk.u;
+            for (int e = 0; e < 4; ++e) pk.e[e] = T(oacc[db][qb][e] * inv);
+            *reinterpret_cast<u32x2*>(orow + (size_t)(db >> 1) * p.o_ds + 16 * (db & 1) + 4 * g) = pk.u;
         }
+    }
 }
 
 }  // namespace sdl
