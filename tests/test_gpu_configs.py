@@ -13,6 +13,10 @@
   oracle at max|d| <= 1e-4 max|ref| (above and in test_gpu_block.py), which is
   how tools/validate_denoiser.py:53-55 grades a low-precision denoise against
   an FP32 run.
+* The deepest block of a full-depth DiT forward at both sizes, in its storage
+  precision, against the oracle on the activations the 35 blocks before it
+  produced on the device (the residual stream of a real 36-block stack, not
+  N(0, 1) inputs).
 """
 import time
 
@@ -23,6 +27,7 @@ import ernie_amd as E
 import kat
 import oracle as O
 from gpu_util import NAMES, dev, empty, host
+from test_gpu_facade import device_copy
 from test_oracle import small_block, small_heads
 
 pytestmark = pytest.mark.gpu
@@ -195,3 +200,57 @@ def test_full_depth_denoise_against_fp32_device(case):
     nrmse, rtol, atol = kat.DENOISER_GATES["fp16"]
     g = kat.gate(low, ref, atol, rtol, nrmse)
     assert g["passed"], g
+
+
+# (name, dtype, latent rows, latent columns, text slots, valid text, seed)
+DEEP_CASES = [
+    ("1024x1024_fp16", E.FP16, 64, 64, 64, 40, 3),
+    ("2048x1024_bf16", E.BF16, 64, 128, 2048, 300, 6),
+]
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("case", DEEP_CASES, ids=lambda c: c[0])
+def test_deepest_block_of_full_depth_dit_against_oracle(case):
+    import torch
+    _, dt, H, W, text_tokens, valid_text, seed = case
+    fac = E.Facade(0)
+    try:
+        ctx = fac.hip
+        for b in range(35):
+            ctx.block_init_random(b, DIM, FFN, dt, seed=seed * 1000 + b, std=0.02)
+        w35 = small_block(DIM, FFN, seed=seed, block=35)
+        ctx.block_upload(35, w35, DIM, FFN, dt)
+        ctx.heads_init_random(DIM, LATENT_CH, TEXT_DIM, dt, seed=seed * 1000 + 999, std=0.02)
+        latent = torch.empty((LATENT_CH, H, W), dtype=torch.float32, device="cuda")
+        ctx.fill_normal(latent, E.FP32, latent.numel(), seed=seed)
+        text = torch.empty((text_tokens, TEXT_DIM), dtype=torch.float32, device="cuda")
+        ctx.fill_normal(text, E.FP32, text.numel(), seed=seed + 1)
+        text[valid_text:] = 0.0  # pad_text
+        cos, sin, mask, valid = E.dit_constants(E.rope_frequencies(), W, H, valid_text, text_tokens)
+        feat = O.timestep_features(1000.0)
+        keep = {f"head-{i}" for i in range(2, 8)} | {"block-34", "block-35"}
+        seen = {}
+
+        def observer(stage, ptr, w, h, c):
+            if stage in keep:
+                seen[stage] = device_copy(ctx, ptr, w * h * c).reshape(-1, w)
+
+        pred = empty((LATENT_CH, H * W))
+        fac.run_dit(list(range(36)), latent, H, W, text, text_tokens, dev(feat), DIM, dev(cos), dev(sin), pred,
+                    mask=dev(mask), valid_prefix=valid, dtype=dt, observer=observer)
+        assert set(seen) == keep
+        mods = np.concatenate([seen[f"head-{i}"] for i in range(2, 8)])
+        x_in = seen["block-34"]
+        assert x_in.shape == (H * W + text_tokens, DIM) and np.isfinite(x_in).all()
+        t0 = time.perf_counter()
+        ocos, osin, omask = O.dit_constants(O.rope_frequencies(), W, H, valid_text, text_tokens)
+        ref = O.block_forward(w35, x_in, mods, ocos, osin, omask)
+        print(f"oracle {time.perf_counter() - t0:.1f} s, |x| max {np.abs(x_in).max():.3g}", flush=True)
+        g = kat.gate(seen["block-35"], ref, *kat.BLOCK_GATES[NAMES[dt]])
+        print(g, flush=True)
+        assert g["passed"], g
+    finally:
+        torch.cuda.synchronize()
+        fac.close()
+        torch.cuda.empty_cache()
