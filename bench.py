@@ -358,6 +358,9 @@ def main():
         "sdpa_gemm_tflops": (tot_flop / (tot_ms * 1e-3)) / 1e12 if tot_ms else None,
         "kernels": kernels,
         "step_seconds": [round(float(s), 5) for s in step_s],
+        # Per-step device time (events between consecutive Euler updates): median and minimum.
+        "ms_per_step_median": float(np.median(step_s)) * 1e3 if len(step_s) else None,
+        "ms_per_step_min": float(np.min(step_s)) * 1e3 if len(step_s) else None,
         "latent_finite": finite,
     }
     if args.mfma_ceiling == "on":
