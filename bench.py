@@ -137,11 +137,14 @@ def cpu_baseline(tokens):
               (FFN, DIM), (DIM, FFN))
     w = {n: O.normal(s, 0, offset=i << 40, mean=1.0 if n.startswith("norm") else 0.0, std=0.02)
          for i, (n, s) in enumerate(zip(names, shapes))}
-    grid = 64 if tokens >= 4160 else 32
-    text = tokens - grid * grid
-    cos, sin, mask = O.dit_constants(O.rope_frequencies(), grid, grid, min(40, text), text)
-    x = O.normal((tokens, DIM), 1)
-    mods = O.normal((6, DIM), 101, std=0.5)
+
+    def inputs(S):
+        grid = 64 if S >= 4160 else 32
+        text = S - grid * grid
+        cos, sin, mask = O.dit_constants(O.rope_frequencies(), grid, grid, min(40, text), text)
+        return O.normal((S, DIM), 1), O.normal((6, DIM), 101, std=0.5), cos, sin, mask
+
+    x, mods, cos, sin, mask = inputs(tokens)
     t0 = time.perf_counter()
     O.block_forward(w, x, mods, cos, sin, mask, precise=False, threads=threads)
     block_s = time.perf_counter() - t0
@@ -150,10 +153,16 @@ def cpu_baseline(tokens):
     t0 = time.perf_counter()
     O.block_forward(w, x, mods, cos, sin, mask, precise=False, threads=4)
     block4_s = time.perf_counter() - t0
+    # The one-block FP32 configuration at 1056 tokens (32 x 32 image + 32 text, all valid).
+    x, mods, cos, sin, mask = inputs(1056)
+    t0 = time.perf_counter()
+    O.block_forward(w, x, mods, cos, sin, mask, precise=False, threads=threads)
+    block1056_s = time.perf_counter() - t0
     return {"value": 1.0 / (36.0 * block_s), "unit": "steps/s", "cores": threads, "kind": "port",
             "sample": f"1 FP32 DiT block (dim 4096, FFN 12288, S={tokens}) of the C++ oracle, "
                       f"{block_s:.2f} s, extrapolated x36 blocks per step (heads and Euler excluded)",
-            "block_seconds": block_s, "block_seconds_4_threads": block4_s, "host": host_cpu()}
+            "block_seconds": block_s, "block_seconds_4_threads": block4_s,
+            "block_seconds_1056_tokens": block1056_s, "host": host_cpu()}
 
 
 def text_cpu_baseline(bucket, threads):
