@@ -215,7 +215,7 @@ def test_qk_norm_rope_against_oracle(ctx, dt):
 
 
 @pytest.mark.slow
-@pytest.mark.parametrize("dt", [E.FP32, E.FP16], ids=lambda d: NAMES[d])
+@pytest.mark.parametrize("dt", [E.FP32, E.FP16, E.BF16], ids=lambda d: NAMES[d])
 def test_sdpa_config1_every_row_against_oracle(ctx, dt):
     # The standalone SDPA workload at full size: 32 heads x 128, S = 4160 (4096 image
     # tokens + a 64-token text bucket whose last 24 keys are padding), Q/K/V ~ N(0,1), scale
@@ -239,9 +239,11 @@ def test_sdpa_config1_every_row_against_oracle(ctx, dt):
     else:
         g = kat.gate(got, ref, *kat.BLOCK_GATES[NAMES[dt]])
         assert g["passed"], g
-        # Per-row error bound as well, so that a few wrong rows cannot hide in the norm.
+        # Per-row error bound as well (the gate's atol + rtol max|ref|), so that a few wrong
+        # rows cannot hide in the norm.
+        atol, rtol, _ = kat.BLOCK_GATES[NAMES[dt]]
         row_err = np.abs(got - ref).max(axis=2)
-        assert float(row_err.max()) <= 0.02 + 0.02 * float(np.abs(ref).max()), float(row_err.max())
+        assert float(row_err.max()) <= atol + rtol * float(np.abs(ref).max()), float(row_err.max())
 
 
 def test_euler_and_finite_contracts(ctx):
